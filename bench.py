@@ -1,0 +1,327 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X layer kernels on the reference's layer-kernel workloads.
+
+Default workload: one Devstral-Small-2 decoder layer at a 64-token decode step (hidden 5120,
+intermediate 32768, 32 q / 8 kv heads of 128, KV pool 2048 pages x 256 slots). A step is that
+layer's five kernels - RMSNorm+residual, RoPE, paged KV store, RMSNorm+residual, SiluAndMul - over
+one 64-token batch. Inputs are resident in HBM before the timed region. The cold protocol (default)
+cycles through enough distinct layer buffer sets (each with its own KV cache) that a step never
+finds its data in the 256 MB Infinity Cache - what a 40-layer forward pass sees; steps are replayed
+from a captured HIP graph, as the reference's model runner replays its decode graphs.
+
+Printed on one JSON line: the metric (credited HBM bytes per step / time per step), microseconds
+per layer, each kernel's launch time and bandwidth (HIP events on the launch stream), the roofline
+of the dominant kernel, and the CPU baseline (the numpy oracle timed on a bounded sample of the
+same workload on the host).
+
+    python bench.py [--steps K] [--warmup W] [--workload NAME] [--protocol cold|hot] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+import __graft_entry__  # noqa: E402
+
+METRIC = "HBM GB/s & % of peak for layer kernels; µs/layer at 64-token decode"
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+COLD_BYTES = 768 << 20         # working set cycled by the cold protocol (3x the Infinity Cache)
+OPS = ("fused_add_rmsnorm", "rope", "append_paged_kv_cache", "silu_and_mul")
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=None, help="timed steps (default: workload-dependent)")
+    p.add_argument("--warmup", type=int, default=None)
+    p.add_argument("--workload", default="decode64_24b")
+    p.add_argument("--protocol", choices=("cold", "hot"), default="cold")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU time of the baseline sample")
+    p.add_argument("--fp8-norms", action="store_true", help="use the fp8-output norm (the reference's in-layer variant)")
+    return p.parse_args()
+
+
+class Timer:
+    """HIP events on the current stream around each launch of one kernel."""
+
+    def __init__(self):
+        self.pairs = []
+
+    def start(self):
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        return e
+
+    def stop(self, start):
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.pairs.append((start, e))
+
+    def mean_us(self) -> float:
+        torch.cuda.synchronize()
+        return 1000.0 * sum(a.elapsed_time(b) for a, b in self.pairs) / len(self.pairs)
+
+
+def footprint_bytes(shape) -> int:
+    """Bytes one layer set's kernels touch (inputs + outputs + destination cache rows)."""
+    n, h, i = shape.tokens, shape.hidden, shape.inter
+    return 2 * (4 * n * h + 3 * n * i + n * shape.qkv_width) + 4 * n * shape.kv_heads * shape.head_dim
+
+
+def time_ops_per_launch(mas, layer_sets, reps: int) -> dict[str, float]:
+    """Per-kernel launch time (µs), HIP events bracketing every launch, cycling the layer sets."""
+    timers = {op: Timer() for op in OPS}
+    norm_only = layer_sets[0].inputs.shape.norm_only
+    for r in range(reps):
+        b = layer_sets[r % len(layer_sets)]
+        li, s = b.inputs, b.inputs.shape
+        t = timers["fused_add_rmsnorm"].start()
+        mas.norm.fused_add_rmsnorm(li.hidden, li.residual, li.norm_weight, s.eps)
+        timers["fused_add_rmsnorm"].stop(t)
+        if norm_only:
+            continue
+        t = timers["rope"].start()
+        mas.rope.apply_rope_with_cos_sin_cache_inplace(li.positions, li.q, li.k, s.head_dim, li.table, True)
+        timers["rope"].stop(t)
+        t = timers["append_paged_kv_cache"].start()
+        mas.page.append_paged_kv_cache(b.k3, b.v3, li.batch_indices, li.positions, (li.k_cache, li.v_cache),
+                                       b.kv_indices, li.kv_indptr, None, "NHD")
+        timers["append_paged_kv_cache"].stop(t)
+        t = timers["silu_and_mul"].start()
+        mas.activation.silu_and_mul(li.gate_up, out=b.silu_out)
+        timers["silu_and_mul"].stop(t)
+    return {op: timers[op].mean_us() for op in OPS if timers[op].pairs}
+
+
+def capture(fn) -> torch.cuda.CUDAGraph:
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def cpu_baseline_layer(shape, seconds: float, fp8_norms: bool) -> dict:
+    """The oracle's five layer ops on a bounded sample of the workload, timed on the host."""
+    from oracle import ops as oops
+
+    mas = __graft_entry__.load_package()
+    wl = mas.workloads
+    tokens = shape.tokens
+    # A sample of whole tokens: the full batch when it fits the time budget, else a row slice.
+    if tokens * (shape.inter + shape.hidden) > 64 * (32768 + 5120):
+        tokens = 64
+    li = wl.make_layer_inputs(shape, "cpu", seed=1, with_cache=False)
+
+    def u16(t):
+        return t[:tokens].contiguous().view(torch.int16).numpy().view(np.uint16)
+
+    x, r, w = u16(li.hidden), u16(li.residual), li.norm_weight.view(torch.int16).numpy().view(np.uint16)
+    a, w2 = u16(li.attn_out), li.post_norm_weight.view(torch.int16).numpy().view(np.uint16)
+    gu = u16(li.gate_up)
+    qkv = u16(li.qkv)
+    hq, hk, d = shape.q_heads, shape.kv_heads, shape.head_dim
+    q = qkv[:, : hq * d].reshape(tokens, hq, d)
+    k = qkv[:, hq * d:(hq + hk) * d].reshape(tokens, hk, d)
+    v = qkv[:, (hq + hk) * d:].reshape(tokens, hk, d)
+    pos = li.positions[:tokens].numpy()
+    table = li.table.numpy()
+    slots = li.slot_mapping[:tokens].numpy()
+    # the destination pages only; untouched pages play no part in the store
+    pages_used = np.unique(slots // shape.page_size)
+    remap = {p: j for j, p in enumerate(pages_used)}
+    local_slots = np.array([remap[s // shape.page_size] * shape.page_size + s % shape.page_size for s in slots])
+    kc = np.zeros((len(pages_used), shape.page_size, hk, d), np.uint16)
+    vc = np.zeros_like(kc)
+
+    def layer():
+        nonlocal x, r, kc, vc
+        if fp8_norms:
+            _, r = oops.fused_add_rmsnorm_quant(x, r, w, 0.05, shape.eps)
+        else:
+            _, r = oops.fused_add_rmsnorm(x, r, w, shape.eps)
+        if shape.norm_only:
+            return
+        oops.rope(q, k, pos, table)
+        kc, vc = oops.store_kv_slots(kc, vc, k, v, local_slots)
+        if fp8_norms:
+            _, r = oops.fused_add_rmsnorm_quant(a, r, w2, 0.05, shape.eps)
+        else:
+            _, r = oops.fused_add_rmsnorm(a, r, w2, shape.eps)
+        oops.silu_and_mul(gu)
+
+    sample_shape = type(shape)(**{**shape.__dict__, "tokens": tokens})
+    per_layer = wl.layer_credited_bytes(sample_shape)
+    if fp8_norms:
+        per_layer -= 2 * tokens * shape.hidden
+    layer()                                  # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        layer()
+        reps += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": round(per_layer * reps / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{reps} single-threaded numpy passes of the step's ops on {tokens} of "
+                      f"{shape.tokens} tokens ({dt:.1f} s)"}
+
+
+def run_layer_workload(mas, args, shape, dev) -> dict:
+    wl, lp = mas.workloads, mas.layer_pass
+    n_sets = 1 if args.protocol == "hot" else max(2, math.ceil(COLD_BYTES / footprint_bytes(shape)))
+    table = mas.rope.cos_sin_cache(shape.max_position, shape.head_dim, shape.theta).to(dev)
+    sets = [lp.LayerBuffers(wl.make_layer_inputs(shape, dev, seed=i, fill_on_device=True, table=table),
+                            fp8_norms=args.fp8_norms) for i in range(n_sets)]
+    per_step = wl.layer_credited_bytes(shape)
+    if args.fp8_norms:
+        per_step -= 2 * shape.tokens * shape.hidden
+    steps = args.steps if args.steps is not None else max(n_sets, (2000 if shape.decode else 40))
+    warmup = args.warmup if args.warmup is not None else max(n_sets, steps // 10)
+
+    def run_range(lo, hi):
+        for i in range(lo, hi):
+            lp.run_layer(sets[i % n_sets])
+
+    full = capture(lambda: run_range(0, n_sets))
+    graphs = {}
+
+    def replay(k):
+        for _ in range(k // n_sets):
+            full.replay()
+        rem = k % n_sets
+        if rem:
+            if rem not in graphs:
+                graphs[rem] = capture(lambda: run_range(0, rem))
+            graphs[rem].replay()
+
+    replay(warmup)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    replay(steps)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+
+    # stream-launched steps (no graph), for comparison
+    stream_steps = min(steps, 10 * n_sets) if shape.decode else min(steps, 4 * n_sets)
+    torch.cuda.synchronize()
+    s0 = time.perf_counter()
+    run_range(0, stream_steps)
+    torch.cuda.synchronize()
+    stream_us = (time.perf_counter() - s0) / stream_steps * 1e6
+
+    reps = 40 * n_sets if shape.decode else 4 * n_sets
+    op_us = time_ops_per_launch(mas, sets, reps)
+    cb = wl.credited_bytes(shape)
+    ops = {op: {"us": round(us, 3), "GB/s": round(cb[op] / us / 1e3, 1),
+                "frac": round(cb[op] / us / 1e3 / PEAK_HBM_GBS, 4)} for op, us in op_us.items()}
+    ms_per_step = elapsed / steps * 1e3
+    dominant = "fused_add_rmsnorm" if shape.norm_only else "silu_and_mul"
+    return {"steps": steps, "warmup": warmup, "ms_per_step": ms_per_step, "per_step_bytes": per_step,
+            "value": per_step / (ms_per_step * 1e-3) / 1e9, "stream_us_per_step": stream_us, "ops": ops,
+            "sets": n_sets, "dominant": dominant, "dominant_bytes": cb[dominant], "dominant_us": op_us[dominant]}
+
+
+def run_pass_workload(mas, args, shape, dev) -> dict:
+    lp, wl = mas.layer_pass, mas.workloads
+    passes = [lp.DecodePass(shape, dev, seed=0, fp8_norms=args.fp8_norms)]
+    per_step = passes[0].credited_bytes()
+    if args.fp8_norms:
+        per_step -= 2 * shape.layers * shape.tokens * shape.hidden
+    steps = args.steps if args.steps is not None else 20
+    warmup = args.warmup if args.warmup is not None else 3
+    g = capture(passes[0].run)
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        g.replay()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    op_us = time_ops_per_launch(mas, passes[0].layers, 2 * shape.layers)
+    cb = wl.credited_bytes(shape)
+    ops = {op: {"us": round(us, 3), "GB/s": round(cb[op] / us / 1e3, 1),
+                "frac": round(cb[op] / us / 1e3 / PEAK_HBM_GBS, 4)} for op, us in op_us.items()}
+    ms_per_step = elapsed / steps * 1e3
+    return {"steps": steps, "warmup": warmup, "ms_per_step": ms_per_step, "per_step_bytes": per_step,
+            "value": per_step / (ms_per_step * 1e-3) / 1e9, "ops": ops, "sets": 1, "dominant": "silu_and_mul",
+            "dominant_bytes": cb["silu_and_mul"], "dominant_us": op_us["silu_and_mul"],
+            "us_per_layer": ms_per_step * 1e3 / shape.layers}
+
+
+def main() -> int:
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE {world}); the layer kernels are token-parallel and would shard without exchange",
+              file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    mas = __graft_entry__.load_package()
+    mas.load_library()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    shape = mas.workloads.SHAPES[args.workload]
+    if shape.layers > 1:
+        res = run_pass_workload(mas, args, shape, dev)
+    else:
+        res = run_layer_workload(mas, args, shape, dev)
+
+    dom_gbs = res["dominant_bytes"] / res["dominant_us"] / 1e3
+    line = {
+        "metric": METRIC,
+        "value": round(res["value"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": res["steps"],
+        "warmup": res["warmup"],
+        "ms_per_step": round(res["ms_per_step"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": shape.name, "tokens": shape.tokens, "hidden": shape.hidden,
+                   "intermediate": shape.inter, "q_heads": shape.q_heads, "kv_heads": shape.kv_heads,
+                   "head_dim": shape.head_dim, "kv_pages": shape.num_pages, "page_size": shape.page_size,
+                   "layers": shape.layers, "protocol": args.protocol, "layer_sets": res["sets"],
+                   "launch": "hip-graph", "norm_output": "fp8" if args.fp8_norms else "bf16"},
+        "us_per_layer": round(res.get("us_per_layer", res["ms_per_step"] * 1e3), 3),
+        "frac_of_peak": round(res["value"] / PEAK_HBM_GBS, 4),
+        "ops": res["ops"],
+        "roofline": {"bound": "hbm", "kernel": res["dominant"], "achieved": round(dom_gbs, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(dom_gbs / PEAK_HBM_GBS, 4),
+                     "traffic": None, "bytes_per_launch": res["dominant_bytes"],
+                     "avg_launch_us": round(res["dominant_us"], 3)},
+    }
+    if "stream_us_per_step" in res:
+        line["stream_us_per_step"] = round(res["stream_us_per_step"], 3)
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline_layer(shape, args.cpu_seconds, args.fp8_norms)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,156 @@
+/*
+ * mas_kernels.h - C ABI of the MI355X (gfx950) per-layer kernels of mini-agent-serve's
+ * Devstral/Mistral decoder: fused residual-add + RMSNorm (bf16 and fp8-e4m3fn outputs),
+ * SiluAndMul, NeoX / GPT-J rotary embedding from a cos/sin table, the paged KV-cache append
+ * (block-table and slot-mapping forms) and the token-embedding gather.
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers; tensors are bf16 unless stated (bf16 travels as raw 16-bit
+ *     words, fp8 as raw bytes). Strides are in ELEMENTS of the pointed-to type, and the last
+ *     (hidden / head_dim) dimension is always contiguous.
+ *   - Work is enqueued on `stream` and nothing else: no allocation, no host synchronisation,
+ *     no use of the null stream, so every call may be captured into a HIP graph.
+ *   - The return value is MAS_OK (0), a negative MAS_ERR_* argument error (nothing was
+ *     enqueued), or a positive hipError_t reported by the launch.
+ *   - Index inputs are range-checked on the device. A row whose index is out of range is left
+ *     unwritten (embedding: zero-filled) and, when `err` is non-NULL, the kernel ORs a
+ *     MAS_ERRBIT_* bit into *err. No kernel reads or writes outside the buffers described.
+ *
+ * Reference interfaces replaced (paths relative to the mini-agent-serve repository):
+ *   miniagentserve/models/devstral2/devstral2.py:18-23  flashinfer imports
+ *   miniagentserve/models/devstral2/devstral2.py:260,282 nn.Embedding
+ */
+#ifndef MAS_KERNELS_H
+#define MAS_KERNELS_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MAS_OK 0
+#define MAS_ERR_INVALID_VALUE (-1) /* null pointer, negative size, bad stride or eps       */
+#define MAS_ERR_UNSUPPORTED (-2)   /* a shape this library does not implement             */
+#define MAS_ERR_MISALIGNED (-3)    /* a pointer or stride breaks the kernel's alignment   */
+#define MAS_ERR_DEVICE (-4)        /* hipGetDevice / device-attribute query failed        */
+
+#define MAS_ERRBIT_TOKEN_ID 1u  /* embedding: id < 0 or id >= vocab                       */
+#define MAS_ERRBIT_POSITION 2u  /* rope: position < 0 or >= table rows; kv: position < 0  */
+#define MAS_ERRBIT_BATCH 4u     /* kv: batch index outside [0, batch)                     */
+#define MAS_ERRBIT_PAGE 8u      /* kv: page slot past kv_indices or page id out of range  */
+#define MAS_ERRBIT_SLOT 16u     /* kv slot form: slot >= num_pages * page_size            */
+
+/* Library version, (major << 16) | (minor << 8) | patch. */
+int mas_version(void);
+
+/* Human-readable text for a return code of this library. */
+const char* mas_status_string(int status);
+
+/*
+ * Fused residual add + RMSNorm, bf16 output written in place over `input`:
+ *   s = f32(input) + f32(residual);  residual <- bf16(s);
+ *   input <- bf16(s * rsqrt(mean(s*s) + eps) * f32(weight))
+ * input/residual: [rows, hidden]; weight: [hidden].
+ * Replaces flashinfer.norm.fused_add_rmsnorm(input, residual, weight, eps, enable_pdl)
+ * called at miniagentserve/models/devstral2/devstral2.py:305-307.
+ */
+int mas_fused_add_rmsnorm_bf16(void* input, int64_t input_stride, void* residual, int64_t residual_stride,
+                               const void* weight, int64_t rows, int64_t hidden, float eps,
+                               hipStream_t stream);
+
+/*
+ * Fused residual add + RMSNorm with a per-tensor fp8 (OCP e4m3fn) output; `input` is read only:
+ *   s as above;  residual <- bf16(s);
+ *   out <- e4m3fn(clamp(s * rsqrt(mean(s*s) + eps) * f32(weight) / scale, -448, 448))
+ * `scale` is read from the device word `scale_dev` when it is non-NULL, else `scale_host` is used.
+ * NaN stays NaN (code 0x7f with the input's sign). out: [rows, hidden] bytes.
+ * Replaces flashinfer.norm.fused_add_rmsnorm_quant(out, input, residual, weight, scale, eps,
+ * enable_pdl) called at miniagentserve/models/devstral2/devstral2.py:241-252.
+ */
+int mas_fused_add_rmsnorm_quant_fp8(void* out, int64_t out_stride, const void* input, int64_t input_stride,
+                                    void* residual, int64_t residual_stride, const void* weight,
+                                    const float* scale_dev, float scale_host, int64_t rows, int64_t hidden,
+                                    float eps, hipStream_t stream);
+
+/*
+ * SiluAndMul gating: out[r, i] = bf16(silu(f32(in[r, i])) * f32(in[r, inter + i])), i < inter
+ * (gate half first, up half second). in: [rows, 2*inter]; out: [rows, inter].
+ * Replaces flashinfer.activation.silu_and_mul(input, enable_pdl) called at
+ * miniagentserve/models/devstral2/devstral2.py:224.
+ */
+int mas_silu_and_mul_bf16(void* out, int64_t out_stride, const void* input, int64_t input_stride,
+                          int64_t rows, int64_t inter, hipStream_t stream);
+
+/*
+ * Rotary embedding in place from a cos/sin table, applied to q and k heads.
+ * q: rows x num_q_heads heads; head h of row t starts at q + t*q_stride + h*q_head_stride
+ * (k likewise). table: fp32 [table_rows, rotary_dim] with row stride `table_stride`; the first
+ * rotary_dim/2 columns are cos, the rest sin. The first `rotary_dim` elements of each head are
+ * rotated; the remaining head_dim - rotary_dim are untouched.
+ *   is_neox != 0: pairs (i, i + rotary_dim/2) use cos[i], sin[i]   (rotate-half)
+ *   is_neox == 0: pairs (2i, 2i + 1)          use cos[i], sin[i]   (interleaved)
+ *   x_a' = x_a*cos - x_b*sin;  x_b' = x_b*cos + x_a*sin   (fp32 math, one bf16 rounding)
+ * positions: `rows` indices, int32 when pos_is_int64 == 0, else int64.
+ * rotary_dim must be one of 32, 64, 128, 256, 512 and <= head_dim.
+ * Replaces flashinfer.rope.apply_rope_with_cos_sin_cache_inplace(positions, query, key,
+ * head_size, cos_sin_cache, is_neox) called at miniagentserve/models/devstral2/devstral2.py:163-166.
+ */
+int mas_rope_cos_sin_cache_bf16(void* q, int64_t q_stride, int64_t q_head_stride, int64_t num_q_heads,
+                                void* k, int64_t k_stride, int64_t k_head_stride, int64_t num_k_heads,
+                                const void* positions, int pos_is_int64, const float* table,
+                                int64_t table_stride, int64_t table_rows, int64_t rows, int64_t head_dim,
+                                int64_t rotary_dim, int is_neox, uint32_t* err, hipStream_t stream);
+
+/*
+ * Paged KV-cache append, block-table form. For token t:
+ *   b = batch_indices[t], p = positions[t],
+ *   page = kv_indices[kv_indptr[b] + p / page_size], entry = p % page_size,
+ *   k_cache[page, entry, h, :] = key[t, h, :]  and the same for value, for h < num_heads.
+ * Cache element (page, entry, h, d) is at cache + page*page_stride + entry*entry_stride +
+ * h*head_stride + d, which covers the NHD ([pages, page_size, heads, dim]) and HND
+ * ([pages, heads, page_size, dim]) layouts. key/value element (t, h, d) is at
+ * key + t*key_stride + h*key_head_stride + d. batch_indices, positions, kv_indices and kv_indptr
+ * are int32; `batch` = number of kv_indptr entries - 1, `num_indices` = kv_indices length.
+ * Duplicate destinations are allowed (one of the writers wins).
+ * Replaces flashinfer.page.append_paged_kv_cache(append_key, append_value, batch_indices,
+ * positions, paged_kv_cache, kv_indices, kv_indptr, kv_last_page_len, kv_layout) called at
+ * miniagentserve/models/devstral2/devstral2.py:170-173 (kv_last_page_len carries no information
+ * the store needs and is not an argument here).
+ */
+int mas_append_paged_kv_cache_bf16(void* k_cache, void* v_cache, int64_t page_stride, int64_t entry_stride,
+                                   int64_t head_stride, int64_t num_pages, int64_t page_size,
+                                   const void* key, int64_t key_stride, int64_t key_head_stride,
+                                   const void* value, int64_t value_stride, int64_t value_head_stride,
+                                   const int32_t* batch_indices, const int32_t* positions,
+                                   const int32_t* kv_indices, int64_t num_indices, const int32_t* kv_indptr,
+                                   int64_t batch, int64_t rows, int64_t num_heads, int64_t head_dim,
+                                   uint32_t* err, hipStream_t stream);
+
+/*
+ * Paged KV-cache store, slot-mapping form: slot = slot_mapping[t] (int64), page = slot / page_size,
+ * entry = slot % page_size, then as above. A negative slot marks a padding token and is skipped.
+ * Equivalent to the block-table form with slot = block_tables[b, p / page_size]*page_size +
+ * p % page_size (miniagentserve/models/devstral2/devstral2.py:170-173,289).
+ */
+int mas_store_kv_slots_bf16(void* k_cache, void* v_cache, int64_t page_stride, int64_t entry_stride,
+                            int64_t head_stride, int64_t num_pages, int64_t page_size, const void* key,
+                            int64_t key_stride, int64_t key_head_stride, const void* value,
+                            int64_t value_stride, int64_t value_head_stride, const int64_t* slot_mapping,
+                            int64_t rows, int64_t num_heads, int64_t head_dim, uint32_t* err,
+                            hipStream_t stream);
+
+/*
+ * Token-embedding gather: out[t, :] = weight[ids[t], :], a bit copy. ids: int64 [rows];
+ * weight: [vocab, hidden] with row stride weight_stride; out: [rows, hidden].
+ * Replaces nn.Embedding.forward at miniagentserve/models/devstral2/devstral2.py:260,282.
+ */
+int mas_embedding_bf16(void* out, int64_t out_stride, const void* weight, int64_t weight_stride, int64_t vocab,
+                       const int64_t* ids, int64_t rows, int64_t hidden, uint32_t* err, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MAS_KERNELS_H */

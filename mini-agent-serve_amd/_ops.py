@@ -1,0 +1,116 @@
+"""torch.library registrations of the ops under the ``mas`` namespace.
+
+The public wrappers call the kernels directly in eager mode (one ctypes call, no dispatcher hop)
+and route through these ops only while ``torch.compile`` traces, so a compiled model, like the
+reference's ``torch.compile(model, dynamic=True)`` at miniagentserve/engine/model_runner.py:98,
+keeps each kernel as one opaque node instead of breaking its graph at a ctypes call.
+"""
+from __future__ import annotations
+
+import torch
+from torch.library import custom_op
+
+from . import activation, embedding, norm, page, rope
+
+Tensor = torch.Tensor
+
+
+@custom_op("mas::fused_add_rmsnorm", mutates_args=("input", "residual"))
+def _fused_add_rmsnorm(input: Tensor, residual: Tensor, weight: Tensor, eps: float) -> None:
+    norm._fused_add_rmsnorm(input, residual, weight, eps)
+
+
+@_fused_add_rmsnorm.register_fake
+def _(input, residual, weight, eps):
+    return None
+
+
+@custom_op("mas::fused_add_rmsnorm_quant", mutates_args=("out", "residual"))
+def _fused_add_rmsnorm_quant(out: Tensor, input: Tensor, residual: Tensor, weight: Tensor, scale: Tensor,
+                             eps: float) -> None:
+    norm._fused_add_rmsnorm_quant(out, input, residual, weight, scale, eps)
+
+
+@_fused_add_rmsnorm_quant.register_fake
+def _(out, input, residual, weight, scale, eps):
+    return None
+
+
+@custom_op("mas::fused_add_rmsnorm_quant_hs", mutates_args=("out", "residual"))
+def _fused_add_rmsnorm_quant_hs(out: Tensor, input: Tensor, residual: Tensor, weight: Tensor, scale: float,
+                                eps: float) -> None:
+    norm._fused_add_rmsnorm_quant(out, input, residual, weight, scale, eps)
+
+
+@_fused_add_rmsnorm_quant_hs.register_fake
+def _(out, input, residual, weight, scale, eps):
+    return None
+
+
+@custom_op("mas::silu_and_mul", mutates_args=())
+def _silu_and_mul(input: Tensor) -> Tensor:
+    out = torch.empty(tuple(input.shape[:-1]) + (input.shape[-1] // 2,), dtype=input.dtype, device=input.device)
+    activation._silu_and_mul(input, out)
+    return out
+
+
+@_silu_and_mul.register_fake
+def _(input):
+    return input.new_empty(tuple(input.shape[:-1]) + (input.shape[-1] // 2,))
+
+
+@custom_op("mas::silu_and_mul_out", mutates_args=("out",))
+def _silu_and_mul_out(input: Tensor, out: Tensor) -> None:
+    activation._silu_and_mul(input, out)
+
+
+@_silu_and_mul_out.register_fake
+def _(input, out):
+    return None
+
+
+@custom_op("mas::apply_rope_with_cos_sin_cache_inplace", mutates_args=("query", "key"))
+def _apply_rope(positions: Tensor, query: Tensor, key: Tensor, head_size: int, cos_sin_cache: Tensor,
+                is_neox: bool) -> None:
+    rope._apply_rope(positions, query, key, head_size, cos_sin_cache, is_neox)
+
+
+@_apply_rope.register_fake
+def _(positions, query, key, head_size, cos_sin_cache, is_neox):
+    return None
+
+
+@custom_op("mas::append_paged_kv_cache", mutates_args=("k_cache", "v_cache"))
+def _append_paged_kv_cache(append_key: Tensor, append_value: Tensor, batch_indices: Tensor, positions: Tensor,
+                           k_cache: Tensor, v_cache: Tensor, kv_indices: Tensor, kv_indptr: Tensor,
+                           kv_layout: str) -> None:
+    page._append(append_key, append_value, batch_indices, positions, (k_cache, v_cache), kv_indices, kv_indptr,
+                 kv_layout, None)
+
+
+@_append_paged_kv_cache.register_fake
+def _(append_key, append_value, batch_indices, positions, k_cache, v_cache, kv_indices, kv_indptr, kv_layout):
+    return None
+
+
+@custom_op("mas::store_kv_slots", mutates_args=("k_cache", "v_cache"))
+def _store_kv_slots(key: Tensor, value: Tensor, k_cache: Tensor, v_cache: Tensor, slot_mapping: Tensor,
+                    kv_layout: str) -> None:
+    page._store_slots(key, value, k_cache, v_cache, slot_mapping, kv_layout, None)
+
+
+@_store_kv_slots.register_fake
+def _(key, value, k_cache, v_cache, slot_mapping, kv_layout):
+    return None
+
+
+@custom_op("mas::embedding", mutates_args=())
+def _embedding(input_ids: Tensor, weight: Tensor) -> Tensor:
+    out = torch.empty(tuple(input_ids.shape) + (weight.shape[1],), dtype=weight.dtype, device=weight.device)
+    embedding._embedding(input_ids, weight, out)
+    return out
+
+
+@_embedding.register_fake
+def _(input_ids, weight):
+    return weight.new_empty(tuple(input_ids.shape) + (weight.shape[1],))

@@ -1,0 +1,140 @@
+// device.h - gfx950 device helpers shared by the layer kernels: 128-bit vector memory access,
+// bf16 / fp8-e4m3fn conversions, DPP wavefront reductions and launch-time device queries.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mas_kernels.h"
+
+namespace mas {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+// ---- memory ------------------------------------------------------------------------------
+// Streaming accesses carry the non-temporal hint: every byte these kernels move is touched once.
+__device__ __forceinline__ u32x4 load_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ void store_stream(void* p, u32x4 v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
+__device__ __forceinline__ void store_stream(void* p, u32x2 v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x2*>(p));
+}
+// Keeps the compiler's scheduler from moving instructions across this point: placed after a
+// kernel's group of loads so that all of them issue before the first instruction that waits on one.
+__device__ __forceinline__ void load_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// Cached access, for data re-read by other waves (norm weights, cos/sin rows, index tables).
+__device__ __forceinline__ u32x4 load_cached(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ f32x4 load_cached_f4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+
+// ---- bf16 ----------------------------------------------------------------------------------
+// A bf16 value is the high half of an fp32, so widening is a shift.
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Two fp32 -> packed bf16 pair, round-to-nearest-even (one v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+// Unpack 8 bf16 (one 128-bit vector) into fp32.
+__device__ __forceinline__ void unpack8(u32x4 v, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = bf16_lo(v[i]);
+    f[2 * i + 1] = bf16_hi(v[i]);
+  }
+}
+__device__ __forceinline__ u32x4 pack8(const float* f) {
+  u32x4 v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = pack_bf16x2(f[2 * i], f[2 * i + 1]);
+  return v;
+}
+
+// ---- fp8 e4m3fn (OCP: bias 7, no infinities, max 448, NaN = S.1111.111) -------------------
+// Clamp to [-448, 448] then round to nearest even; NaN maps to 0x7f with the input's sign.
+// Written with integer arithmetic so the result does not depend on the hardware converter's
+// saturation mode.
+__device__ __forceinline__ uint32_t fp8e4m3_saturate_encode(float f) {
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7fu;
+  const float af = fminf(__uint_as_float(a), 448.0f);
+  a = __float_as_uint(af);
+  if (a >= 0x3c800000u) {  // |f| >= 2^-6: normal. Round the mantissa at bit 20, then rebias 127 -> 7.
+    const uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
+    return sign | ((r >> 20) - (120u << 3));
+  }
+  // Subnormal (or zero): the value is m * 2^-9 with m in [0, 8]; m = 8 encodes 2^-6 exactly.
+  return sign | static_cast<uint32_t>(__builtin_rintf(af * 512.0f));
+}
+
+// ---- wavefront / block reductions ----------------------------------------------------------
+template <int kCtrl>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xf, 0xf,
+                                                               false));
+}
+
+// Sum over the 64 lanes of a wavefront; every lane receives the total. Rows of 16 lanes reduce
+// through DPP (quad_perm xor1, xor2, row_half_mirror, row_mirror), then the four row sums are
+// read out and added in a fixed order.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_move<0xb1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_move<0x4e>(v);   // quad_perm [2,3,0,1]
+  v += dpp_move<0x141>(v);  // row_half_mirror
+  v += dpp_move<0x140>(v);  // row_mirror
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
+// Sum over the block; `slots` is an LDS array with one float per wavefront. The caller alternates
+// between two slot arrays on consecutive calls, so one barrier per call is enough.
+__device__ __forceinline__ float block_sum(float v, float* slots) {
+  v = wave_sum(v);
+  const int nwaves = blockDim.x / kWave;
+  if (nwaves == 1) return v;
+  if ((threadIdx.x & (kWave - 1)) == 0) slots[threadIdx.x / kWave] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int i = 0; i < nwaves; ++i) t += slots[i];
+  return t;
+}
+
+__device__ __forceinline__ void report(uint32_t* err, uint32_t bit) {
+  if (err != nullptr) __hip_atomic_fetch_or(err, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ int wave_id_uniform() {
+  return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+}
+
+// ---- host-side helpers ---------------------------------------------------------------------
+// Compute units of the current device (cached per device after the first query).
+int device_cu_count(int* cus);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int launch_status() {
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MAS_OK : static_cast<int>(e);
+}
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace mas

@@ -1,0 +1,111 @@
+// silu_and_mul.hip - SiluAndMul gating over the gate_up projection output.
+//
+// Semantics (miniagentserve/models/devstral2/devstral2.py:223-224, flashinfer.activation.silu_and_mul;
+// gate first, up second by the concat order at devstral2.py:364):
+//   g = f32(in[r, i]), u = f32(in[r, I + i]);  out[r, i] = bf16((g / (1 + exp(-g))) * u)
+//
+// Streaming kernel: each workgroup owns a tile of 256 * UNROLL 128-bit output vectors of one
+// row; each lane issues all of its gate and up loads before any arithmetic, so 2 * UNROLL
+// 16-byte loads per lane are in flight. 6 bytes move per output element (read 4, write 2).
+#include "device.h"
+
+namespace mas {
+namespace {
+
+constexpr int kBlock = 256;
+
+__device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + __expf(-g))) * u; }
+
+template <int UNROLL>
+__global__ __launch_bounds__(kBlock) void silu_and_mul_vec(void* __restrict__ out, int64_t out_stride,
+                                                           const void* __restrict__ in, int64_t in_stride,
+                                                           int64_t inter, int64_t tiles_per_row, int64_t ntiles) {
+  const int64_t nvec = inter >> 3;
+  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int64_t row = tile / tiles_per_row;
+    const int64_t v0 = (tile - row * tiles_per_row) * (kBlock * UNROLL) + threadIdx.x;
+    const uint16_t* g = static_cast<const uint16_t*>(in) + row * in_stride;
+    const uint16_t* u = g + inter;
+    uint16_t* o = static_cast<uint16_t*>(out) + row * out_stride;
+
+    // Loads are unconditional (indices past the row end are clamped to its last vector) so the
+    // compiler issues them back to back; only the stores are guarded.
+    u32x4 gv[UNROLL], uv[UNROLL];
+#pragma unroll
+    for (int j = 0; j < UNROLL; ++j) {
+      const int64_t v = v0 + j * kBlock;
+      const int64_t vl = v < nvec ? v : nvec - 1;
+      gv[j] = load_stream(g + 8 * vl);
+      uv[j] = load_stream(u + 8 * vl);
+    }
+    load_fence();
+#pragma unroll
+    for (int j = 0; j < UNROLL; ++j) {
+      const int64_t v = v0 + j * kBlock;
+      if (v < nvec) {
+        float gf[8], uf[8], y[8];
+        unpack8(gv[j], gf);
+        unpack8(uv[j], uf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = silu_mul(gf[e], uf[e]);
+        store_stream(o + 8 * v, pack8(y));
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void silu_and_mul_scalar(void* __restrict__ out, int64_t out_stride,
+                                                              const void* __restrict__ in, int64_t in_stride,
+                                                              int64_t rows, int64_t inter) {
+  const int64_t total = rows * inter;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * kBlock) {
+    const int64_t row = i / inter, col = i - row * inter;
+    const uint16_t* g = static_cast<const uint16_t*>(in) + row * in_stride;
+    const float y = silu_mul(bf16_lo(g[col]), bf16_lo(g[inter + col]));
+    static_cast<uint16_t*>(out)[row * out_stride + col] = static_cast<uint16_t>(pack_bf16x2(y, 0.f));
+  }
+}
+
+template <int UNROLL>
+int launch_vec(void* out, int64_t out_stride, const void* in, int64_t in_stride, int64_t rows, int64_t inter,
+               int cus, hipStream_t s) {
+  const int64_t tiles_per_row = cdiv(inter / 8, kBlock * UNROLL);
+  const int64_t ntiles = rows * tiles_per_row;
+  const int64_t grid = ntiles < INT32_MAX ? ntiles : INT32_MAX;
+  (void)cus;
+  hipLaunchKernelGGL((silu_and_mul_vec<UNROLL>), dim3(static_cast<uint32_t>(grid)), dim3(kBlock), 0, s, out,
+                     out_stride, in, in_stride, inter, tiles_per_row, ntiles);
+  return launch_status();
+}
+
+}  // namespace
+}  // namespace mas
+
+extern "C" int mas_silu_and_mul_bf16(void* out, int64_t out_stride, const void* input, int64_t input_stride,
+                                     int64_t rows, int64_t inter, hipStream_t stream) {
+  using namespace mas;
+  if (rows < 0 || inter < 0) return MAS_ERR_INVALID_VALUE;
+  if (rows == 0 || inter == 0) return MAS_OK;
+  if (out == nullptr || input == nullptr) return MAS_ERR_INVALID_VALUE;
+  if (rows > 1 && (out_stride < inter || input_stride < 2 * inter)) return MAS_ERR_INVALID_VALUE;
+  int cus = 0;
+  if (const int st = device_cu_count(&cus); st != MAS_OK) return st;
+  const bool vec_ok = inter % 8 == 0 && aligned16(out) && aligned16(input) && out_stride % 8 == 0 &&
+                      input_stride % 8 == 0;
+  if (!vec_ok) {
+    const int64_t blocks = cdiv(rows * inter, kBlock);
+    const int64_t grid = blocks < 8 * cus ? blocks : 8 * cus;
+    hipLaunchKernelGGL(silu_and_mul_scalar, dim3(static_cast<uint32_t>(grid)), dim3(kBlock), 0, stream, out,
+                       out_stride, input, input_stride, rows, inter);
+    return launch_status();
+  }
+  // Enough tiles to keep every CU busy with several workgroups: 4 vectors per lane; otherwise
+  // spread the work over more, smaller tiles.
+  const int64_t vectors = rows * (inter / 8);
+  if (vectors >= static_cast<int64_t>(kBlock) * 4 * 8 * cus)
+    return launch_vec<4>(out, out_stride, input, input_stride, rows, inter, cus, stream);
+  if (vectors >= static_cast<int64_t>(kBlock) * 2 * 4 * cus)
+    return launch_vec<2>(out, out_stride, input, input_stride, rows, inter, cus, stream);
+  return launch_vec<1>(out, out_stride, input, input_stride, rows, inter, cus, stream);
+}

@@ -1,0 +1,70 @@
+"""Token-embedding gather, the drop-in for ``nn.Embedding`` at
+miniagentserve/models/devstral2/devstral2.py:260,282.
+
+``out[t, :] = weight[input_ids[t], :]``, a bit copy. With tied embeddings the table is shared with
+lm_head (devstral2.py:317-318), so the op only reads it.
+"""
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from . import _lib
+from ._tensors import error_word, require_dtype, require_gpu, require_same_device
+
+__all__ = ["embedding", "Embedding"]
+
+
+def _embedding(input_ids: torch.Tensor, weight: torch.Tensor, out: torch.Tensor,
+               error_flags: torch.Tensor | None = None) -> None:
+    require_gpu(input_ids, "input_ids")
+    require_gpu(weight, "weight")
+    require_gpu(out, "out")
+    require_dtype(input_ids, "input_ids", torch.int64)
+    require_dtype(weight, "weight", torch.bfloat16)
+    require_dtype(out, "out", torch.bfloat16)
+    device = require_same_device(("input_ids", input_ids), ("weight", weight), ("out", out))
+    if weight.dim() != 2 or (weight.shape[1] > 1 and weight.stride(1) != 1):
+        raise ValueError(f"weight must be [vocab, hidden] with a contiguous last dimension, got {tuple(weight.shape)}")
+    vocab, hidden = weight.shape
+    if not input_ids.is_contiguous():
+        raise ValueError("input_ids must be contiguous")
+    rows = input_ids.numel()
+    if tuple(out.shape) != tuple(input_ids.shape) + (hidden,) or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous {tuple(input_ids.shape) + (hidden,)} tensor")
+    st = _lib.load().mas_embedding_bf16(out.data_ptr(), hidden, weight.data_ptr(), weight.stride(0), vocab,
+                                        input_ids.data_ptr(), rows, hidden, error_word(error_flags, device),
+                                        _lib.stream_handle(device))
+    _lib.check(st, "embedding")
+
+
+def embedding(input_ids: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = None, *,
+              error_flags: torch.Tensor | None = None) -> torch.Tensor:
+    """Rows of ``weight`` (bf16 ``[vocab, hidden]``) selected by int64 ``input_ids``.
+
+    An id outside ``[0, vocab)`` yields a zero row instead of reading out of bounds; with
+    ``error_flags`` (a 1-element int32 device tensor) the kernel also sets bit 1 in it.
+    """
+    if torch.compiler.is_compiling():
+        return torch.ops.mas.embedding(input_ids, weight)
+    if out is None:
+        out = torch.empty(tuple(input_ids.shape) + (weight.shape[1],), dtype=weight.dtype, device=weight.device)
+    _embedding(input_ids, weight, out, error_flags)
+    return out
+
+
+class Embedding(nn.Module):
+    """``nn.Embedding(num_embeddings, embedding_dim)`` whose forward is the HIP gather."""
+
+    def __init__(self, num_embeddings: int, embedding_dim: int, device=None, dtype=torch.bfloat16):
+        super().__init__()
+        self.num_embeddings = num_embeddings
+        self.embedding_dim = embedding_dim
+        self.weight = nn.Parameter(torch.empty(num_embeddings, embedding_dim, device=device, dtype=dtype),
+                                   requires_grad=False)
+
+    def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
+        return embedding(input_ids, self.weight)
+
+    def extra_repr(self) -> str:
+        return f"{self.num_embeddings}, {self.embedding_dim}"

@@ -1,0 +1,183 @@
+"""Seeded synthetic inputs for the five layer-kernel workloads (the shapes of mini-agent-serve's
+Devstral-Small-2 24B and Devstral-2 123B decoders), and the credited-byte model used to report
+HBM bandwidth.
+
+Tensors are drawn as N(0, 1) in fp32 and cast to bf16; norm weights are 1 + 0.1 N(0, 1). q, k and v
+are column views of one fused qkv buffer ``[N, (Hq + 2 Hk) D]``, exactly as the reference splits its
+qkv GEMM output (miniagentserve/models/devstral2/devstral2.py:158-161). Index tensors use the
+reference's dtypes: positions / batch indices / page tables int32, token ids int64
+(miniagentserve/engine/model_runner.py:43-47).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+from .rope import cos_sin_cache
+
+__all__ = ["Shape", "SHAPES", "LayerInputs", "make_layer_inputs", "credited_bytes", "layer_credited_bytes"]
+
+
+@dataclass(frozen=True)
+class Shape:
+    name: str
+    tokens: int
+    hidden: int
+    inter: int
+    q_heads: int
+    kv_heads: int
+    head_dim: int
+    num_pages: int
+    page_size: int
+    seqs: int                   # sequences in the batch (decode: one token each)
+    decode: bool                # decode: random positions; prefill: contiguous 0..len-1 per sequence
+    max_position: int = 32768
+    theta: float = 1e6
+    eps: float = 1e-5
+    layers: int = 1
+    vocab: int = 131072
+    norm_only: bool = False     # the step is one RMSNorm + residual (the single-op CPU case)
+
+    @property
+    def qkv_width(self) -> int:
+        return (self.q_heads + 2 * self.kv_heads) * self.head_dim
+
+
+SHAPES: dict[str, Shape] = {s.name: s for s in [
+    # the CPU-runnable single-op case: RMSNorm + residual on [256, 5120]
+    Shape("rmsnorm_256x5120", 256, 5120, 32768, 32, 8, 128, 1, 256, 256, True, norm_only=True),
+    # Devstral-Small-2 decode step, one layer, 64 tokens; 2048 pages x 256 slots
+    Shape("decode64_24b", 64, 5120, 32768, 32, 8, 128, 2048, 256, 64, True),
+    # Devstral-Small-2 chunked prefill, one layer, 4 x 2048 tokens; 4096-page pool
+    Shape("prefill8192_24b", 8192, 5120, 32768, 32, 8, 128, 4096, 256, 4, False),
+    # Devstral-2 123B prefill, one layer, 4 x 4096 tokens; 8192-page pool
+    Shape("prefill16384_123b", 16384, 12288, 28672, 96, 8, 128, 8192, 256, 4, False),
+    # 40-layer decode pass over 256 sequences (GEMM and attention outputs replaced by N(0,1));
+    # 512 pages x 256 slots per layer, each sequence's current page distinct
+    Shape("decode_pass_256x40", 256, 5120, 32768, 32, 8, 128, 512, 256, 256, True, layers=40),
+]}
+
+
+@dataclass
+class LayerInputs:
+    shape: Shape
+    hidden: torch.Tensor        # [N, H] bf16, the previous sublayer's output entering the first norm
+    residual: torch.Tensor      # [N, H] bf16
+    norm_weight: torch.Tensor   # [H] bf16, input_layernorm
+    attn_out: torch.Tensor      # [N, H] bf16, stand-in for the o_proj output entering the second norm
+    post_norm_weight: torch.Tensor  # [H] bf16, post_attention_layernorm
+    gate_up: torch.Tensor       # [N, 2I] bf16
+    qkv: torch.Tensor           # [N, (Hq + 2Hk) D] bf16
+    positions: torch.Tensor     # [N] int32
+    batch_indices: torch.Tensor  # [N] int32
+    block_tables: torch.Tensor  # [batch, width] int32
+    kv_indptr: torch.Tensor     # [batch + 1] int32
+    slot_mapping: torch.Tensor  # [N] int64, the same destinations as the block-table form
+    table: torch.Tensor         # [max_position, D] fp32 cos/sin
+    k_cache: torch.Tensor | None = None
+    v_cache: torch.Tensor | None = None
+    extra: dict = field(default_factory=dict)
+
+    @property
+    def q(self) -> torch.Tensor:
+        s = self.shape
+        return self.qkv[:, : s.q_heads * s.head_dim]
+
+    @property
+    def k(self) -> torch.Tensor:
+        s = self.shape
+        return self.qkv[:, s.q_heads * s.head_dim: (s.q_heads + s.kv_heads) * s.head_dim]
+
+    @property
+    def v(self) -> torch.Tensor:
+        s = self.shape
+        return self.qkv[:, (s.q_heads + s.kv_heads) * s.head_dim:]
+
+
+def _indices(shape: Shape, gen: torch.Generator):
+    """Positions, batch indices, block tables, indptr and slots on the CPU."""
+    n, ps = shape.tokens, shape.page_size
+    if shape.decode:
+        # one token per sequence at a random position; every sequence's current page is distinct
+        positions = torch.randint(0, shape.max_position, (n,), generator=gen, dtype=torch.int64)
+        width = -(-shape.max_position // ps)
+        pages = torch.randperm(shape.num_pages, generator=gen)[:n]
+        tables = torch.randint(0, shape.num_pages, (n, width), generator=gen, dtype=torch.int64)
+        tables[torch.arange(n), positions // ps] = pages
+        batch = torch.arange(n)
+    else:
+        per_seq = n // shape.seqs
+        width = -(-per_seq // ps)
+        positions = torch.arange(per_seq).repeat(shape.seqs)
+        batch = torch.arange(shape.seqs).repeat_interleave(per_seq)
+        tables = torch.randperm(shape.num_pages, generator=gen)[: shape.seqs * width].reshape(shape.seqs, width)
+    slots = tables[batch, positions // ps] * ps + positions % ps
+    indptr = torch.arange(tables.shape[0] + 1) * tables.shape[1]
+    return (positions.to(torch.int32), batch.to(torch.int32), tables.to(torch.int32), indptr.to(torch.int32),
+            slots.to(torch.int64))
+
+
+def make_layer_inputs(shape: Shape | str, device: torch.device | str = "cpu", seed: int = 0,
+                      with_cache: bool = True, fill_on_device: bool = False,
+                      table: torch.Tensor | None = None) -> LayerInputs:
+    """One layer's inputs. ``fill_on_device`` draws the big tensors with the device's generator
+    (fast for the prefill shapes); otherwise everything is drawn on the CPU and copied, so the
+    oracle can see the same values."""
+    if isinstance(shape, str):
+        shape = SHAPES[shape]
+    device = torch.device(device)
+    cpu_gen = torch.Generator().manual_seed(seed)
+    dev_gen = torch.Generator(device=device).manual_seed(seed) if fill_on_device else None
+    n = shape.tokens
+
+    def normal(*size, scale=1.0, shift=0.0):
+        if fill_on_device:
+            t = torch.randn(*size, generator=dev_gen, device=device)
+        else:
+            t = torch.randn(*size, generator=cpu_gen).to(device)
+        return (shift + scale * t).to(torch.bfloat16) if (scale != 1.0 or shift != 0.0) else t.to(torch.bfloat16)
+
+    hidden = normal(n, shape.hidden)
+    residual = normal(n, shape.hidden)
+    weight = normal(shape.hidden, scale=0.1, shift=1.0)
+    attn_out = normal(n, shape.hidden)
+    post_weight = normal(shape.hidden, scale=0.1, shift=1.0)
+    gate_up = normal(n, 2 * shape.inter)
+    qkv = normal(n, shape.qkv_width)
+    positions, batch, tables, indptr, slots = _indices(shape, cpu_gen)
+    if table is None:
+        table = cos_sin_cache(shape.max_position, shape.head_dim, shape.theta)
+    inputs = LayerInputs(shape, hidden, residual, weight, attn_out, post_weight, gate_up, qkv, positions.to(device),
+                         batch.to(device), tables.to(device), indptr.to(device), slots.to(device), table.to(device))
+    if with_cache:
+        cache_shape = (shape.num_pages, shape.page_size, shape.kv_heads, shape.head_dim)
+        inputs.k_cache = torch.zeros(cache_shape, dtype=torch.bfloat16, device=device)
+        inputs.v_cache = torch.zeros(cache_shape, dtype=torch.bfloat16, device=device)
+    return inputs
+
+
+def layer_credited_bytes(shape: Shape) -> int:
+    """One decoder layer's five kernels: two norms (bf16 outputs), SiluAndMul, RoPE, KV store
+    (one norm for a norm-only shape)."""
+    b = credited_bytes(shape)
+    if shape.norm_only:
+        return b["fused_add_rmsnorm"]
+    return 2 * b["fused_add_rmsnorm"] + b["silu_and_mul"] + b["rope"] + b["append_paged_kv_cache"]
+
+
+def credited_bytes(shape: Shape) -> dict[str, int]:
+    """Algorithmic HBM bytes per launch: each mandatory input element read once, each output
+    element written once, index arrays included, the norm weight once, the cos/sin table not
+    credited (it could be computed in the kernel)."""
+    n, h, i = shape.tokens, shape.hidden, shape.inter
+    heads = shape.q_heads + shape.kv_heads
+    d = shape.head_dim
+    return {
+        "fused_add_rmsnorm": 8 * n * h + 2 * h,
+        "fused_add_rmsnorm_quant": 7 * n * h + 2 * h,
+        "silu_and_mul": 6 * n * i,
+        "rope": 4 * n * heads * d + 4 * n,
+        "append_paged_kv_cache": 8 * n * shape.kv_heads * d + 8 * n,
+        "embedding": 4 * n * h + 8 * n,
+    }

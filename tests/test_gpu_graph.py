@@ -1,0 +1,84 @@
+"""The ops inside HIP graphs and torch.compile, the two ways the reference's model runner executes
+its forward (miniagentserve/engine/model_runner.py:98,101-119)."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _layer_pass(mas, li, out_silu):
+    """The reference's per-layer order for the five kernels: norm, rope, kv store, norm, silu."""
+    s = li.shape
+    mas.fused_add_rmsnorm(li.hidden, li.residual, li.norm_weight, s.eps)
+    mas.apply_rope_with_cos_sin_cache_inplace(li.positions, li.q, li.k, s.head_dim, li.table, True)
+    k = li.k.view(s.tokens, s.kv_heads, s.head_dim)
+    v = li.v.view(s.tokens, s.kv_heads, s.head_dim)
+    mas.append_paged_kv_cache(k, v, li.batch_indices, li.positions, (li.k_cache, li.v_cache),
+                              li.block_tables.flatten(), li.kv_indptr, None, "NHD")
+    mas.fused_add_rmsnorm(li.hidden, li.residual, li.norm_weight, s.eps)
+    mas.silu_and_mul(li.gate_up, out=out_silu)
+
+
+def _snapshot(li, out):
+    return [t.clone() for t in (li.hidden, li.residual, li.qkv, li.k_cache, li.v_cache, out)]
+
+
+def test_graph_replays_match_eager(mas, dev):
+    wl = mas.workloads
+    shape = wl.SHAPES["decode64_24b"]
+    base = wl.make_layer_inputs(shape, dev, seed=3)
+    originals = _snapshot(base, torch.empty(0))[:3]
+
+    def reset(li):
+        li.hidden.copy_(originals[0])
+        li.residual.copy_(originals[1])
+        li.qkv.copy_(originals[2])
+        li.k_cache.zero_()
+        li.v_cache.zero_()
+
+    out = torch.empty(shape.tokens, shape.inter, dtype=torch.bfloat16, device=dev)
+    _layer_pass(mas, base, out)
+    torch.cuda.synchronize()
+    want = _snapshot(base, out)
+
+    reset(base)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        _layer_pass(mas, base, out)            # warm-up on a side stream, as the runner does
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    reset(base)
+    with torch.cuda.graph(graph):
+        _layer_pass(mas, base, out)
+    for _ in range(3):
+        reset(base)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = _snapshot(base, out)
+        for a, b in zip(got, want):
+            assert torch.equal(a, b)
+
+
+def test_torch_compile_matches_eager(mas, dev):
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(37, 1024, generator=g, device=dev).bfloat16()
+    r = torch.randn(37, 1024, generator=g, device=dev).bfloat16()
+    w = (1 + 0.1 * torch.randn(1024, generator=g, device=dev)).bfloat16()
+    gu = torch.randn(37, 2 * 512, generator=g, device=dev).bfloat16()
+    scale = torch.tensor(0.05, device=dev)
+
+    def f(x, r, gu):
+        mas.fused_add_rmsnorm(x, r, w, 1e-5)
+        out8 = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=x.device)
+        mas.fused_add_rmsnorm_quant(out8, x, r, w, scale, 1e-5)
+        return x + 0, r + 0, out8.view(torch.uint8) + 0, mas.silu_and_mul(gu) * 2
+
+    want = f(x.clone(), r.clone(), gu)
+    compiled = torch.compile(f, dynamic=True, fullgraph=True)
+    got = compiled(x.clone(), r.clone(), gu)
+    for a, b in zip(got, want):
+        assert torch.equal(a, b)
