@@ -10,7 +10,8 @@ finds its data in the 256 MB Infinity Cache - what a 40-layer forward pass sees;
 from a captured HIP graph, as the reference's model runner replays its decode graphs.
 
 Printed on one JSON line: the metric (credited HBM bytes per step / time per step), microseconds
-per layer, each kernel's launch time and bandwidth (HIP events on the launch stream), the roofline
+per layer, each kernel's average launch duration and bandwidth (HIP events around a graph of
+back-to-back launches of that kernel, on the stream it runs on), the roofline
 of the dominant kernel, and the CPU baseline (the numpy oracle timed on a bounded sample of the
 same workload on the host).
 
@@ -53,56 +54,66 @@ def parse_args():
     return p.parse_args()
 
 
-class Timer:
-    """HIP events on the current stream around each launch of one kernel."""
-
-    def __init__(self):
-        self.pairs = []
-
-    def start(self):
-        e = torch.cuda.Event(enable_timing=True)
-        e.record()
-        return e
-
-    def stop(self, start):
-        e = torch.cuda.Event(enable_timing=True)
-        e.record()
-        self.pairs.append((start, e))
-
-    def mean_us(self) -> float:
-        torch.cuda.synchronize()
-        return 1000.0 * sum(a.elapsed_time(b) for a, b in self.pairs) / len(self.pairs)
-
-
 def footprint_bytes(shape) -> int:
     """Bytes one layer set's kernels touch (inputs + outputs + destination cache rows)."""
     n, h, i = shape.tokens, shape.hidden, shape.inter
     return 2 * (4 * n * h + 3 * n * i + n * shape.qkv_width) + 4 * n * shape.kv_heads * shape.head_dim
 
 
-def time_ops_per_launch(mas, layer_sets, reps: int) -> dict[str, float]:
-    """Per-kernel launch time (µs), HIP events bracketing every launch, cycling the layer sets."""
-    timers = {op: Timer() for op in OPS}
-    norm_only = layer_sets[0].inputs.shape.norm_only
-    for r in range(reps):
-        b = layer_sets[r % len(layer_sets)]
-        li, s = b.inputs, b.inputs.shape
-        t = timers["fused_add_rmsnorm"].start()
-        mas.norm.fused_add_rmsnorm(li.hidden, li.residual, li.norm_weight, s.eps)
-        timers["fused_add_rmsnorm"].stop(t)
-        if norm_only:
-            continue
-        t = timers["rope"].start()
-        mas.rope.apply_rope_with_cos_sin_cache_inplace(li.positions, li.q, li.k, s.head_dim, li.table, True)
-        timers["rope"].stop(t)
-        t = timers["append_paged_kv_cache"].start()
-        mas.page.append_paged_kv_cache(b.k3, b.v3, li.batch_indices, li.positions, (li.k_cache, li.v_cache),
-                                       b.kv_indices, li.kv_indptr, None, "NHD")
-        timers["append_paged_kv_cache"].stop(t)
-        t = timers["silu_and_mul"].start()
-        mas.activation.silu_and_mul(li.gate_up, out=b.silu_out)
-        timers["silu_and_mul"].stop(t)
-    return {op: timers[op].mean_us() for op in OPS if timers[op].pairs}
+def op_launcher(mas, b, op):
+    """A closure launching one kernel of the layer on the buffers of ``b``."""
+    li, s = b.inputs, b.inputs.shape
+    if op == "fused_add_rmsnorm":
+        return lambda: mas.norm.fused_add_rmsnorm(li.hidden, li.residual, li.norm_weight, s.eps)
+    if op == "rope":
+        return lambda: mas.rope.apply_rope_with_cos_sin_cache_inplace(li.positions, li.q, li.k, s.head_dim, li.table,
+                                                                      True)
+    if op == "append_paged_kv_cache":
+        return lambda: mas.page.append_paged_kv_cache(b.k3, b.v3, li.batch_indices, li.positions,
+                                                      (li.k_cache, li.v_cache), b.kv_indices, li.kv_indptr, None,
+                                                      "NHD")
+    if op == "silu_and_mul":
+        return lambda: mas.activation.silu_and_mul(li.gate_up, out=b.silu_out)
+    raise ValueError(op)
+
+
+def time_ops(mas, layer_sets, launches: int, ops=OPS) -> dict[str, float]:
+    """Average launch duration (µs) of each kernel: a HIP graph of ``launches`` back-to-back launches
+    of that kernel alone, cycling the layer sets, bracketed by two HIP events on the stream the
+    graph replays on."""
+    out = {}
+    for op in ops:
+        fns = [op_launcher(mas, layer_sets[i % len(layer_sets)], op) for i in range(launches)]
+
+        def body():
+            for f in fns:
+                f()
+
+        g = capture(body)
+        g.replay()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        g.replay()
+        stop.record()
+        torch.cuda.synchronize()
+        out[op] = 1000.0 * start.elapsed_time(stop) / launches
+        del g
+    return out
+
+
+def copy_ceiling_gbs(dev, nbytes: int = 1 << 30) -> float:
+    """Device-to-device copy rate (read + write bytes per second), a practical streaming ceiling."""
+    a = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(10):
+        b.copy_(a)
+    stop.record()
+    torch.cuda.synchronize()
+    return 2 * nbytes * 10 / (start.elapsed_time(stop) * 1e-3) / 1e9
 
 
 def capture(fn) -> torch.cuda.CUDAGraph:
@@ -193,20 +204,23 @@ def run_layer_workload(mas, args, shape, dev) -> dict:
     per_step = wl.layer_credited_bytes(shape)
     if args.fp8_norms:
         per_step -= 2 * shape.tokens * shape.hidden
-    steps = args.steps if args.steps is not None else max(n_sets, (2000 if shape.decode else 40))
+    steps = args.steps if args.steps is not None else (2000 if shape.decode else 40)
     warmup = args.warmup if args.warmup is not None else max(n_sets, steps // 10)
 
     def run_range(lo, hi):
         for i in range(lo, hi):
             lp.run_layer(sets[i % n_sets])
 
-    full = capture(lambda: run_range(0, n_sets))
+    # one replay runs a whole number of passes over the layer sets and at least 50 steps, so the
+    # graph launch itself is amortised
+    per_graph = n_sets * max(1, math.ceil(50 / n_sets))
+    full = capture(lambda: run_range(0, per_graph))
     graphs = {}
 
     def replay(k):
-        for _ in range(k // n_sets):
+        for _ in range(k // per_graph):
             full.replay()
-        rem = k % n_sets
+        rem = k % per_graph
         if rem:
             if rem not in graphs:
                 graphs[rem] = capture(lambda: run_range(0, rem))
@@ -227,8 +241,8 @@ def run_layer_workload(mas, args, shape, dev) -> dict:
     torch.cuda.synchronize()
     stream_us = (time.perf_counter() - s0) / stream_steps * 1e6
 
-    reps = 40 * n_sets if shape.decode else 4 * n_sets
-    op_us = time_ops_per_launch(mas, sets, reps)
+    launches = max(2 * n_sets, 100) if shape.decode else 4 * n_sets
+    op_us = time_ops(mas, sets, launches, ("fused_add_rmsnorm",) if shape.norm_only else OPS)
     cb = wl.credited_bytes(shape)
     ops = {op: {"us": round(us, 3), "GB/s": round(cb[op] / us / 1e3, 1),
                 "frac": round(cb[op] / us / 1e3 / PEAK_HBM_GBS, 4)} for op, us in op_us.items()}
@@ -256,7 +270,7 @@ def run_pass_workload(mas, args, shape, dev) -> dict:
         g.replay()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    op_us = time_ops_per_launch(mas, passes[0].layers, 2 * shape.layers)
+    op_us = time_ops(mas, passes[0].layers, shape.layers)
     cb = wl.credited_bytes(shape)
     ops = {op: {"us": round(us, 3), "GB/s": round(cb[op] / us / 1e3, 1),
                 "frac": round(cb[op] / us / 1e3 / PEAK_HBM_GBS, 4)} for op, us in op_us.items()}
@@ -317,6 +331,7 @@ def main() -> int:
     }
     if "stream_us_per_step" in res:
         line["stream_us_per_step"] = round(res["stream_us_per_step"], 3)
+    line["copy_ceiling_GBps"] = round(copy_ceiling_gbs(dev), 1)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_layer(shape, args.cpu_seconds, args.fp8_norms)
     print(json.dumps(line), flush=True)

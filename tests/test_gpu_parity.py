@@ -355,3 +355,43 @@ def test_empty_inputs_are_no_ops(mas, dev):
                                   torch.zeros(4, 64, dtype=torch.bfloat16, device=dev))
     assert out.shape == (0, 64)
     torch.cuda.synchronize()
+
+
+# ---- committed golden fixtures ------------------------------------------------------------------------
+
+def test_kernels_reproduce_golden_fixtures(mas, dev):
+    from conftest import GOLDEN_DIR, from_bits
+    gd = np.load(GOLDEN_DIR / "layer_ops.npz")
+
+    def dev_bf16(key):
+        return from_bits(gd[key]).to(dev)
+
+    x, r = dev_bf16("norm_x"), dev_bf16("norm_r")
+    mas.fused_add_rmsnorm(x, r, dev_bf16("norm_w"), float(gd["norm_eps"]))
+    assert np.array_equal(bits(r), gd["norm_res"])
+    _close_bf16(bits(x), gd["norm_out"], min_exact=0.98)
+
+    x, r = dev_bf16("norm_x"), dev_bf16("norm_r")
+    out = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=dev)
+    mas.fused_add_rmsnorm_quant(out, x, r, dev_bf16("norm_w"), float(gd["quant_scale"]), float(gd["norm_eps"]))
+    assert np.array_equal(bits(r), gd["quant_res"])
+    gv, wv = on.fp8_to_f32(fp8_codes(out)), on.fp8_to_f32(gd["quant_out"])
+    assert np.all(np.abs(gv - wv) <= np.maximum(np.abs(wv) * 2.0 ** -3, 2.0 ** -9))
+
+    _close_bf16(bits(mas.silu_and_mul(dev_bf16("silu_in"))), gd["silu_out"], min_exact=0.95)
+
+    table = torch.from_numpy(gd["rope_table"]).to(dev)
+    pos = torch.from_numpy(gd["rope_pos"]).to(dev)
+    for layout, neox in (("neox", True), ("gptj", False)):
+        q, k = dev_bf16("rope_q"), dev_bf16("rope_k")
+        mas.apply_rope_with_cos_sin_cache_inplace(pos, q, k, 128, table, neox)
+        assert np.array_equal(bits(q), gd[f"rope_{layout}_q"]) and np.array_equal(bits(k), gd[f"rope_{layout}_k"])
+
+    kc, vc = dev_bf16("kv_kc0"), dev_bf16("kv_vc0")
+    i32 = {key: torch.from_numpy(gd[key]).to(dev) for key in ("kv_tables", "kv_indptr", "kv_bidx", "kv_pos")}
+    mas.append_paged_kv_cache(dev_bf16("kv_k"), dev_bf16("kv_v"), i32["kv_bidx"], i32["kv_pos"], (kc, vc),
+                              i32["kv_tables"].flatten(), i32["kv_indptr"])
+    assert np.array_equal(bits(kc), gd["kv_kc"]) and np.array_equal(bits(vc), gd["kv_vc"])
+
+    out = mas.embedding.embedding(torch.from_numpy(gd["emb_ids"]).to(dev), dev_bf16("emb_table"))
+    assert np.array_equal(bits(out), gd["emb_out"])

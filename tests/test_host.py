@@ -1,0 +1,130 @@
+"""Host-side checks that need no GPU: the C-ABI library loads and exports every entry point that
+include/mas_kernels.h declares, status reporting, argument validation (raised before anything is
+enqueued), the torch.library registrations and their fake kernels, and the golden fixtures."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN_DIR, ROOT
+
+HEADER = ROOT / "include" / "mas_kernels.h"
+
+
+def declared_entry_points() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return re.findall(r"^\s*(?:int|const char\s*\*)\s+(mas_\w+)\s*\(", text, flags=re.M)
+
+
+def test_header_declares_the_bound_entry_points(mas):
+    declared = declared_entry_points()
+    assert len(declared) >= 9
+    assert sorted(declared) == sorted(mas._lib.exported_symbols())
+
+
+def test_library_loads_and_exports_every_declared_symbol(mas):
+    lib = mas.load_library()
+    raw = ctypes.CDLL(str(mas._build.LIBRARY_PATH))
+    for name in declared_entry_points():
+        assert hasattr(raw, name), f"{name} not exported"
+        assert getattr(lib, name) is not None
+
+
+def test_library_links_against_one_hip_runtime(mas):
+    mas.load_library()
+    maps = Path("/proc/self/maps").read_text()
+    runtimes = set(re.findall(r"\S*libamdhip64\S*", maps))
+    assert len(runtimes) == 1, runtimes
+
+
+def test_status_strings_and_version(mas):
+    lib = mas.load_library()
+    assert lib.mas_status_string(0) == b"ok"
+    assert b"unsupported" in lib.mas_status_string(-2)
+    assert b"alignment" in lib.mas_status_string(-3)
+    assert mas.library_version() == (0, 1, 0)
+    with pytest.raises(mas._lib.KernelError, match="status -1"):
+        mas._lib.check(-1, "op")
+    assert mas._lib.describe_error_bits(1 | 8) == "token id outside [0, vocab); " \
+                                                 "page slot past kv_indices or page id outside the cache"
+
+
+def test_rows_view():
+    from mini_agent_serve_amd._tensors import rows_view
+    t = torch.empty(6, 10)
+    assert rows_view(t, "t") == (6, 10)
+    assert rows_view(torch.empty(4, 3, 10), "t") == (12, 10)
+    qkv = torch.empty(5, 24)
+    assert rows_view(qkv[:, 8:16], "q") == (5, 24)
+    assert rows_view(torch.empty(1, 1, 7), "t") == (1, 7)
+    assert rows_view(torch.empty(4, 1, 7).as_strided((4, 1, 7), (7, 99, 1)), "t") == (4, 7)
+    with pytest.raises(ValueError, match="contiguous in its last dimension"):
+        rows_view(torch.empty(10, 6).t(), "t")
+    assert rows_view(torch.empty(3, 4, 8)[:, ::2], "t") == (6, 16)     # every other row: one stride
+    with pytest.raises(ValueError, match="one row index"):
+        rows_view(torch.empty(3, 4, 8)[:, :2], "t")
+
+
+def test_arguments_are_validated_before_launch(mas):
+    cpu = torch.zeros(4, 64, dtype=torch.bfloat16)
+    w = torch.ones(64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU"):
+        mas.fused_add_rmsnorm(cpu, cpu.clone(), w)
+    with pytest.raises(ValueError, match="GPU"):
+        mas.silu_and_mul(cpu)
+    with pytest.raises(ValueError, match="GPU"):
+        mas.embedding.embedding(torch.zeros(3, dtype=torch.int64), cpu)
+    with pytest.raises(ValueError, match="GPU"):
+        mas.apply_rope_with_cos_sin_cache_inplace(torch.zeros(4, dtype=torch.int32), cpu, cpu, 64,
+                                                  torch.zeros(8, 64))
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    with FakeTensorMode():                      # GPU-device tensors without a GPU: checks run, nothing launches
+        h = torch.empty(4, 64, dtype=torch.bfloat16, device="cuda")
+        wd = torch.empty(64, dtype=torch.bfloat16, device="cuda")
+        with pytest.raises(TypeError, match="bfloat16"):
+            mas.fused_add_rmsnorm(h.float(), h.float(), wd)
+        with pytest.raises(ValueError, match="weight must be a contiguous"):
+            mas.fused_add_rmsnorm(h, h.clone(), torch.empty(32, dtype=torch.bfloat16, device="cuda"))
+        with pytest.raises(ValueError, match="even"):
+            mas.silu_and_mul(torch.empty(4, 63, dtype=torch.bfloat16, device="cuda"))
+        with pytest.raises(ValueError, match="rotary_dim"):
+            mas.apply_rope_with_cos_sin_cache_inplace(torch.empty(4, dtype=torch.int32, device="cuda"), h, h, 64,
+                                                      torch.empty(8, 48, device="cuda"))
+        with pytest.raises(ValueError, match="kv_layout"):
+            mas.append_paged_kv_cache(h, h, None, None, (h, h), None, None, None, "NDH")
+        with pytest.raises(TypeError, match="int64"):
+            mas.embedding.embedding(torch.empty(3, dtype=torch.int32, device="cuda"), h)
+
+
+def test_fake_kernels_under_fake_tensor_mode(mas):
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    with FakeTensorMode():
+        x = torch.empty(7, 2 * 96, dtype=torch.bfloat16, device="cuda")
+        assert torch.ops.mas.silu_and_mul(x).shape == (7, 96)
+        ids = torch.empty(2, 5, dtype=torch.int64, device="cuda")
+        table = torch.empty(10, 32, dtype=torch.bfloat16, device="cuda")
+        assert torch.ops.mas.embedding(ids, table).shape == (2, 5, 32)
+        h = torch.empty(3, 64, dtype=torch.bfloat16, device="cuda")
+        torch.ops.mas.fused_add_rmsnorm(h, h.clone(), torch.empty(64, dtype=torch.bfloat16, device="cuda"), 1e-6)
+    expected = {"fused_add_rmsnorm", "fused_add_rmsnorm_quant", "fused_add_rmsnorm_quant_hs", "silu_and_mul",
+                "silu_and_mul_out", "apply_rope_with_cos_sin_cache_inplace", "append_paged_kv_cache",
+                "store_kv_slots", "embedding"}
+    assert expected <= {name for name in dir(torch.ops.mas) if not name.startswith("_")}
+
+
+def test_golden_fixtures_reproduce():
+    """The committed fixtures are what the oracle computes today."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("gen_golden", GOLDEN_DIR / "gen_golden.py")
+    gen = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(gen)
+    fresh = gen.build()
+    stored = np.load(GOLDEN_DIR / "layer_ops.npz")
+    assert set(stored.files) == set(fresh)
+    for key in stored.files:
+        assert np.array_equal(stored[key], fresh[key]), key
