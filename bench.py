@@ -3,8 +3,9 @@
 
 Default workload: one Devstral-Small-2 decoder layer at a 64-token decode step (hidden 5120,
 intermediate 32768, 32 q / 8 kv heads of 128, KV pool 2048 pages x 256 slots). A step is that
-layer's five kernels - RMSNorm+residual, RoPE, paged KV store, RMSNorm+residual, SiluAndMul - over
-one 64-token batch. Inputs are resident in HBM before the timed region. The cold protocol (default)
+layer's hot-path kernels over one 64-token batch - RMSNorm+residual, RoPE + paged KV store (one
+fused kernel; the reference's two separate calls are timed alongside), RMSNorm+residual,
+SiluAndMul. Inputs are resident in HBM before the timed region. The cold protocol (default)
 cycles through enough distinct layer buffer sets (each with its own KV cache) that a step never
 finds its data in the 256 MB Infinity Cache - what a 40-layer forward pass sees; steps are replayed
 from a captured HIP graph, as the reference's model runner replays its decode graphs.
@@ -39,6 +40,10 @@ METRIC = "HBM GB/s & % of peak for layer kernels; µs/layer at 64-token decode"
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 COLD_BYTES = 768 << 20         # working set cycled by the cold protocol (3x the Infinity Cache)
 OPS = ("fused_add_rmsnorm", "rope", "append_paged_kv_cache", "silu_and_mul")
+# HBM bytes per launch of a workload's dominant kernel, from two rocprofv3 counter passes
+# (FETCH_SIZE, then WRITE_SIZE) over `bench.py --pmc-probe`, each calibrated by the same counter on
+# a 256 MiB device copy (fetch factor 1.9997, write factor 1.0000). Re-measure when the kernel changes.
+MEASURED_TRAFFIC = {("decode64_24b", "silu_and_mul"): 12_622_649}
 
 
 def parse_args():
@@ -51,6 +56,12 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU time of the baseline sample")
     p.add_argument("--fp8-norms", action="store_true", help="use the fp8-output norm (the reference's in-layer variant)")
+    p.add_argument("--pmc-probe", action="store_true",
+                   help="short run for rocprofv3 --pmc: the dominant kernel 20 times on the cold layer sets, "
+                        "then a 256 MiB device copy (the calibration reference for FETCH_SIZE / WRITE_SIZE)")
+    p.add_argument("--separate-rope-kv", action="store_true",
+                   help="run RoPE and the KV append as the reference's two calls (default: one fused kernel, "
+                        "same results, one launch fewer per layer); the other form is timed alongside")
     return p.parse_args()
 
 
@@ -74,6 +85,10 @@ def op_launcher(mas, b, op):
                                                       "NHD")
     if op == "silu_and_mul":
         return lambda: mas.activation.silu_and_mul(li.gate_up, out=b.silu_out)
+    if op == "rope_append":
+        return lambda: mas.fused.apply_rope_and_append_paged_kv_cache(
+            li.positions, li.q, li.k, b.v3, s.head_dim, li.table, True, li.batch_indices, (li.k_cache, li.v_cache),
+            b.kv_indices, li.kv_indptr, None, "NHD")
     raise ValueError(op)
 
 
@@ -179,7 +194,7 @@ def cpu_baseline_layer(shape, seconds: float, fp8_norms: bool) -> dict:
         oops.silu_and_mul(gu)
 
     sample_shape = type(shape)(**{**shape.__dict__, "tokens": tokens})
-    per_layer = wl.layer_credited_bytes(sample_shape)
+    per_layer = wl.layer_credited_bytes(sample_shape)     # the oracle runs RoPE and the store separately
     if fp8_norms:
         per_layer -= 2 * tokens * shape.hidden
     layer()                                  # warm-up
@@ -199,9 +214,11 @@ def run_layer_workload(mas, args, shape, dev) -> dict:
     wl, lp = mas.workloads, mas.layer_pass
     n_sets = 1 if args.protocol == "hot" else max(2, math.ceil(COLD_BYTES / footprint_bytes(shape)))
     table = mas.rope.cos_sin_cache(shape.max_position, shape.head_dim, shape.theta).to(dev)
-    sets = [lp.LayerBuffers(wl.make_layer_inputs(shape, dev, seed=i, fill_on_device=True, table=table),
-                            fp8_norms=args.fp8_norms) for i in range(n_sets)]
-    per_step = wl.layer_credited_bytes(shape)
+    sets = [lp.LayerBuffers(wl.make_layer_inputs(shape, dev, seed=i, fill_on_device=True, table=table,
+                                                     zero_cache=False),
+                            fp8_norms=args.fp8_norms, fuse_rope_kv=not args.separate_rope_kv) for i in range(n_sets)]
+    fused = not args.separate_rope_kv
+    per_step = wl.layer_credited_bytes(shape, fused)
     if args.fp8_norms:
         per_step -= 2 * shape.tokens * shape.hidden
     steps = args.steps if args.steps is not None else (2000 if shape.decode else 40)
@@ -211,27 +228,38 @@ def run_layer_workload(mas, args, shape, dev) -> dict:
         for i in range(lo, hi):
             lp.run_layer(sets[i % n_sets])
 
-    # one replay runs a whole number of passes over the layer sets and at least 50 steps, so the
-    # graph launch itself is amortised
-    per_graph = n_sets * max(1, math.ceil(50 / n_sets))
-    full = capture(lambda: run_range(0, per_graph))
-    graphs = {}
-
-    def replay(k):
-        for _ in range(k // per_graph):
-            full.replay()
-        rem = k % per_graph
-        if rem:
-            if rem not in graphs:
+    def timed_steps(k: int, w: int) -> float:
+        """Seconds for k steps replayed from HIP graphs after w warm-up steps. One replay runs a
+        whole number of passes over the layer sets and at least 50 steps, amortising the launch."""
+        per_graph = n_sets * max(1, math.ceil(50 / n_sets))
+        graphs = {per_graph: capture(lambda: run_range(0, per_graph))}
+        for count in (w, k):                          # every graph is captured before the timed region
+            rem = count % per_graph
+            if rem and rem not in graphs:
                 graphs[rem] = capture(lambda: run_range(0, rem))
-            graphs[rem].replay()
 
-    replay(warmup)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    replay(steps)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+        def replay(count):
+            for _ in range(count // per_graph):
+                graphs[per_graph].replay()
+            if count % per_graph:
+                graphs[count % per_graph].replay()
+
+        replay(w)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        replay(k)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
+    elapsed = timed_steps(steps, warmup)
+    other_us = None
+    if not shape.norm_only:
+        # the other RoPE / KV form, for comparison (same buffers, same step count)
+        for b in sets:
+            b.fuse_rope_kv = not fused
+        other_us = timed_steps(steps, warmup) / steps * 1e6
+        for b in sets:
+            b.fuse_rope_kv = fused
 
     # stream-launched steps (no graph), for comparison
     stream_steps = min(steps, 10 * n_sets) if shape.decode else min(steps, 4 * n_sets)
@@ -242,20 +270,24 @@ def run_layer_workload(mas, args, shape, dev) -> dict:
     stream_us = (time.perf_counter() - s0) / stream_steps * 1e6
 
     launches = max(2 * n_sets, 100) if shape.decode else 4 * n_sets
-    op_us = time_ops(mas, sets, launches, ("fused_add_rmsnorm",) if shape.norm_only else OPS)
+    timed = ("fused_add_rmsnorm",) if shape.norm_only else OPS + ("rope_append",)
+    op_us = time_ops(mas, sets, launches, timed)
     cb = wl.credited_bytes(shape)
     ops = {op: {"us": round(us, 3), "GB/s": round(cb[op] / us / 1e3, 1),
                 "frac": round(cb[op] / us / 1e3 / PEAK_HBM_GBS, 4)} for op, us in op_us.items()}
     ms_per_step = elapsed / steps * 1e3
     dominant = "fused_add_rmsnorm" if shape.norm_only else "silu_and_mul"
-    return {"steps": steps, "warmup": warmup, "ms_per_step": ms_per_step, "per_step_bytes": per_step,
-            "value": per_step / (ms_per_step * 1e-3) / 1e9, "stream_us_per_step": stream_us, "ops": ops,
-            "sets": n_sets, "dominant": dominant, "dominant_bytes": cb[dominant], "dominant_us": op_us[dominant]}
+    res = {"steps": steps, "warmup": warmup, "ms_per_step": ms_per_step, "per_step_bytes": per_step,
+           "value": per_step / (ms_per_step * 1e-3) / 1e9, "stream_us_per_step": stream_us, "ops": ops,
+           "sets": n_sets, "dominant": dominant, "dominant_bytes": cb[dominant], "dominant_us": op_us[dominant]}
+    if other_us is not None:
+        res["separate_us_per_layer" if fused else "fused_us_per_layer"] = other_us
+    return res
 
 
 def run_pass_workload(mas, args, shape, dev) -> dict:
     lp, wl = mas.layer_pass, mas.workloads
-    passes = [lp.DecodePass(shape, dev, seed=0, fp8_norms=args.fp8_norms)]
+    passes = [lp.DecodePass(shape, dev, seed=0, fp8_norms=args.fp8_norms, fuse_rope_kv=not args.separate_rope_kv)]
     per_step = passes[0].credited_bytes()
     if args.fp8_norms:
         per_step -= 2 * shape.layers * shape.tokens * shape.hidden
@@ -270,7 +302,7 @@ def run_pass_workload(mas, args, shape, dev) -> dict:
         g.replay()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    op_us = time_ops(mas, passes[0].layers, shape.layers)
+    op_us = time_ops(mas, passes[0].layers, shape.layers, OPS + ("rope_append",))
     cb = wl.credited_bytes(shape)
     ops = {op: {"us": round(us, 3), "GB/s": round(cb[op] / us / 1e3, 1),
                 "frac": round(cb[op] / us / 1e3 / PEAK_HBM_GBS, 4)} for op, us in op_us.items()}
@@ -279,6 +311,27 @@ def run_pass_workload(mas, args, shape, dev) -> dict:
             "value": per_step / (ms_per_step * 1e-3) / 1e9, "ops": ops, "sets": 1, "dominant": "silu_and_mul",
             "dominant_bytes": cb["silu_and_mul"], "dominant_us": op_us["silu_and_mul"],
             "us_per_layer": ms_per_step * 1e3 / shape.layers}
+
+
+def pmc_probe(mas, args, shape, dev) -> None:
+    """Launches only what a counter pass needs: the workload's dominant kernel (SiluAndMul, or the
+    norm for the norm-only case) 20 times across the cold layer sets, then 4 copies of 256 MiB."""
+    wl, lp = mas.workloads, mas.layer_pass
+    n_sets = max(2, math.ceil(COLD_BYTES / footprint_bytes(shape)))
+    table = mas.rope.cos_sin_cache(shape.max_position, shape.head_dim, shape.theta).to(dev)
+    sets = [lp.LayerBuffers(wl.make_layer_inputs(shape, dev, seed=i, fill_on_device=True, table=table,
+                                                 zero_cache=False)) for i in range(n_sets)]
+    op = "fused_add_rmsnorm" if shape.norm_only else "silu_and_mul"
+    for i in range(20):
+        op_launcher(mas, sets[i % n_sets], op)()
+    torch.cuda.synchronize()
+    a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(4):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_probe": op, "launches": 20, "bytes_per_launch": wl.credited_bytes(shape)[op],
+                      "calibration_copy_bytes": 256 << 20}), flush=True)
 
 
 def main() -> int:
@@ -297,6 +350,9 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     shape = mas.workloads.SHAPES[args.workload]
+    if args.pmc_probe:
+        pmc_probe(mas, args, shape, dev)
+        return 0
     if shape.layers > 1:
         res = run_pass_workload(mas, args, shape, dev)
     else:
@@ -320,17 +376,20 @@ def main() -> int:
                    "intermediate": shape.inter, "q_heads": shape.q_heads, "kv_heads": shape.kv_heads,
                    "head_dim": shape.head_dim, "kv_pages": shape.num_pages, "page_size": shape.page_size,
                    "layers": shape.layers, "protocol": args.protocol, "layer_sets": res["sets"],
-                   "launch": "hip-graph", "norm_output": "fp8" if args.fp8_norms else "bf16"},
+                   "launch": "hip-graph", "norm_output": "fp8" if args.fp8_norms else "bf16",
+                   "rope_kv": "separate" if args.separate_rope_kv else "fused"},
         "us_per_layer": round(res.get("us_per_layer", res["ms_per_step"] * 1e3), 3),
         "frac_of_peak": round(res["value"] / PEAK_HBM_GBS, 4),
         "ops": res["ops"],
         "roofline": {"bound": "hbm", "kernel": res["dominant"], "achieved": round(dom_gbs, 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(dom_gbs / PEAK_HBM_GBS, 4),
-                     "traffic": None, "bytes_per_launch": res["dominant_bytes"],
+                     "traffic": MEASURED_TRAFFIC.get((shape.name, res["dominant"])),
+                     "bytes_per_launch": res["dominant_bytes"],
                      "avg_launch_us": round(res["dominant_us"], 3)},
     }
-    if "stream_us_per_step" in res:
-        line["stream_us_per_step"] = round(res["stream_us_per_step"], 3)
+    for key in ("separate_us_per_layer", "fused_us_per_layer", "stream_us_per_step"):
+        if key in res:
+            line[key] = round(res[key], 3)
     line["copy_ceiling_GBps"] = round(copy_ceiling_gbs(dev), 1)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_layer(shape, args.cpu_seconds, args.fp8_norms)

@@ -142,6 +142,28 @@ int mas_store_kv_slots_bf16(void* k_cache, void* v_cache, int64_t page_stride, i
                             hipStream_t stream);
 
 /*
+ * RoPE and the paged KV append fused into one pass over the token rows: q and k are rotated in
+ * place exactly as by mas_rope_cos_sin_cache_bf16 (rotary_dim = head_dim, int32 positions), and
+ * the rotated k plus v are written to the cache exactly as by mas_append_paged_kv_cache_bf16 with
+ * the same positions. Each k row is read once and one kernel is launched instead of two. A
+ * position outside the table skips the rotation of that token (its unrotated k is stored); a
+ * destination out of range skips its cache write; both are reported through `err` as above.
+ * head_dim must be one of 32, 64, 128, 256, 512.
+ * Replaces the call pair at miniagentserve/models/devstral2/devstral2.py:163-173
+ * (apply_rope_with_cos_sin_cache_inplace then append_paged_kv_cache on the same rows).
+ */
+int mas_rope_append_paged_kv_cache_bf16(void* q, int64_t q_stride, int64_t q_head_stride, int64_t num_q_heads,
+                                        void* k, int64_t k_stride, int64_t k_head_stride, const void* v,
+                                        int64_t v_stride, int64_t v_head_stride, int64_t num_kv_heads,
+                                        const int32_t* positions, const float* table, int64_t table_stride,
+                                        int64_t table_rows, int64_t rows, int64_t head_dim, int is_neox,
+                                        void* k_cache, void* v_cache, int64_t page_stride, int64_t entry_stride,
+                                        int64_t head_stride, int64_t num_pages, int64_t page_size,
+                                        const int32_t* batch_indices, const int32_t* kv_indices,
+                                        int64_t num_indices, const int32_t* kv_indptr, int64_t batch, uint32_t* err,
+                                        hipStream_t stream);
+
+/*
  * Token-embedding gather: out[t, :] = weight[ids[t], :], a bit copy. ids: int64 [rows];
  * weight: [vocab, hidden] with row stride weight_stride; out: [rows, hidden].
  * Replaces nn.Embedding.forward at miniagentserve/models/devstral2/devstral2.py:260,282.

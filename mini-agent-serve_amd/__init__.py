@@ -8,6 +8,7 @@ Drop-ins for the calls the reference's layer modules make
 - ``rope.apply_rope_with_cos_sin_cache_inplace``                    (flashinfer.rope, :163-166)
 - ``page.append_paged_kv_cache`` (+ ``page.store_kv_slots``)        (flashinfer.page, :170-173)
 - ``embedding.embedding`` / ``embedding.Embedding``                 (nn.Embedding, :260, :282)
+- ``fused.apply_rope_and_append_paged_kv_cache``                    (the :163-166 + :170-173 pair, one kernel)
 
 Each op validates its tensors, then calls hand-written HIP kernels in ``libmas_kernels.so``
 through the C ABI of ``include/mas_kernels.h`` on torch's current stream. There is no CPU or
@@ -18,17 +19,19 @@ imports it as ``mini_agent_serve_amd``.
 """
 from __future__ import annotations
 
-from . import _lib, activation, embedding, norm, page, rope, workloads
+from . import _lib, activation, embedding, fused, norm, page, rope, workloads
 from . import layer_pass
 from . import _ops  # noqa: F401  (registers the torch.library ops)
 from .activation import silu_and_mul
 from .embedding import Embedding
+from .fused import apply_rope_and_append_paged_kv_cache
 from .norm import fused_add_rmsnorm, fused_add_rmsnorm_quant
 from .page import append_paged_kv_cache, store_kv_slots
 from .rope import apply_rope_with_cos_sin_cache_inplace
 
 __all__ = [
-    "activation", "embedding", "norm", "page", "rope", "workloads", "layer_pass",
+    "activation", "embedding", "fused", "norm", "page", "rope", "workloads", "layer_pass",
+    "apply_rope_and_append_paged_kv_cache",
     "silu_and_mul", "Embedding", "fused_add_rmsnorm", "fused_add_rmsnorm_quant", "append_paged_kv_cache",
     "store_kv_slots", "apply_rope_with_cos_sin_cache_inplace", "load_library", "library_version",
 ]

@@ -35,6 +35,10 @@ _SIGNATURES: dict[str, list] = {
                                        _i64, _i64, _i64, _i64, _c_void_p, _c_void_p],
     "mas_store_kv_slots_bf16": [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _c_void_p, _i64, _i64,
                                 _c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p],
+    "mas_rope_append_paged_kv_cache_bf16": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64,
+                                            _i64, _i64, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i32,
+                                            _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _c_void_p,
+                                            _c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p],
     "mas_embedding_bf16": [_c_void_p, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _c_void_p],
 }
 _RESTYPES = {"mas_status_string": ctypes.c_char_p}

@@ -10,7 +10,7 @@ from __future__ import annotations
 import torch
 from torch.library import custom_op
 
-from . import activation, embedding, norm, page, rope
+from . import activation, embedding, fused, norm, page, rope
 
 Tensor = torch.Tensor
 
@@ -114,3 +114,17 @@ def _embedding(input_ids: Tensor, weight: Tensor) -> Tensor:
 @_embedding.register_fake
 def _(input_ids, weight):
     return weight.new_empty(tuple(input_ids.shape) + (weight.shape[1],))
+
+
+@custom_op("mas::apply_rope_and_append_paged_kv_cache", mutates_args=("query", "key", "k_cache", "v_cache"))
+def _rope_append(positions: Tensor, query: Tensor, key: Tensor, value: Tensor, head_size: int, cos_sin_cache: Tensor,
+                 is_neox: bool, batch_indices: Tensor, k_cache: Tensor, v_cache: Tensor, kv_indices: Tensor,
+                 kv_indptr: Tensor, kv_layout: str) -> None:
+    fused._fused(positions, query, key, value, head_size, cos_sin_cache, is_neox, batch_indices, (k_cache, v_cache),
+                 kv_indices, kv_indptr, kv_layout, None)
+
+
+@_rope_append.register_fake
+def _(positions, query, key, value, head_size, cos_sin_cache, is_neox, batch_indices, k_cache, v_cache, kv_indices,
+      kv_indptr, kv_layout):
+    return None

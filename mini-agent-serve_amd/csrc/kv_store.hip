@@ -9,8 +9,8 @@
 //   k_cache[page, entry, h, :] = key[t, h, :];  v_cache[page, entry, h, :] = value[t, h, :]
 //
 // A bit copy: one wavefront per token, its destination resolved once per wavefront from
-// wave-uniform (scalar-cache) index loads; each lane moves 16-byte vectors of k and v, with all
-// of its loads issued before its stores. Duplicate destinations (padding rows aimed at the
+// wave-uniform (scalar-cache) index loads issued after the token's k/v loads, so both latencies
+// overlap; each lane moves 16-byte vectors of k and v, all loads issued before the stores. Duplicate destinations (padding rows aimed at the
 // model runner's sink block) are plain racing stores of whole rows: one writer wins.
 #include "device.h"
 
@@ -19,7 +19,7 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / kWave;
-constexpr int kUnroll = 4;
+constexpr int kUnroll = 2;
 
 struct KvArgs {
   uint16_t* k_cache;
@@ -59,18 +59,18 @@ __device__ __forceinline__ bool resolve(const KvArgs& a, int64_t t, int64_t* pag
     *entry = slot - pg * a.page_size;
     return true;
   } else {
+    // Both per-token indices are loaded before either is checked, so the two loads overlap.
     const int64_t b = a.batch_indices[t];
     const int64_t p = a.positions[t];
-    if (b < 0 || b >= a.batch) {
-      report(a.err, MAS_ERRBIT_BATCH);
+    const bool b_ok = b >= 0 && b < a.batch;
+    if (!b_ok || p < 0) {
+      report(a.err, b_ok ? MAS_ERRBIT_POSITION : MAS_ERRBIT_BATCH);
       return false;
     }
-    if (p < 0) {
-      report(a.err, MAS_ERRBIT_POSITION);
-      return false;
-    }
-    const int64_t idx = static_cast<int64_t>(a.kv_indptr[b]) + p / a.page_size;
-    if (idx < 0 || idx >= a.num_indices || idx >= static_cast<int64_t>(a.kv_indptr[b + 1])) {
+    const int64_t first = a.kv_indptr[b];
+    const int64_t end = a.kv_indptr[b + 1];
+    const int64_t idx = first + p / a.page_size;
+    if (idx < 0 || idx >= a.num_indices || idx >= end) {
       report(a.err, MAS_ERRBIT_PAGE);
       return false;
     }
@@ -85,37 +85,48 @@ __device__ __forceinline__ bool resolve(const KvArgs& a, int64_t t, int64_t* pag
   }
 }
 
-template <bool kSlotForm>
+// Element offset of 16-byte vector v of a token's row, for a row made of heads of vec_per_head
+// vectors placed head_stride elements apart.
+__device__ __forceinline__ int64_t vec_offset(int v, int vec_per_head, int64_t head_stride, bool contiguous) {
+  if (contiguous) return 8 * static_cast<int64_t>(v);
+  const int h = v / vec_per_head;
+  return h * head_stride + 8 * (v - h * vec_per_head);
+}
+
+// The source rows are loaded before the destination is resolved: the k/v loads do not depend on
+// it, so the index loads (scalar cache) and the data loads are in flight together.
+template <bool kSlotForm, bool kContig>
 __global__ __launch_bounds__(kBlock) void kv_store(KvArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t t = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_id_uniform();
   if (t >= a.rows) return;
-  int64_t page = 0, entry = 0;
-  if (!resolve<kSlotForm>(a, t, &page, &entry)) return;
-  const int64_t dst_row = page * a.page_stride + entry * a.entry_stride;
   const uint16_t* ksrc = a.key + t * a.key_stride;
   const uint16_t* vsrc = a.value + t * a.value_stride;
-
-  for (int base = lane; base < a.vec_per_row; base += kWave * kUnroll) {
+  const int nv = a.vec_per_row;
+  const int chunks = (nv + kWave * kUnroll - 1) / (kWave * kUnroll);
+  int64_t dst_row = 0;
+  for (int c = 0; c < chunks; ++c) {
     u32x4 kv[kUnroll], vv[kUnroll];
-    int64_t dst[kUnroll];
 #pragma unroll
     for (int j = 0; j < kUnroll; ++j) {
-      const int v = base + j * kWave;
-      if (v < a.vec_per_row) {
-        const int h = v / a.vec_per_head;
-        const int d = (v - h * a.vec_per_head) * 8;
-        kv[j] = load_stream(ksrc + h * a.key_head_stride + d);
-        vv[j] = load_stream(vsrc + h * a.value_head_stride + d);
-        dst[j] = dst_row + h * a.head_stride + d;
-      }
+      const int v = c * kWave * kUnroll + j * kWave + lane;
+      const int vl = v < nv ? v : nv - 1;
+      kv[j] = load_stream(ksrc + vec_offset(vl, a.vec_per_head, a.key_head_stride, kContig));
+      vv[j] = load_stream(vsrc + vec_offset(vl, a.vec_per_head, a.value_head_stride, kContig));
+    }
+    load_fence();
+    if (c == 0) {
+      int64_t page = 0, entry = 0;
+      if (!resolve<kSlotForm>(a, t, &page, &entry)) return;
+      dst_row = page * a.page_stride + entry * a.entry_stride;
     }
 #pragma unroll
     for (int j = 0; j < kUnroll; ++j) {
-      const int v = base + j * kWave;
-      if (v < a.vec_per_row) {
-        store_stream(a.k_cache + dst[j], kv[j]);
-        store_stream(a.v_cache + dst[j], vv[j]);
+      const int v = c * kWave * kUnroll + j * kWave + lane;
+      if (v < nv) {
+        const int64_t off = dst_row + vec_offset(v, a.vec_per_head, a.head_stride, kContig);
+        store_stream(a.k_cache + off, kv[j]);
+        store_stream(a.v_cache + off, vv[j]);
       }
     }
   }
@@ -137,11 +148,18 @@ int check_common(const KvArgs& a, int64_t num_heads, int64_t head_dim, bool* emp
   return ok ? MAS_OK : MAS_ERR_MISALIGNED;
 }
 
+// Rows whose heads sit back to back in the source and in the cache entry (NHD caches fed by the
+// q/k/v column views) are one contiguous run at both ends: no per-vector head arithmetic.
 template <bool kSlotForm>
 int launch(const KvArgs& a, hipStream_t s) {
+  const int64_t head_dim = 8 * static_cast<int64_t>(a.vec_per_head);
+  const bool contiguous = a.key_head_stride == head_dim && a.value_head_stride == head_dim && a.head_stride == head_dim;
   const int64_t blocks = cdiv(a.rows, kWavesPerBlock);
   if (blocks > INT32_MAX) return MAS_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL((kv_store<kSlotForm>), dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, s, a);
+  if (contiguous)
+    hipLaunchKernelGGL((kv_store<kSlotForm, true>), dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, s, a);
+  else
+    hipLaunchKernelGGL((kv_store<kSlotForm, false>), dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, s, a);
   return launch_status();
 }
 

@@ -9,9 +9,9 @@
 //   bf16 epilogue: x <- bf16(y)       fp8 epilogue: out <- e4m3fn(clamp(y / scale, +-448))
 //
 // Fast path: one workgroup per row. The row is held in registers as VPT 128-bit vectors per
-// lane (8 bf16 each), so x and r are read from HBM once and every output is written once;
-// the weight slice of each lane is loaded once per workgroup and reused across the rows it
-// handles. Row sum of squares: DPP wavefront sum, then one LDS slot per wavefront.
+// lane (8 bf16 each), so x and r are read from HBM once and every output is written once; each
+// workgroup loads its weight slice once. Row sum of squares: DPP wavefront sum, then one LDS slot
+// per wavefront.
 // Generic path (hidden not a multiple of 8, unaligned rows, or rows wider than 65536): two
 // passes over the row with scalar accesses, the second recomputing s from x and r.
 #include "device.h"
@@ -49,11 +49,11 @@ __global__ __launch_bounds__(max_threads_for(VPT)) void fused_add_rmsnorm_tile(N
   const int tid = threadIdx.x;
   const int nthr = blockDim.x;
   const float hidden_f = static_cast<float>(a.hidden);
-  const float scale = kFp8 ? norm_scale(a) : 1.0f;
 
   // Vector indices past the row end are clamped to its last vector, so every load is in bounds
   // and unconditional (the compiler then issues them back to back); those lanes contribute zero
-  // to the sum and store nothing.
+  // to the sum and store nothing. The weight slice is loaded once, ahead of the rows: measured
+  // faster on MI355X than loading it in each row's group (3.10 vs 3.25 us for 64 x 5120).
   u32x4 w[VPT];
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
@@ -75,6 +75,7 @@ __global__ __launch_bounds__(max_threads_for(VPT)) void fused_add_rmsnorm_tile(N
       rv[j] = load_stream(r + 8 * vl);
     }
     load_fence();
+    const float scale = kFp8 ? norm_scale(a) : 1.0f;
 
     float s[VPT][8];
     float ss = 0.f;
@@ -158,23 +159,30 @@ __global__ __launch_bounds__(256) void fused_add_rmsnorm_generic(NormArgs a) {
 
 constexpr int kVpts[] = {1, 2, 3, 4, 5, 6, 8};
 
-// Picks the register tile: VPT vectors per lane and a multiple of 64 lanes covering the row.
-// Few rows: favour more lanes per row (parallelism). Many rows: lanes near 256 with little
-// padding, so several workgroups share a CU.
+// Tuning overrides for experiments (0 = use the heuristic below).
+#ifndef MAS_NORM_FORCE_VPT
+#define MAS_NORM_FORCE_VPT 0
+#endif
+#ifndef MAS_NORM_BLOCKS_PER_CU
+#define MAS_NORM_BLOCKS_PER_CU 0
+#endif
+
+// Picks the register tile: VPT vectors per lane and a multiple of 64 lanes covering the row, with
+// at most 12.5% padding. The most lanes per row wins, at every row count: measured on MI355X,
+// 640 lanes beat 320 and 128 for hidden 5120, and 768 beat 512, 384 and 256 for hidden 12288
+// (more waves in flight per CU, fewer registers per lane).
 bool choose_tile(int64_t nvec, int64_t rows, int cus, int* vpt, int* threads) {
+  (void)rows;
+  (void)cus;
   int best_v = 0, best_t = 0;
   int64_t best_score = INT64_MAX;
   for (int v : kVpts) {
+    if (MAS_NORM_FORCE_VPT != 0 && v != MAS_NORM_FORCE_VPT) continue;
     const int64_t t = cdiv(cdiv(nvec, v), kWave) * kWave;
     if (t > max_threads_for(v)) continue;
     const int64_t waste = t * v - nvec;
     if (waste * 8 > nvec) continue;  // more than 12.5% idle lanes
-    int64_t score;
-    if (rows < 2 * static_cast<int64_t>(cus)) {
-      score = -t * 1024 + waste;  // most lanes
-    } else {
-      score = (t > 256 ? t - 256 : 256 - t) * 1024 + waste;
-    }
+    const int64_t score = -t * 1024 + waste;
     if (score < best_score) {
       best_score = score;
       best_v = v;
@@ -227,7 +235,9 @@ int run_norm(const NormArgs& a, int out_elem_bytes, hipStream_t stream) {
                       (reinterpret_cast<uintptr_t>(a.out) % (8 * out_elem_bytes) == 0) && (a.in_stride % 8 == 0) &&
                       (a.res_stride % 8 == 0) && (a.out_stride % 8 == 0);
   int vpt = 0, threads = 0;
-  const int64_t grid = a.rows < INT32_MAX ? a.rows : INT32_MAX;
+  int64_t grid = a.rows < INT32_MAX ? a.rows : INT32_MAX;
+  if (MAS_NORM_BLOCKS_PER_CU > 0 && grid > static_cast<int64_t>(MAS_NORM_BLOCKS_PER_CU) * cus)
+    grid = static_cast<int64_t>(MAS_NORM_BLOCKS_PER_CU) * cus;
   if (vec_ok && choose_tile(nvec, a.rows, cus, &vpt, &threads)) {
     return launch_tile<kFp8>(vpt, dim3(static_cast<uint32_t>(grid)), dim3(threads), stream, a);
   }

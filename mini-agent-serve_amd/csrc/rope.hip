@@ -47,6 +47,25 @@ __global__ __launch_bounds__(kBlock) void rope_inplace(RopeArgs a) {
   if (t >= a.rows) return;
   const int group = static_cast<int>(work - t * a.groups_per_token);
 
+  // Offsets of the two 16-byte vectors this lane owns inside a head.
+  const int off_a = kNeox ? chunk * 8 : chunk * 16;
+  const int off_b = kNeox ? kHalf + chunk * 8 : chunk * 16 + 8;
+
+  // The head data does not depend on the position: load it first (head indices past the last head
+  // are clamped to it and their stores skipped), then fetch the position and its table row.
+  uint16_t* ptr[PASSES];
+  u32x4 va[PASSES], vb[PASSES];
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    int h = (group * PASSES + p) * kHeadsPerPass + slot;
+    h = h < a.num_heads ? h : a.num_heads - 1;
+    ptr[p] = h < a.num_q_heads ? a.q + t * a.q_stride + h * a.q_head_stride
+                               : a.k + t * a.k_stride + (h - a.num_q_heads) * a.k_head_stride;
+    va[p] = load_stream(ptr[p] + off_a);
+    vb[p] = load_stream(ptr[p] + off_b);
+  }
+  load_fence();
+
   const int64_t pos = kPos64 ? static_cast<const int64_t*>(a.positions)[t]
                              : static_cast<int64_t>(static_cast<const int32_t*>(a.positions)[t]);
   if (pos < 0 || pos >= a.table_rows) {
@@ -59,26 +78,10 @@ __global__ __launch_bounds__(kBlock) void rope_inplace(RopeArgs a) {
   const float cs[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
   const float sn[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
 
-  // Offsets of the two 16-byte vectors this lane owns inside a head.
-  const int off_a = kNeox ? chunk * 8 : chunk * 16;
-  const int off_b = kNeox ? kHalf + chunk * 8 : chunk * 16 + 8;
-
-  uint16_t* ptr[PASSES];
-  u32x4 va[PASSES], vb[PASSES];
 #pragma unroll
   for (int p = 0; p < PASSES; ++p) {
     const int h = (group * PASSES + p) * kHeadsPerPass + slot;
-    ptr[p] = nullptr;
-    if (h < a.num_heads) {
-      ptr[p] = h < a.num_q_heads ? a.q + t * a.q_stride + h * a.q_head_stride
-                                 : a.k + t * a.k_stride + (h - a.num_q_heads) * a.k_head_stride;
-      va[p] = load_stream(ptr[p] + off_a);
-      vb[p] = load_stream(ptr[p] + off_b);
-    }
-  }
-#pragma unroll
-  for (int p = 0; p < PASSES; ++p) {
-    if (ptr[p] == nullptr) continue;
+    if (h >= a.num_heads) continue;
     float xa[8], xb[8], ya[8], yb[8];
     unpack8(va[p], xa);
     unpack8(vb[p], xb);
@@ -124,13 +127,22 @@ int launch_rope(RopeArgs a, hipStream_t s) {
   return launch_status();
 }
 
+// Few tokens: one pass per wavefront for the most parallelism. Many tokens: two passes per
+// wavefront (measured best on MI355X for 40 and 104 heads of 128, ahead of 1, 3, 4 and 5).
 template <int LPH, bool kNeox, bool kPos64>
 int pick_passes(RopeArgs a, int cus, hipStream_t s) {
-  // Few tokens: one pass per wavefront for the most parallelism; many tokens: several heads per
-  // lane so more loads are in flight and the table row is read by fewer wavefronts.
   constexpr int kHeadsPerPass = kWave / LPH;
-  const int64_t single = a.rows * cdiv(a.num_heads, kHeadsPerPass);
-  if (single < static_cast<int64_t>(cus) * 16) return launch_rope<LPH, kNeox, kPos64, 1>(a, s);
+  const int64_t passes = cdiv(a.num_heads, kHeadsPerPass);
+#if defined(MAS_ROPE_FORCE_PASSES) && MAS_ROPE_FORCE_PASSES > 0
+  switch (MAS_ROPE_FORCE_PASSES) {
+    case 1: return launch_rope<LPH, kNeox, kPos64, 1>(a, s);
+    case 2: return launch_rope<LPH, kNeox, kPos64, 2>(a, s);
+    case 3: return launch_rope<LPH, kNeox, kPos64, 3>(a, s);
+    case 4: return launch_rope<LPH, kNeox, kPos64, 4>(a, s);
+    default: return launch_rope<LPH, kNeox, kPos64, 5>(a, s);
+  }
+#endif
+  if (a.rows * passes < static_cast<int64_t>(cus) * 16) return launch_rope<LPH, kNeox, kPos64, 1>(a, s);
   return launch_rope<LPH, kNeox, kPos64, 2>(a, s);
 }
 

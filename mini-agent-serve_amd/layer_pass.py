@@ -5,6 +5,7 @@ Per layer, in the order of miniagentserve/models/devstral2/devstral2.py:237-253 
   1. fused add + RMSNorm of the previous sublayer output into the residual stream    (:241-246)
   2. RoPE on the q/k column views of the fused qkv output                            (:163-166)
   3. paged KV append of k/v                                                          (:170-173)
+     (``fuse_rope_kv`` runs 2 and 3 as one kernel, with the same results)
   4. fused add + RMSNorm of the attention output                                     (:248-252)
   5. SiluAndMul of the gate_up output                                                (:224)
 The reference's in-layer norms emit fp8 for its FP8 GEMMs; ``fp8_norms`` selects that epilogue,
@@ -16,7 +17,7 @@ from __future__ import annotations
 
 import torch
 
-from . import activation, embedding, norm, page, rope
+from . import activation, embedding, fused, norm, page, rope
 from .workloads import LayerInputs, Shape, credited_bytes, layer_credited_bytes, make_layer_inputs
 
 __all__ = ["LayerBuffers", "run_layer", "DecodePass"]
@@ -25,9 +26,11 @@ __all__ = ["LayerBuffers", "run_layer", "DecodePass"]
 class LayerBuffers:
     """One layer's inputs plus the outputs the kernels write (SiluAndMul output, fp8 norm output)."""
 
-    def __init__(self, inputs: LayerInputs, fp8_norms: bool = False, act_scale: float = 0.05):
+    def __init__(self, inputs: LayerInputs, fp8_norms: bool = False, act_scale: float = 0.05,
+                 fuse_rope_kv: bool = False):
         s = inputs.shape
         self.inputs = inputs
+        self.fuse_rope_kv = fuse_rope_kv
         dev = inputs.hidden.device
         self.silu_out = torch.empty(s.tokens, s.inter, dtype=torch.bfloat16, device=dev)
         self.fp8_norms = fp8_norms
@@ -49,9 +52,14 @@ def run_layer(b: LayerBuffers) -> None:
         norm.fused_add_rmsnorm(li.hidden, li.residual, li.norm_weight, s.eps)
     if s.norm_only:
         return
-    rope.apply_rope_with_cos_sin_cache_inplace(li.positions, li.q, li.k, s.head_dim, li.table, True)
-    page.append_paged_kv_cache(b.k3, b.v3, li.batch_indices, li.positions, (li.k_cache, li.v_cache), b.kv_indices,
-                               li.kv_indptr, None, "NHD")
+    if b.fuse_rope_kv:
+        fused.apply_rope_and_append_paged_kv_cache(li.positions, li.q, li.k, b.v3, s.head_dim, li.table, True,
+                                                   li.batch_indices, (li.k_cache, li.v_cache), b.kv_indices,
+                                                   li.kv_indptr, None, "NHD")
+    else:
+        rope.apply_rope_with_cos_sin_cache_inplace(li.positions, li.q, li.k, s.head_dim, li.table, True)
+        page.append_paged_kv_cache(b.k3, b.v3, li.batch_indices, li.positions, (li.k_cache, li.v_cache),
+                                   b.kv_indices, li.kv_indptr, None, "NHD")
     if b.fp8_norms:
         norm.fused_add_rmsnorm_quant(b.norm_out, li.attn_out, li.residual, li.post_norm_weight, b.act_scale, s.eps)
     else:
@@ -67,7 +75,8 @@ class DecodePass:
     ``[layers, pages, page_size, kv_heads, head_dim]`` (model_runner.py:83-85).
     """
 
-    def __init__(self, shape: Shape, device: torch.device, seed: int = 0, fp8_norms: bool = False):
+    def __init__(self, shape: Shape, device: torch.device, seed: int = 0, fp8_norms: bool = False,
+                 fuse_rope_kv: bool = False):
         self.shape = shape
         self.device = device
         table = rope.cos_sin_cache(shape.max_position, shape.head_dim, shape.theta).to(device)
@@ -80,7 +89,7 @@ class DecodePass:
                 residual.zero_()          # devstral2.py:302: the stream starts at zero
             else:
                 li.residual = residual
-            self.layers.append(LayerBuffers(li, fp8_norms))
+            self.layers.append(LayerBuffers(li, fp8_norms, fuse_rope_kv=fuse_rope_kv))
         gen = torch.Generator(device=device).manual_seed(seed)
         self.embed_table = torch.randn(shape.vocab, shape.hidden, generator=gen, device=device).to(torch.bfloat16)
         cpu = torch.Generator().manual_seed(seed)
@@ -93,4 +102,6 @@ class DecodePass:
             run_layer(b)
 
     def credited_bytes(self) -> int:
-        return credited_bytes(self.shape)["embedding"] + self.shape.layers * layer_credited_bytes(self.shape)
+        fused_rope_kv = self.layers[0].fuse_rope_kv
+        return credited_bytes(self.shape)["embedding"] + self.shape.layers * layer_credited_bytes(self.shape,
+                                                                                                   fused_rope_kv)

@@ -120,10 +120,11 @@ def _indices(shape: Shape, gen: torch.Generator):
 
 def make_layer_inputs(shape: Shape | str, device: torch.device | str = "cpu", seed: int = 0,
                       with_cache: bool = True, fill_on_device: bool = False,
-                      table: torch.Tensor | None = None) -> LayerInputs:
+                      table: torch.Tensor | None = None, zero_cache: bool = True) -> LayerInputs:
     """One layer's inputs. ``fill_on_device`` draws the big tensors with the device's generator
     (fast for the prefill shapes); otherwise everything is drawn on the CPU and copied, so the
-    oracle can see the same values."""
+    oracle can see the same values. ``zero_cache=False`` leaves the KV cache uninitialised (timing
+    runs, where only the slots a step writes matter)."""
     if isinstance(shape, str):
         shape = SHAPES[shape]
     device = torch.device(device)
@@ -152,18 +153,20 @@ def make_layer_inputs(shape: Shape | str, device: torch.device | str = "cpu", se
                          batch.to(device), tables.to(device), indptr.to(device), slots.to(device), table.to(device))
     if with_cache:
         cache_shape = (shape.num_pages, shape.page_size, shape.kv_heads, shape.head_dim)
-        inputs.k_cache = torch.zeros(cache_shape, dtype=torch.bfloat16, device=device)
-        inputs.v_cache = torch.zeros(cache_shape, dtype=torch.bfloat16, device=device)
+        alloc = torch.zeros if zero_cache else torch.empty
+        inputs.k_cache = alloc(cache_shape, dtype=torch.bfloat16, device=device)
+        inputs.v_cache = alloc(cache_shape, dtype=torch.bfloat16, device=device)
     return inputs
 
 
-def layer_credited_bytes(shape: Shape) -> int:
-    """One decoder layer's five kernels: two norms (bf16 outputs), SiluAndMul, RoPE, KV store
-    (one norm for a norm-only shape)."""
+def layer_credited_bytes(shape: Shape, fused_rope_kv: bool = False) -> int:
+    """One decoder layer's kernels: two norms (bf16 outputs), SiluAndMul, RoPE, KV store (one norm
+    for a norm-only shape). With RoPE and the store fused, k is read once: 2·N·Hk·D bytes fewer."""
     b = credited_bytes(shape)
     if shape.norm_only:
         return b["fused_add_rmsnorm"]
-    return 2 * b["fused_add_rmsnorm"] + b["silu_and_mul"] + b["rope"] + b["append_paged_kv_cache"]
+    rope_kv = b["rope_append"] if fused_rope_kv else b["rope"] + b["append_paged_kv_cache"]
+    return 2 * b["fused_add_rmsnorm"] + b["silu_and_mul"] + rope_kv
 
 
 def credited_bytes(shape: Shape) -> dict[str, int]:
@@ -179,5 +182,7 @@ def credited_bytes(shape: Shape) -> dict[str, int]:
         "silu_and_mul": 6 * n * i,
         "rope": 4 * n * heads * d + 4 * n,
         "append_paged_kv_cache": 8 * n * shape.kv_heads * d + 8 * n,
+        # fused RoPE + KV append: q, k read and written; v read; k and v written to the cache
+        "rope_append": 4 * n * heads * d + 4 * n + 6 * n * shape.kv_heads * d + 4 * n,
         "embedding": 4 * n * h + 8 * n,
     }

@@ -395,3 +395,81 @@ def test_kernels_reproduce_golden_fixtures(mas, dev):
 
     out = mas.embedding.embedding(torch.from_numpy(gd["emb_ids"]).to(dev), dev_bf16("emb_table"))
     assert np.array_equal(bits(out), gd["emb_out"])
+
+
+# ---- fused RoPE + paged KV append ------------------------------------------------------------------
+
+@pytest.mark.parametrize("neox", [True, False])
+@pytest.mark.parametrize("n,hq,hk,d,page_size", [(1, 32, 8, 128, 256), (64, 32, 8, 128, 256), (300, 32, 8, 128, 16),
+                                                  (37, 96, 8, 128, 256), (9, 4, 2, 64, 4), (5, 2, 1, 256, 8),
+                                                  (3, 0, 2, 128, 16)])
+def test_rope_append_fused_matches_separate_calls(mas, dev, neox, n, hq, hk, d, page_size):
+    g = torch.Generator().manual_seed(n * 31 + hq + d)
+    lens = [n // 2, n - n // 2] if n > 1 else [1]
+    lens = [x for x in lens if x > 0]
+    width = -(-max(lens) // page_size) + 1
+    pages = len(lens) * width + 2
+    tables, indptr, bidx, pos = _kv_case(g, pages, page_size, hk, d, lens, width)
+    pos = pos + 3                                          # not starting at 0
+    table = mas.rope.cos_sin_cache(max(pos.tolist()) + 5, d, 1e6)
+    qkv = _randn_bf16(g, n, (hq + 2 * hk) * d)
+    k0 = torch.randn(pages, page_size, hk, d, generator=g).bfloat16()
+    v0 = torch.randn(pages, page_size, hk, d, generator=g).bfloat16()
+    args = (pos.to(dev), bidx.to(dev), tables.flatten().to(dev), indptr.to(dev), table.to(dev))
+
+    def run(fused: bool):
+        buf = qkv.to(dev)
+        q, k, v = buf.split([hq * d, hk * d, hk * d], dim=-1)
+        kc, vc = k0.to(dev), v0.to(dev)
+        p, b, ind, ptr_, tab = args
+        if fused:
+            mas.apply_rope_and_append_paged_kv_cache(p, q, k, v.view(n, hk, d), d, tab, neox, b, (kc, vc), ind, ptr_)
+        else:
+            mas.apply_rope_with_cos_sin_cache_inplace(p, q, k, d, tab, neox)
+            mas.append_paged_kv_cache(k.view(n, hk, d), v.view(n, hk, d), b, p, (kc, vc), ind, ptr_)
+        return buf, kc, vc
+
+    fb, fk, fv = run(True)
+    sb, sk, sv = run(False)
+    assert torch.equal(fb, sb) and torch.equal(fk, sk) and torch.equal(fv, sv)
+    # and against the oracle
+    q_bits = bits(qkv[:, : hq * d]).reshape(n, hq, d)
+    k_bits = bits(qkv[:, hq * d:(hq + hk) * d]).reshape(n, hk, d)
+    want_q, want_k = ops.rope(q_bits, k_bits, pos.numpy(), table.numpy(), is_neox=neox)
+    want_kc, want_vc = ops.append_paged_kv_cache(bits(k0), bits(v0), want_k,
+                                                 bits(qkv[:, (hq + hk) * d:]).reshape(n, hk, d), bidx.numpy(),
+                                                 pos.numpy(), tables.flatten().numpy(), indptr.numpy())
+    assert np.array_equal(bits(fb[:, : hq * d]).reshape(n, hq, d), want_q)
+    assert np.array_equal(bits(fk), want_kc) and np.array_equal(bits(fv), want_vc)
+
+
+def test_rope_append_fused_error_paths(mas, dev):
+    g = torch.Generator().manual_seed(97)
+    n, hq, hk, d, ps = 6, 4, 2, 64, 4
+    tables = torch.tensor([[0, 1], [2, 3]], dtype=torch.int32)
+    indptr = torch.tensor([0, 2, 4], dtype=torch.int32)
+    bidx = torch.tensor([0, 0, 1, 1, 7, 1], dtype=torch.int32)
+    pos = torch.tensor([1, 5, 30, 2, 0, 3], dtype=torch.int32)      # 30: past the table and the pages
+    table = mas.rope.cos_sin_cache(16, d, 1e4)
+    qkv = _randn_bf16(g, n, (hq + 2 * hk) * d)
+    buf = qkv.to(dev)
+    q, k, v = buf.split([hq * d, hk * d, hk * d], dim=-1)
+    kc = torch.zeros(4, ps, hk, d, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    mas.apply_rope_and_append_paged_kv_cache(pos.to(dev), q, k, v.view(n, hk, d), d, table.to(dev), True,
+                                             bidx.to(dev), (kc, vc), tables.flatten().to(dev), indptr.to(dev),
+                                             error_flags=flags)
+    assert int(flags.item()) == 2 | 4 | 8
+    ok_rope = (pos < 16).numpy()
+    want_q, want_k = ops.rope(bits(qkv[:, :hq * d]).reshape(n, hq, d)[ok_rope],
+                              bits(qkv[:, hq * d:(hq + hk) * d]).reshape(n, hk, d)[ok_rope], pos.numpy()[ok_rope],
+                              table.numpy())
+    assert np.array_equal(bits(q).reshape(n, hq, d)[ok_rope], want_q)
+    assert np.array_equal(bits(q).reshape(n, hq, d)[~ok_rope], bits(qkv[:, :hq * d]).reshape(n, hq, d)[~ok_rope])
+    # tokens 0, 1, 3, 5 land in the cache; token 2 (page slot past its sequence) and 4 (batch 7) do not
+    kb = bits(kc)
+    k_rot = bits(k).reshape(n, hk, d)
+    for t, (page, entry) in {0: (0, 1), 1: (1, 1), 3: (2, 2), 5: (2, 3)}.items():
+        assert np.array_equal(kb[page, entry], k_rot[t])
+    assert int((kc != 0).any(dim=-1).any(dim=-1).sum()) == 4
