@@ -39,7 +39,6 @@ import __graft_entry__  # noqa: E402
 METRIC = "HBM GB/s & % of peak for layer kernels; µs/layer at 64-token decode"
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 COLD_BYTES = 768 << 20         # working set cycled by the cold protocol (3x the Infinity Cache)
-OPS = ("fused_add_rmsnorm", "rope", "append_paged_kv_cache", "silu_and_mul")
 # HBM bytes per launch of a workload's dominant kernel, from two rocprofv3 counter passes
 # (FETCH_SIZE, then WRITE_SIZE) over `bench.py --pmc-probe`, each calibrated by the same counter on
 # a 256 MiB device copy (fetch factor 1.9997, write factor 1.0000). Re-measure when the kernel changes.
@@ -55,7 +54,9 @@ def parse_args():
     p.add_argument("--protocol", choices=("cold", "hot"), default="cold")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU time of the baseline sample")
-    p.add_argument("--fp8-norms", action="store_true", help="use the fp8-output norm (the reference's in-layer variant)")
+    p.add_argument("--fp8", action="store_true",
+                   help="the reference's FP8 dataflow: norms write fp8 for the qkv / gate_up GEMMs and SiluAndMul "
+                        "writes the quantized down_proj input")
     p.add_argument("--pmc-probe", action="store_true",
                    help="short run for rocprofv3 --pmc: the dominant kernel 20 times on the cold layer sets, "
                         "then a 256 MiB device copy (the calibration reference for FETCH_SIZE / WRITE_SIZE)")
@@ -69,6 +70,15 @@ def footprint_bytes(shape) -> int:
     """Bytes one layer set's kernels touch (inputs + outputs + destination cache rows)."""
     n, h, i = shape.tokens, shape.hidden, shape.inter
     return 2 * (4 * n * h + 3 * n * i + n * shape.qkv_width) + 4 * n * shape.kv_heads * shape.head_dim
+
+
+def step_ops(shape, fp8: bool) -> tuple[str, ...]:
+    """The kernels timed one by one: norm, RoPE, KV store, SiluAndMul (the dominant kernel), and the
+    fused RoPE + KV kernel; their fp8-output forms under the fp8 dataflow."""
+    norm = "fused_add_rmsnorm_quant" if fp8 else "fused_add_rmsnorm"
+    if shape.norm_only:
+        return (norm,)
+    return (norm, "rope", "append_paged_kv_cache", "silu_and_mul_quant" if fp8 else "silu_and_mul", "rope_append")
 
 
 def op_launcher(mas, b, op):
@@ -85,6 +95,11 @@ def op_launcher(mas, b, op):
                                                       "NHD")
     if op == "silu_and_mul":
         return lambda: mas.activation.silu_and_mul(li.gate_up, out=b.silu_out)
+    if op == "silu_and_mul_quant":
+        return lambda: mas.activation.silu_and_mul_quant(li.gate_up, b.act_scale, out=b.silu_out)
+    if op == "fused_add_rmsnorm_quant":
+        return lambda: mas.norm.fused_add_rmsnorm_quant(b.norm_out, li.hidden, li.residual, li.norm_weight,
+                                                        b.act_scale, s.eps)
     if op == "rope_append":
         return lambda: mas.fused.apply_rope_and_append_paged_kv_cache(
             li.positions, li.q, li.k, b.v3, s.head_dim, li.table, True, li.batch_indices, (li.k_cache, li.v_cache),
@@ -92,7 +107,7 @@ def op_launcher(mas, b, op):
     raise ValueError(op)
 
 
-def time_ops(mas, layer_sets, launches: int, ops=OPS) -> dict[str, float]:
+def time_ops(mas, layer_sets, launches: int, ops: tuple[str, ...]) -> dict[str, float]:
     """Average launch duration (µs) of each kernel: a HIP graph of ``launches`` back-to-back launches
     of that kernel alone, cycling the layer sets, bracketed by two HIP events on the stream the
     graph replays on."""
@@ -144,7 +159,7 @@ def capture(fn) -> torch.cuda.CUDAGraph:
     return g
 
 
-def cpu_baseline_layer(shape, seconds: float, fp8_norms: bool) -> dict:
+def cpu_baseline_layer(shape, seconds: float, fp8: bool) -> dict:
     """The oracle's five layer ops on a bounded sample of the workload, timed on the host."""
     from oracle import ops as oops
 
@@ -179,7 +194,7 @@ def cpu_baseline_layer(shape, seconds: float, fp8_norms: bool) -> dict:
 
     def layer():
         nonlocal x, r, kc, vc
-        if fp8_norms:
+        if fp8:
             _, r = oops.fused_add_rmsnorm_quant(x, r, w, 0.05, shape.eps)
         else:
             _, r = oops.fused_add_rmsnorm(x, r, w, shape.eps)
@@ -187,16 +202,15 @@ def cpu_baseline_layer(shape, seconds: float, fp8_norms: bool) -> dict:
             return
         oops.rope(q, k, pos, table)
         kc, vc = oops.store_kv_slots(kc, vc, k, v, local_slots)
-        if fp8_norms:
+        if fp8:
             _, r = oops.fused_add_rmsnorm_quant(a, r, w2, 0.05, shape.eps)
+            oops.silu_and_mul_quant(gu, 0.05)
         else:
             _, r = oops.fused_add_rmsnorm(a, r, w2, shape.eps)
-        oops.silu_and_mul(gu)
+            oops.silu_and_mul(gu)
 
     sample_shape = type(shape)(**{**shape.__dict__, "tokens": tokens})
-    per_layer = wl.layer_credited_bytes(sample_shape)     # the oracle runs RoPE and the store separately
-    if fp8_norms:
-        per_layer -= 2 * tokens * shape.hidden
+    per_layer = wl.layer_credited_bytes(sample_shape, False, fp8)   # the oracle runs RoPE and the store separately
     layer()                                  # warm-up
     reps, t0 = 0, time.perf_counter()
     while True:
@@ -216,11 +230,9 @@ def run_layer_workload(mas, args, shape, dev) -> dict:
     table = mas.rope.cos_sin_cache(shape.max_position, shape.head_dim, shape.theta).to(dev)
     sets = [lp.LayerBuffers(wl.make_layer_inputs(shape, dev, seed=i, fill_on_device=True, table=table,
                                                      zero_cache=False),
-                            fp8_norms=args.fp8_norms, fuse_rope_kv=not args.separate_rope_kv) for i in range(n_sets)]
+                            fp8=args.fp8, fuse_rope_kv=not args.separate_rope_kv) for i in range(n_sets)]
     fused = not args.separate_rope_kv
-    per_step = wl.layer_credited_bytes(shape, fused)
-    if args.fp8_norms:
-        per_step -= 2 * shape.tokens * shape.hidden
+    per_step = wl.layer_credited_bytes(shape, fused, args.fp8)
     steps = args.steps if args.steps is not None else (2000 if shape.decode else 40)
     warmup = args.warmup if args.warmup is not None else max(n_sets, steps // 10)
 
@@ -270,13 +282,12 @@ def run_layer_workload(mas, args, shape, dev) -> dict:
     stream_us = (time.perf_counter() - s0) / stream_steps * 1e6
 
     launches = max(2 * n_sets, 100) if shape.decode else 4 * n_sets
-    timed = ("fused_add_rmsnorm",) if shape.norm_only else OPS + ("rope_append",)
-    op_us = time_ops(mas, sets, launches, timed)
+    op_us = time_ops(mas, sets, launches, step_ops(shape, args.fp8))
     cb = wl.credited_bytes(shape)
     ops = {op: {"us": round(us, 3), "GB/s": round(cb[op] / us / 1e3, 1),
                 "frac": round(cb[op] / us / 1e3 / PEAK_HBM_GBS, 4)} for op, us in op_us.items()}
     ms_per_step = elapsed / steps * 1e3
-    dominant = "fused_add_rmsnorm" if shape.norm_only else "silu_and_mul"
+    dominant = step_ops(shape, args.fp8)[0 if shape.norm_only else 3]
     res = {"steps": steps, "warmup": warmup, "ms_per_step": ms_per_step, "per_step_bytes": per_step,
            "value": per_step / (ms_per_step * 1e-3) / 1e9, "stream_us_per_step": stream_us, "ops": ops,
            "sets": n_sets, "dominant": dominant, "dominant_bytes": cb[dominant], "dominant_us": op_us[dominant]}
@@ -287,10 +298,8 @@ def run_layer_workload(mas, args, shape, dev) -> dict:
 
 def run_pass_workload(mas, args, shape, dev) -> dict:
     lp, wl = mas.layer_pass, mas.workloads
-    passes = [lp.DecodePass(shape, dev, seed=0, fp8_norms=args.fp8_norms, fuse_rope_kv=not args.separate_rope_kv)]
+    passes = [lp.DecodePass(shape, dev, seed=0, fp8=args.fp8, fuse_rope_kv=not args.separate_rope_kv)]
     per_step = passes[0].credited_bytes()
-    if args.fp8_norms:
-        per_step -= 2 * shape.layers * shape.tokens * shape.hidden
     steps = args.steps if args.steps is not None else 20
     warmup = args.warmup if args.warmup is not None else 3
     g = capture(passes[0].run)
@@ -302,14 +311,16 @@ def run_pass_workload(mas, args, shape, dev) -> dict:
         g.replay()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    op_us = time_ops(mas, passes[0].layers, shape.layers, OPS + ("rope_append",))
+    ops_timed = step_ops(shape, args.fp8)
+    op_us = time_ops(mas, passes[0].layers, shape.layers, ops_timed)
     cb = wl.credited_bytes(shape)
     ops = {op: {"us": round(us, 3), "GB/s": round(cb[op] / us / 1e3, 1),
                 "frac": round(cb[op] / us / 1e3 / PEAK_HBM_GBS, 4)} for op, us in op_us.items()}
     ms_per_step = elapsed / steps * 1e3
+    dominant = ops_timed[3]
     return {"steps": steps, "warmup": warmup, "ms_per_step": ms_per_step, "per_step_bytes": per_step,
-            "value": per_step / (ms_per_step * 1e-3) / 1e9, "ops": ops, "sets": 1, "dominant": "silu_and_mul",
-            "dominant_bytes": cb["silu_and_mul"], "dominant_us": op_us["silu_and_mul"],
+            "value": per_step / (ms_per_step * 1e-3) / 1e9, "ops": ops, "sets": 1, "dominant": dominant,
+            "dominant_bytes": cb[dominant], "dominant_us": op_us[dominant],
             "us_per_layer": ms_per_step * 1e3 / shape.layers}
 
 
@@ -321,7 +332,7 @@ def pmc_probe(mas, args, shape, dev) -> None:
     table = mas.rope.cos_sin_cache(shape.max_position, shape.head_dim, shape.theta).to(dev)
     sets = [lp.LayerBuffers(wl.make_layer_inputs(shape, dev, seed=i, fill_on_device=True, table=table,
                                                  zero_cache=False)) for i in range(n_sets)]
-    op = "fused_add_rmsnorm" if shape.norm_only else "silu_and_mul"
+    op = step_ops(shape, False)[0 if shape.norm_only else 3]
     for i in range(20):
         op_launcher(mas, sets[i % n_sets], op)()
     torch.cuda.synchronize()
@@ -376,7 +387,7 @@ def main() -> int:
                    "intermediate": shape.inter, "q_heads": shape.q_heads, "kv_heads": shape.kv_heads,
                    "head_dim": shape.head_dim, "kv_pages": shape.num_pages, "page_size": shape.page_size,
                    "layers": shape.layers, "protocol": args.protocol, "layer_sets": res["sets"],
-                   "launch": "hip-graph", "norm_output": "fp8" if args.fp8_norms else "bf16",
+                   "launch": "hip-graph", "dataflow": "fp8" if args.fp8 else "bf16",
                    "rope_kv": "separate" if args.separate_rope_kv else "fused"},
         "us_per_layer": round(res.get("us_per_layer", res["ms_per_step"] * 1e3), 3),
         "frac_of_peak": round(res["value"] / PEAK_HBM_GBS, 4),
@@ -392,7 +403,7 @@ def main() -> int:
             line[key] = round(res[key], 3)
     line["copy_ceiling_GBps"] = round(copy_ceiling_gbs(dev), 1)
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline_layer(shape, args.cpu_seconds, args.fp8_norms)
+        line["cpu_baseline"] = cpu_baseline_layer(shape, args.cpu_seconds, args.fp8)
     print(json.dumps(line), flush=True)
     return 0
 

@@ -84,6 +84,18 @@ int mas_silu_and_mul_bf16(void* out, int64_t out_stride, const void* input, int6
                           int64_t rows, int64_t inter, hipStream_t stream);
 
 /*
+ * SiluAndMul with the per-tensor fp8 quantize of its result fused in:
+ *   y = bf16(silu(f32(in[r, i])) * f32(in[r, inter + i]))            (the unfused op's output)
+ *   out[r, i] = e4m3fn(clamp(f32(y) / scale, -448, 448))             (NaN stays NaN)
+ * `scale` is read from `scale_dev` when it is non-NULL, else `scale_host` is used. out: bytes.
+ * Replaces the silu_and_mul call at miniagentserve/models/devstral2/devstral2.py:224 together with
+ * the quantize_fp8 that down_proj applies to its result (devstral2.py:93-95,110-111).
+ */
+int mas_silu_and_mul_quant_fp8(void* out, int64_t out_stride, const void* input, int64_t input_stride,
+                               int64_t rows, int64_t inter, const float* scale_dev, float scale_host,
+                               hipStream_t stream);
+
+/*
  * Rotary embedding in place from a cos/sin table, applied to q and k heads.
  * q: rows x num_q_heads heads; head h of row t starts at q + t*q_stride + h*q_head_stride
  * (k likewise). table: fp32 [table_rows, rotary_dim] with row stride `table_stride`; the first

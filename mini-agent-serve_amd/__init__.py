@@ -5,6 +5,7 @@ Drop-ins for the calls the reference's layer modules make
 
 - ``norm.fused_add_rmsnorm`` / ``norm.fused_add_rmsnorm_quant``   (flashinfer.norm, :241-252, :305-307)
 - ``activation.silu_and_mul``                                       (flashinfer.activation, :224)
+- ``activation.silu_and_mul_quant``                                 (:224 with down_proj's fp8 quantize, :93-95)
 - ``rope.apply_rope_with_cos_sin_cache_inplace``                    (flashinfer.rope, :163-166)
 - ``page.append_paged_kv_cache`` (+ ``page.store_kv_slots``)        (flashinfer.page, :170-173)
 - ``embedding.embedding`` / ``embedding.Embedding``                 (nn.Embedding, :260, :282)
@@ -22,7 +23,7 @@ from __future__ import annotations
 from . import _lib, activation, embedding, fused, norm, page, rope, workloads
 from . import layer_pass
 from . import _ops  # noqa: F401  (registers the torch.library ops)
-from .activation import silu_and_mul
+from .activation import silu_and_mul, silu_and_mul_quant
 from .embedding import Embedding
 from .fused import apply_rope_and_append_paged_kv_cache
 from .norm import fused_add_rmsnorm, fused_add_rmsnorm_quant
@@ -32,7 +33,7 @@ from .rope import apply_rope_with_cos_sin_cache_inplace
 __all__ = [
     "activation", "embedding", "fused", "norm", "page", "rope", "workloads", "layer_pass",
     "apply_rope_and_append_paged_kv_cache",
-    "silu_and_mul", "Embedding", "fused_add_rmsnorm", "fused_add_rmsnorm_quant", "append_paged_kv_cache",
+    "silu_and_mul", "silu_and_mul_quant", "Embedding", "fused_add_rmsnorm", "fused_add_rmsnorm_quant", "append_paged_kv_cache",
     "store_kv_slots", "apply_rope_with_cos_sin_cache_inplace", "load_library", "library_version",
 ]
 

@@ -28,6 +28,7 @@ _SIGNATURES: dict[str, list] = {
     "mas_fused_add_rmsnorm_quant_fp8": [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p,
                                         _f32, _i64, _i64, _f32, _c_void_p],
     "mas_silu_and_mul_bf16": [_c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _c_void_p],
+    "mas_silu_and_mul_quant_fp8": [_c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _c_void_p, _f32, _c_void_p],
     "mas_rope_cos_sin_cache_bf16": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _i64, _i64, _c_void_p, _i32,
                                     _c_void_p, _i64, _i64, _i64, _i64, _i64, _i32, _c_void_p, _c_void_p],
     "mas_append_paged_kv_cache_bf16": [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _c_void_p, _i64, _i64,

@@ -128,3 +128,23 @@ def _rope_append(positions: Tensor, query: Tensor, key: Tensor, value: Tensor, h
 def _(positions, query, key, value, head_size, cos_sin_cache, is_neox, batch_indices, k_cache, v_cache, kv_indices,
       kv_indptr, kv_layout):
     return None
+
+
+@custom_op("mas::silu_and_mul_quant", mutates_args=("out",))
+def _silu_and_mul_quant(input: Tensor, out: Tensor, scale: Tensor) -> None:
+    activation._silu_and_mul_quant(input, out, scale)
+
+
+@_silu_and_mul_quant.register_fake
+def _(input, out, scale):
+    return None
+
+
+@custom_op("mas::silu_and_mul_quant_hs", mutates_args=("out",))
+def _silu_and_mul_quant_hs(input: Tensor, out: Tensor, scale: float) -> None:
+    activation._silu_and_mul_quant(input, out, scale)
+
+
+@_silu_and_mul_quant_hs.register_fake
+def _(input, out, scale):
+    return None

@@ -8,16 +8,26 @@
 //                     page = slot / page_size, entry = slot % page_size
 //   k_cache[page, entry, h, :] = key[t, h, :];  v_cache[page, entry, h, :] = value[t, h, :]
 //
-// A bit copy: one wavefront per token, its destination resolved once per wavefront from
-// wave-uniform (scalar-cache) index loads issued after the token's k/v loads, so both latencies
-// overlap; each lane moves 16-byte vectors of k and v, all loads issued before the stores. Duplicate destinations (padding rows aimed at the
-// model runner's sink block) are plain racing stores of whole rows: one writer wins.
+// A bit copy: one wavefront per (token, tensor), its destination resolved once per wavefront from
+// wave-uniform (scalar-cache) index loads issued after the row's loads, so both latencies overlap;
+// each lane moves 16-byte vectors, all loads issued before the stores.
+// Duplicate destinations (padding rows aimed at the model runner's sink block) are plain racing
+// stores of whole rows: one writer wins.
 #include "device.h"
 
 namespace mas {
 namespace {
 
-constexpr int kBlock = 256;
+// One wavefront per workgroup and per (token, tensor): measured best on MI355X at every size, from
+// the 64-token decode (2.17 us) to 16384 prefill tokens (ahead of 128/256/512-thread workgroups and
+// of one wavefront moving both of a token's rows). Both are overridable for experiments.
+#ifndef MAS_KV_BLOCK
+#define MAS_KV_BLOCK 64
+#endif
+#ifndef MAS_KV_SPLIT
+#define MAS_KV_SPLIT 2
+#endif
+constexpr int kBlock = MAS_KV_BLOCK;
 constexpr int kWavesPerBlock = kBlock / kWave;
 constexpr int kUnroll = 2;
 
@@ -95,11 +105,14 @@ __device__ __forceinline__ int64_t vec_offset(int v, int vec_per_head, int64_t h
 
 // The source rows are loaded before the destination is resolved: the k/v loads do not depend on
 // it, so the index loads (scalar cache) and the data loads are in flight together.
-template <bool kSlotForm, bool kContig>
+// kSplit: 1 = one wavefront moves a token's k and v rows; 2 = one wavefront per (token, tensor).
+template <bool kSlotForm, bool kContig, int kSplit>
 __global__ __launch_bounds__(kBlock) void kv_store(KvArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_id_uniform();
+  const int64_t w = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_id_uniform();
+  const int64_t t = w / kSplit;
   if (t >= a.rows) return;
+  const int half = static_cast<int>(w - t * kSplit);  // kSplit == 2: 0 moves k, 1 moves v
   const uint16_t* ksrc = a.key + t * a.key_stride;
   const uint16_t* vsrc = a.value + t * a.value_stride;
   const int nv = a.vec_per_row;
@@ -111,8 +124,13 @@ __global__ __launch_bounds__(kBlock) void kv_store(KvArgs a) {
     for (int j = 0; j < kUnroll; ++j) {
       const int v = c * kWave * kUnroll + j * kWave + lane;
       const int vl = v < nv ? v : nv - 1;
-      kv[j] = load_stream(ksrc + vec_offset(vl, a.vec_per_head, a.key_head_stride, kContig));
-      vv[j] = load_stream(vsrc + vec_offset(vl, a.vec_per_head, a.value_head_stride, kContig));
+      if constexpr (kSplit == 1) {
+        kv[j] = load_stream(ksrc + vec_offset(vl, a.vec_per_head, a.key_head_stride, kContig));
+        vv[j] = load_stream(vsrc + vec_offset(vl, a.vec_per_head, a.value_head_stride, kContig));
+      } else {
+        kv[j] = half == 0 ? load_stream(ksrc + vec_offset(vl, a.vec_per_head, a.key_head_stride, kContig))
+                          : load_stream(vsrc + vec_offset(vl, a.vec_per_head, a.value_head_stride, kContig));
+      }
     }
     load_fence();
     if (c == 0) {
@@ -125,8 +143,12 @@ __global__ __launch_bounds__(kBlock) void kv_store(KvArgs a) {
       const int v = c * kWave * kUnroll + j * kWave + lane;
       if (v < nv) {
         const int64_t off = dst_row + vec_offset(v, a.vec_per_head, a.head_stride, kContig);
-        store_stream(a.k_cache + off, kv[j]);
-        store_stream(a.v_cache + off, vv[j]);
+        if constexpr (kSplit == 1) {
+          store_stream(a.k_cache + off, kv[j]);
+          store_stream(a.v_cache + off, vv[j]);
+        } else {
+          store_stream((half == 0 ? a.k_cache : a.v_cache) + off, kv[j]);
+        }
       }
     }
   }
@@ -152,14 +174,17 @@ int check_common(const KvArgs& a, int64_t num_heads, int64_t head_dim, bool* emp
 // q/k/v column views) are one contiguous run at both ends: no per-vector head arithmetic.
 template <bool kSlotForm>
 int launch(const KvArgs& a, hipStream_t s) {
+  constexpr int kSplit = MAS_KV_SPLIT;
   const int64_t head_dim = 8 * static_cast<int64_t>(a.vec_per_head);
   const bool contiguous = a.key_head_stride == head_dim && a.value_head_stride == head_dim && a.head_stride == head_dim;
-  const int64_t blocks = cdiv(a.rows, kWavesPerBlock);
+  const int64_t blocks = cdiv(a.rows * kSplit, kWavesPerBlock);
   if (blocks > INT32_MAX) return MAS_ERR_UNSUPPORTED;
   if (contiguous)
-    hipLaunchKernelGGL((kv_store<kSlotForm, true>), dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL((kv_store<kSlotForm, true, kSplit>), dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, s,
+                       a);
   else
-    hipLaunchKernelGGL((kv_store<kSlotForm, false>), dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL((kv_store<kSlotForm, false, kSplit>), dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, s,
+                       a);
   return launch_status();
 }
 

@@ -18,7 +18,10 @@
 namespace mas {
 namespace {
 
-constexpr int kBlock = 256;
+#ifndef MAS_ROPE_BLOCK
+#define MAS_ROPE_BLOCK 256
+#endif
+constexpr int kBlock = MAS_ROPE_BLOCK;  // threads per workgroup (64..512 measured equal on MI355X)
 constexpr int kWavesPerBlock = kBlock / kWave;
 
 struct RopeArgs {

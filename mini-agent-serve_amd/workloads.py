@@ -159,14 +159,17 @@ def make_layer_inputs(shape: Shape | str, device: torch.device | str = "cpu", se
     return inputs
 
 
-def layer_credited_bytes(shape: Shape, fused_rope_kv: bool = False) -> int:
-    """One decoder layer's kernels: two norms (bf16 outputs), SiluAndMul, RoPE, KV store (one norm
-    for a norm-only shape). With RoPE and the store fused, k is read once: 2·N·Hk·D bytes fewer."""
+def layer_credited_bytes(shape: Shape, fused_rope_kv: bool = False, fp8: bool = False) -> int:
+    """One decoder layer's kernels: two norms, SiluAndMul, RoPE, KV store (one norm for a norm-only
+    shape). With RoPE and the store fused, k is read once: 2·N·Hk·D bytes fewer. ``fp8``: the
+    reference's FP8 dataflow - norms write fp8 (7·N·H) and SiluAndMul writes the quantized down_proj
+    input (5·N·I)."""
     b = credited_bytes(shape)
+    norm = b["fused_add_rmsnorm_quant"] if fp8 else b["fused_add_rmsnorm"]
     if shape.norm_only:
-        return b["fused_add_rmsnorm"]
+        return norm
     rope_kv = b["rope_append"] if fused_rope_kv else b["rope"] + b["append_paged_kv_cache"]
-    return 2 * b["fused_add_rmsnorm"] + b["silu_and_mul"] + rope_kv
+    return 2 * norm + (b["silu_and_mul_quant"] if fp8 else b["silu_and_mul"]) + rope_kv
 
 
 def credited_bytes(shape: Shape) -> dict[str, int]:
@@ -180,6 +183,7 @@ def credited_bytes(shape: Shape) -> dict[str, int]:
         "fused_add_rmsnorm": 8 * n * h + 2 * h,
         "fused_add_rmsnorm_quant": 7 * n * h + 2 * h,
         "silu_and_mul": 6 * n * i,
+        "silu_and_mul_quant": 5 * n * i,
         "rope": 4 * n * heads * d + 4 * n,
         "append_paged_kv_cache": 8 * n * shape.kv_heads * d + 8 * n,
         # fused RoPE + KV append: q, k read and written; v read; k and v written to the cache

@@ -82,3 +82,27 @@ def test_torch_compile_matches_eager(mas, dev):
     got = compiled(x.clone(), r.clone(), gu)
     for a, b in zip(got, want):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_layer_pass_fused_and_separate_agree(mas, dev, fp8):
+    """One layer with RoPE + KV fused or as the reference's two calls: bit-identical results."""
+    wl, lp = mas.workloads, mas.layer_pass
+    outs = []
+    for fuse in (True, False):
+        li = wl.make_layer_inputs("decode64_24b", dev, seed=9)
+        b = lp.LayerBuffers(li, fp8=fp8, fuse_rope_kv=fuse)
+        lp.run_layer(b)
+        torch.cuda.synchronize()
+        tensors = [li.hidden, li.residual, li.attn_out, li.qkv, li.k_cache, li.v_cache, b.silu_out]
+        if fp8:
+            tensors.append(b.norm_out)
+        outs.append([t.view(torch.uint8) if t.dtype == torch.float8_e4m3fn else t for t in tensors])
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    if fp8:
+        # SiluAndMul's fp8 output is the quantize of its bf16 output
+        li = wl.make_layer_inputs("decode64_24b", dev, seed=9, with_cache=False)
+        y = mas.silu_and_mul(li.gate_up)
+        ref = (y.float() / 0.05).clamp(-448, 448).to(torch.float8_e4m3fn)
+        assert torch.equal(outs[0][6], ref.view(torch.uint8))

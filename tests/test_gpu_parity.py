@@ -133,6 +133,25 @@ def test_silu_and_mul_strided_input_and_out(mas, dev):
     _close_bf16(bits(out3), ops.silu_and_mul(bits(x3)), min_exact=0.98)
 
 
+@pytest.mark.parametrize("rows,inter", [(1, 8), (3, 100), (64, 32768), (129, 2048), (7, 1000)])
+@pytest.mark.parametrize("scale_kind", ["tensor", "float"])
+def test_silu_and_mul_quant(mas, dev, rows, inter, scale_kind):
+    g = torch.Generator().manual_seed(rows * 11 + inter)
+    x = _randn_bf16(g, rows, 2 * inter, scale=3.0)
+    scale = 0.004
+    s = torch.tensor(scale, dtype=torch.float32, device=dev) if scale_kind == "tensor" else scale
+    out = mas.silu_and_mul_quant(x.to(dev), s)
+    got = fp8_codes(out)
+    want = ops.silu_and_mul_quant(bits(x), scale)
+    gv, wv = on.fp8_to_f32(got), on.fp8_to_f32(want)
+    assert np.all(np.abs(gv - wv) <= np.maximum(np.abs(wv) * 2.0 ** -3, 2.0 ** -9))
+    assert np.mean(got == want) >= 0.99
+    # the fused op equals silu_and_mul followed by the reference's quantize of its bf16 output
+    y = mas.silu_and_mul(x.to(dev))
+    ref = (y.float() / scale).clamp(-448, 448).to(torch.float8_e4m3fn)
+    assert torch.equal(out.view(torch.uint8), ref.view(torch.uint8))
+
+
 # ---- rope -----------------------------------------------------------------------------------------
 
 def _rope_case(mas, dev, n, hq, hk, head_dim, rotary_dim, neox, pos_dtype, seed, max_pos=4096):

@@ -113,7 +113,8 @@ def test_fake_kernels_under_fake_tensor_mode(mas):
         torch.ops.mas.fused_add_rmsnorm(h, h.clone(), torch.empty(64, dtype=torch.bfloat16, device="cuda"), 1e-6)
     expected = {"fused_add_rmsnorm", "fused_add_rmsnorm_quant", "fused_add_rmsnorm_quant_hs", "silu_and_mul",
                 "silu_and_mul_out", "apply_rope_with_cos_sin_cache_inplace", "append_paged_kv_cache",
-                "store_kv_slots", "embedding"}
+                "store_kv_slots", "embedding", "silu_and_mul_quant", "silu_and_mul_quant_hs",
+                "apply_rope_and_append_paged_kv_cache"}
     assert expected <= {name for name in dir(torch.ops.mas) if not name.startswith("_")}
 
 

@@ -133,6 +133,23 @@ def test_silu_and_mul_limits():
     assert got[7] == on.round_bf16(np.array([1e30], np.float32))[0]
 
 
+def test_silu_and_mul_quant_matches_reference_quantize():
+    """The reference's down_proj quantize applied to the bf16 SiluAndMul output:
+    (y / scale).clamp(-448, 448).to(float8_e4m3fn), y = (F.silu(g) * u).bfloat16()."""
+    g = torch.Generator().manual_seed(15)
+    x = _randn_bf16(g, 48, 2 * 512, scale=3.0)
+    for scale in (0.004, 0.05, 1.0):
+        got = ops.silu_and_mul_quant(bits(x), scale)
+        y = (F.silu(x[:, :512].float()) * x[:, 512:].float()).bfloat16()
+        want = (y.float() / scale).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+        gv, wv = on.fp8_to_f32(got), on.fp8_to_f32(want)
+        # y may differ by one bf16 ulp (exp rounding), which moves fp8 by at most one step
+        assert np.all(np.abs(gv - wv) <= np.maximum(np.abs(wv) * 2.0 ** -3, 2.0 ** -9))
+        assert np.mean(got == want) > 0.995
+        if scale == 0.004:
+            assert np.any(np.abs(gv) == 448.0)
+
+
 # ---- RoPE -----------------------------------------------------------------------------------------
 
 def _hf_rope(q, k, positions, table):
