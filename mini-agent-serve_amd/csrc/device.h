@@ -63,22 +63,39 @@ __device__ __forceinline__ u32x4 pack8(const float* f) {
 }
 
 // ---- fp8 e4m3fn (OCP: bias 7, no infinities, max 448, NaN = S.1111.111) -------------------
-// Clamp to [-448, 448] then round to nearest even; NaN maps to 0x7f with the input's sign.
-// Written with integer arithmetic so the result does not depend on the hardware converter's
-// saturation mode.
-__device__ __forceinline__ uint32_t fp8e4m3_saturate_encode(float f) {
-  const uint32_t u = __float_as_uint(f);
-  const uint32_t sign = (u >> 24) & 0x80u;
-  uint32_t a = u & 0x7fffffffu;
-  if (a > 0x7f800000u) return sign | 0x7fu;
-  const float af = fminf(__uint_as_float(a), 448.0f);
-  a = __float_as_uint(af);
-  if (a >= 0x3c800000u) {  // |f| >= 2^-6: normal. Round the mantissa at bit 20, then rebias 127 -> 7.
-    const uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
-    return sign | ((r >> 20) - (120u << 3));
-  }
-  // Subnormal (or zero): the value is m * 2^-9 with m in [0, 8]; m = 8 encodes 2^-6 exactly.
-  return sign | static_cast<uint32_t>(__builtin_rintf(af * 512.0f));
+// Saturating encode of four fp32 values, code i in byte i: |v| > 448 -> +-448, otherwise round to
+// nearest even, NaN -> 0x7f with the input's sign. gfx950's v_cvt_pk_fp8_f32 does the rounding
+// (OCP e4m3 on this target) on inputs clamped beforehand; it writes 0xff for every NaN, so the
+// sign bits are put back with two byte permutes. Matches the integer-arithmetic encoder
+// (clamp, then RNE at mantissa bit 20, subnormals as m * 2^-9) on all 2^32 fp32 inputs.
+// IEEE 754-2019 maximum/minimum (v_maximum3_f32 / v_minimum3_f32 on gfx950): NaN passes through.
+__device__ __forceinline__ float fp8_clamp(float v) {
+  return __builtin_elementwise_minimum(__builtin_elementwise_maximum(v, -448.0f), 448.0f);
+}
+
+__device__ __forceinline__ uint32_t fp8x4_saturate_encode(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(fp8_clamp(a), fp8_clamp(b), 0, false);
+  const uint32_t codes =
+      static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(fp8_clamp(c), fp8_clamp(d), lo, true));
+  const uint32_t signs = __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x0c0c0703u) |
+                         __builtin_amdgcn_perm(__float_as_uint(d), __float_as_uint(c), 0x07030c0cu);
+  return codes & (signs | 0x7f7f7f7fu);
+}
+
+__device__ __forceinline__ uint32_t fp8_saturate_encode(float v) { return fp8x4_saturate_encode(v, v, v, v) & 0xffu; }
+
+// y / s rounded as IEEE division rounds it, from r = 1/s (one division per thread): q0 = y * r is
+// within an ulp of the quotient, the residual q0 * s - y is exact in one fma, and q0 minus the
+// residual times r rounds to the correctly rounded quotient (Markstein, IBM J. Res. Dev. 34(1),
+// 1990). Holds while the residual does not underflow, i.e. for every |y / s| >= 2^-100 - far
+// below fp8's smallest subnormal 2^-9. The residual is formed as q0 * s - y so that a zero
+// quotient keeps its sign (-0 - (+0) * r = -0). A non-finite q0 (y infinite or NaN, or overflow)
+// is returned as is.
+__device__ __forceinline__ float div_by_scale(float y, float s, float r) {
+  const float q0 = y * r;
+  const float e = __builtin_fmaf(q0, s, -y);
+  const float q1 = __builtin_fmaf(-e, r, q0);
+  return __builtin_isfinite(q0) ? q1 : q0;
 }
 
 // ---- wavefront / block reductions ----------------------------------------------------------

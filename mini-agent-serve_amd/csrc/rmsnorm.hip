@@ -76,6 +76,7 @@ __global__ __launch_bounds__(max_threads_for(VPT)) void fused_add_rmsnorm_tile(N
     }
     load_fence();
     const float scale = kFp8 ? norm_scale(a) : 1.0f;
+    const float rcp = 1.0f / scale;
 
     float s[VPT][8];
     float ss = 0.f;
@@ -113,9 +114,8 @@ __global__ __launch_bounds__(max_threads_for(VPT)) void fused_add_rmsnorm_tile(N
           u32x2 q;
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
-            q[h] = fp8e4m3_saturate_encode(y[4 * h] / scale) | (fp8e4m3_saturate_encode(y[4 * h + 1] / scale) << 8) |
-                   (fp8e4m3_saturate_encode(y[4 * h + 2] / scale) << 16) |
-                   (fp8e4m3_saturate_encode(y[4 * h + 3] / scale) << 24);
+            q[h] = fp8x4_saturate_encode(div_by_scale(y[4 * h], scale, rcp), div_by_scale(y[4 * h + 1], scale, rcp),
+                                         div_by_scale(y[4 * h + 2], scale, rcp), div_by_scale(y[4 * h + 3], scale, rcp));
           }
           store_stream(static_cast<uint8_t*>(a.out) + row * a.out_stride + 8 * v, q);
         } else {
@@ -149,7 +149,7 @@ __global__ __launch_bounds__(256) void fused_add_rmsnorm_generic(NormArgs a) {
       const float y = (s * rstd) * bf16_lo(w[i]);
       r[i] = static_cast<uint16_t>(pack_bf16x2(s, 0.f));
       if constexpr (kFp8) {
-        static_cast<uint8_t*>(a.out)[row * a.out_stride + i] = static_cast<uint8_t>(fp8e4m3_saturate_encode(y / scale));
+        static_cast<uint8_t*>(a.out)[row * a.out_stride + i] = static_cast<uint8_t>(fp8_saturate_encode(y / scale));
       } else {
         static_cast<uint16_t*>(a.out)[row * a.out_stride + i] = static_cast<uint16_t>(pack_bf16x2(y, 0.f));
       }

@@ -28,11 +28,10 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 template <int UNROLL>
 __global__ __launch_bounds__(kBlock) void silu_and_mul_vec(void* __restrict__ out, int64_t out_stride,
                                                            const void* __restrict__ in, int64_t in_stride,
-                                                           int64_t inter, int64_t tiles_per_row, int64_t ntiles) {
+                                                           int64_t rows, int64_t inter) {
   const int64_t nvec = inter >> 3;
-  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-    const int64_t row = tile / tiles_per_row;
-    const int64_t v0 = (tile - row * tiles_per_row) * (kBlock * UNROLL) + threadIdx.x;
+  const int64_t v0 = static_cast<int64_t>(blockIdx.x) * (kBlock * UNROLL) + threadIdx.x;
+  for (int64_t row = blockIdx.y; row < rows; row += gridDim.y) {
     const uint16_t* g = static_cast<const uint16_t*>(in) + row * in_stride;
     const uint16_t* u = g + inter;
     uint16_t* o = static_cast<uint16_t*>(out) + row * out_stride;
@@ -69,32 +68,32 @@ __global__ __launch_bounds__(kBlock) void silu_and_mul_vec(void* __restrict__ ou
 // the unfused 6 + 3.
 __global__ __launch_bounds__(kBlock) void silu_and_mul_quant_vec(void* __restrict__ out, int64_t out_stride,
                                                                  const void* __restrict__ in, int64_t in_stride,
-                                                                 int64_t inter, int64_t tiles_per_row, int64_t ntiles,
+                                                                 int64_t rows, int64_t inter,
                                                                  const float* __restrict__ scale_dev, float scale_host) {
   const int64_t nvec = inter >> 3;
-  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-    const int64_t row = tile / tiles_per_row;
-    const int64_t v = (tile - row * tiles_per_row) * kBlock + threadIdx.x;
+  const int64_t v = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  for (int64_t row = blockIdx.y; row < rows; row += gridDim.y) {
     const uint16_t* g = static_cast<const uint16_t*>(in) + row * in_stride;
     const int64_t vl = v < nvec ? v : nvec - 1;
     const u32x4 gv = load_stream(g + 8 * vl);
     const u32x4 uv = load_stream(g + inter + 8 * vl);
     load_fence();
     const float scale = scale_dev != nullptr ? *scale_dev : scale_host;
+    const float rcp = 1.0f / scale;
     if (v < nvec) {
       float gf[8], uf[8];
       unpack8(gv, gf);
       unpack8(uv, uf);
-      uint32_t code[8];
+      float qf[8];
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
         const uint32_t y2 = pack_bf16x2(silu_mul(gf[e], uf[e]), silu_mul(gf[e + 1], uf[e + 1]));
-        code[e] = fp8e4m3_saturate_encode(bf16_lo(y2) / scale);
-        code[e + 1] = fp8e4m3_saturate_encode(bf16_hi(y2) / scale);
+        qf[e] = div_by_scale(bf16_lo(y2), scale, rcp);
+        qf[e + 1] = div_by_scale(bf16_hi(y2), scale, rcp);
       }
       u32x2 q;
-      q[0] = code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24);
-      q[1] = code[4] | (code[5] << 8) | (code[6] << 16) | (code[7] << 24);
+      q[0] = fp8x4_saturate_encode(qf[0], qf[1], qf[2], qf[3]);
+      q[1] = fp8x4_saturate_encode(qf[4], qf[5], qf[6], qf[7]);
       store_stream(static_cast<uint8_t*>(out) + row * out_stride + 8 * v, q);
     }
   }
@@ -112,7 +111,7 @@ __global__ __launch_bounds__(kBlock) void silu_and_mul_quant_scalar(void* __rest
     const int64_t row = i / inter, col = i - row * inter;
     const uint16_t* g = static_cast<const uint16_t*>(in) + row * in_stride;
     const uint32_t y = pack_bf16x2(silu_mul(bf16_lo(g[col]), bf16_lo(g[inter + col])), 0.f);
-    static_cast<uint8_t*>(out)[row * out_stride + col] = static_cast<uint8_t>(fp8e4m3_saturate_encode(bf16_lo(y) / scale));
+    static_cast<uint8_t*>(out)[row * out_stride + col] = static_cast<uint8_t>(fp8_saturate_encode(bf16_lo(y) / scale));
   }
 }
 
@@ -129,15 +128,18 @@ __global__ __launch_bounds__(kBlock) void silu_and_mul_scalar(void* __restrict__
   }
 }
 
+// Grid of (tiles of one row) x (rows): the row comes from blockIdx.y, so no lane divides by the
+// tile count. Rows past the grid's y extent (65535) are covered by a uniform stride loop.
+dim3 row_tile_grid(int64_t tiles_per_row, int64_t rows) {
+  return dim3(static_cast<uint32_t>(tiles_per_row), static_cast<uint32_t>(rows < 65535 ? rows : 65535));
+}
+
 template <int UNROLL>
 int launch_vec(void* out, int64_t out_stride, const void* in, int64_t in_stride, int64_t rows, int64_t inter,
                int cus, hipStream_t s) {
-  const int64_t tiles_per_row = cdiv(inter / 8, kBlock * UNROLL);
-  const int64_t ntiles = rows * tiles_per_row;
-  const int64_t grid = ntiles < INT32_MAX ? ntiles : INT32_MAX;
   (void)cus;
-  hipLaunchKernelGGL((silu_and_mul_vec<UNROLL>), dim3(static_cast<uint32_t>(grid)), dim3(kBlock), 0, s, out,
-                     out_stride, in, in_stride, inter, tiles_per_row, ntiles);
+  hipLaunchKernelGGL((silu_and_mul_vec<UNROLL>), row_tile_grid(cdiv(inter / 8, kBlock * UNROLL), rows), dim3(kBlock),
+                     0, s, out, out_stride, in, in_stride, rows, inter);
   return launch_status();
 }
 
@@ -151,6 +153,7 @@ extern "C" int mas_silu_and_mul_bf16(void* out, int64_t out_stride, const void* 
   if (rows == 0 || inter == 0) return MAS_OK;
   if (out == nullptr || input == nullptr) return MAS_ERR_INVALID_VALUE;
   if (rows > 1 && (out_stride < inter || input_stride < 2 * inter)) return MAS_ERR_INVALID_VALUE;
+  if (inter > (int64_t{1} << 40)) return MAS_ERR_UNSUPPORTED;
   int cus = 0;
   if (const int st = device_cu_count(&cus); st != MAS_OK) return st;
   const bool vec_ok = inter % 8 == 0 && aligned16(out) && aligned16(input) && out_stride % 8 == 0 &&
@@ -184,6 +187,7 @@ extern "C" int mas_silu_and_mul_quant_fp8(void* out, int64_t out_stride, const v
   if (rows == 0 || inter == 0) return MAS_OK;
   if (out == nullptr || input == nullptr) return MAS_ERR_INVALID_VALUE;
   if (rows > 1 && (out_stride < inter || input_stride < 2 * inter)) return MAS_ERR_INVALID_VALUE;
+  if (inter > (int64_t{1} << 40)) return MAS_ERR_UNSUPPORTED;
   int cus = 0;
   if (const int st = device_cu_count(&cus); st != MAS_OK) return st;
   const bool vec_ok = inter % 8 == 0 && (reinterpret_cast<uintptr_t>(out) & 7u) == 0 && aligned16(input) &&
@@ -195,10 +199,7 @@ extern "C" int mas_silu_and_mul_quant_fp8(void* out, int64_t out_stride, const v
                        out_stride, input, input_stride, rows, inter, scale_dev, scale_host);
     return launch_status();
   }
-  const int64_t tiles_per_row = cdiv(inter / 8, kBlock);
-  const int64_t ntiles = rows * tiles_per_row;
-  const int64_t grid = ntiles < INT32_MAX ? ntiles : INT32_MAX;
-  hipLaunchKernelGGL(silu_and_mul_quant_vec, dim3(static_cast<uint32_t>(grid)), dim3(kBlock), 0, stream, out,
-                     out_stride, input, input_stride, inter, tiles_per_row, ntiles, scale_dev, scale_host);
+  hipLaunchKernelGGL(silu_and_mul_quant_vec, row_tile_grid(cdiv(inter / 8, kBlock), rows), dim3(kBlock), 0, stream,
+                     out, out_stride, input, input_stride, rows, inter, scale_dev, scale_host);
   return launch_status();
 }

@@ -152,6 +152,29 @@ def test_silu_and_mul_quant(mas, dev, rows, inter, scale_kind):
     assert torch.equal(out.view(torch.uint8), ref.view(torch.uint8))
 
 
+@pytest.mark.parametrize("scale_kind", ["tensor", "float"])
+def test_silu_and_mul_quant_every_bf16_value(mas, dev, scale_kind):
+    """The fp8 epilogue on every bf16 input. With gate = 32, e^-32 vanishes next to 1 in fp32, so
+    silu(32) = 32 exactly, y = 32 * u is exact in bf16 (or overflows to inf, which saturates just
+    as u does) and y / 32 = u. So the output must be the saturating e4m3fn encode of u for all 2^16
+    patterns: both zeros, subnormals, every rounding midpoint, values past 448 and infinities. A NaN
+    u must give a NaN code; its sign is not checked, since the sign of a NaN produced by
+    arithmetic (32 * u, then rounding to bf16) is unspecified."""
+    u_bits = np.arange(65536, dtype=np.uint16).reshape(64, 1024)
+    x_bits = np.concatenate([np.full_like(u_bits, 0x4200), u_bits], axis=1)   # 0x4200 = bf16 32.0
+    x = torch.from_numpy(x_bits.view(np.int16)).view(torch.bfloat16)
+    s = torch.tensor(32.0, dtype=torch.float32, device=dev) if scale_kind == "tensor" else 32.0
+    got = fp8_codes(mas.silu_and_mul_quant(x.to(dev), s))
+    want = on.f32_to_fp8_saturate(on.bf16_to_f32(u_bits))
+    nan = np.isnan(on.bf16_to_f32(u_bits))
+    with np.errstate(over="ignore", invalid="ignore"):
+        oracle = ops.silu_and_mul_quant(x_bits, 32.0)
+    assert np.array_equal(oracle[~nan], want[~nan]) and np.all(oracle[nan] & 0x7F == 0x7F)
+    assert np.all(got[nan] & 0x7F == 0x7F)
+    bad = np.flatnonzero((got != want) & ~nan)
+    assert bad.size == 0, [(hex(int(u_bits.flat[i])), hex(int(got.flat[i])), hex(int(want.flat[i]))) for i in bad[:8]]
+
+
 # ---- rope -----------------------------------------------------------------------------------------
 
 def _rope_case(mas, dev, n, hq, hk, head_dim, rotary_dim, neox, pos_dtype, seed, max_pos=4096):
