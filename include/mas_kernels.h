@@ -41,6 +41,7 @@ extern "C" {
 #define MAS_ERRBIT_BATCH 4u     /* kv: batch index outside [0, batch)                     */
 #define MAS_ERRBIT_PAGE 8u      /* kv: page slot past kv_indices or page id out of range  */
 #define MAS_ERRBIT_SLOT 16u     /* kv slot form: slot >= num_pages * page_size            */
+#define MAS_ERRBIT_PLACEHOLDER 32u /* embedding: placeholder -1 - r with r >= num_last     */
 
 /* Library version, (major << 16) | (minor << 8) | patch. */
 int mas_version(void);
@@ -161,8 +162,14 @@ int mas_store_kv_slots_bf16(void* k_cache, void* v_cache, int64_t page_stride, i
  * position outside the table skips the rotation of that token (its unrotated k is stored); a
  * destination out of range skips its cache write; both are reported through `err` as above.
  * head_dim must be one of 32, 64, 128, 256, 512.
- * Replaces the call pair at miniagentserve/models/devstral2/devstral2.py:163-173
- * (apply_rope_with_cos_sin_cache_inplace then append_paged_kv_cache on the same rows).
+ * Optional llama-4 query scaling: when q_scale_table (bf16, q_scale_rows entries, row k =
+ * bf16(1 + beta * log1p(k))) is given, q ends as bf16(f32(bf16(rope(q))) *
+ * f32(q_scale_table[pos / q_scale_interval])), the reference's query_states after its two-rounding
+ * multiply; a position past the table leaves q rotated, unscaled and reported (POSITION bit).
+ * Pass NULL (rows and interval then ignored) for no scaling.
+ * Replaces the call sequence at miniagentserve/models/devstral2/devstral2.py:163-179
+ * (apply_rope_with_cos_sin_cache_inplace, append_paged_kv_cache on the same rows, then the
+ * llama-4 query scale).
  */
 int mas_rope_append_paged_kv_cache_bf16(void* q, int64_t q_stride, int64_t q_head_stride, int64_t num_q_heads,
                                         void* k, int64_t k_stride, int64_t k_head_stride, const void* v,
@@ -172,7 +179,9 @@ int mas_rope_append_paged_kv_cache_bf16(void* q, int64_t q_stride, int64_t q_hea
                                         void* k_cache, void* v_cache, int64_t page_stride, int64_t entry_stride,
                                         int64_t head_stride, int64_t num_pages, int64_t page_size,
                                         const int32_t* batch_indices, const int32_t* kv_indices,
-                                        int64_t num_indices, const int32_t* kv_indptr, int64_t batch, uint32_t* err,
+                                        int64_t num_indices, const int32_t* kv_indptr, int64_t batch,
+                                        const void* q_scale_table, int64_t q_scale_rows, int64_t q_scale_interval,
+                                        uint32_t* err,
                                         hipStream_t stream);
 
 /*
@@ -182,6 +191,21 @@ int mas_rope_append_paged_kv_cache_bf16(void* q, int64_t q_stride, int64_t q_hea
  */
 int mas_embedding_bf16(void* out, int64_t out_stride, const void* weight, int64_t weight_stride, int64_t vocab,
                        const int64_t* ids, int64_t rows, int64_t hidden, uint32_t* err, hipStream_t stream);
+
+/*
+ * The step-input path: placeholder resolution fused with the gather. An id -1 - r in ids stands
+ * for last_tokens[r] (int32 [num_last], the previous step's samples, still on the GPU); each is
+ * replaced in ids by that sample, as fill_placeholders does, and the row of the resolved id is
+ * gathered as by mas_embedding_bf16. Non-negative ids are read only. A placeholder with
+ * r >= num_last keeps its id, gets a zero row and sets MAS_ERRBIT_PLACEHOLDER. With out == NULL
+ * (or hidden == 0) only the ids are resolved: the drop-in for fill_placeholders alone.
+ * Replaces ModelRunner.fill_placeholders (miniagentserve/engine/model_runner.py:149-154) and the
+ * embed_tokens call that reads its result (miniagentserve/models/devstral2/devstral2.py:282).
+ */
+int mas_embedding_fill_placeholders_bf16(void* out, int64_t out_stride, const void* weight, int64_t weight_stride,
+                                         int64_t vocab, int64_t* ids, int64_t rows, int64_t hidden,
+                                         const int32_t* last_tokens, int64_t num_last, uint32_t* err,
+                                         hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -39,8 +39,11 @@ _SIGNATURES: dict[str, list] = {
     "mas_rope_append_paged_kv_cache_bf16": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64,
                                             _i64, _i64, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i32,
                                             _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _c_void_p,
-                                            _c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p],
+                                            _c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _i64, _c_void_p,
+                                            _c_void_p],
     "mas_embedding_bf16": [_c_void_p, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _c_void_p],
+    "mas_embedding_fill_placeholders_bf16": [_c_void_p, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64, _i64,
+                                             _c_void_p, _i64, _c_void_p, _c_void_p],
 }
 _RESTYPES = {"mas_status_string": ctypes.c_char_p}
 
@@ -50,6 +53,7 @@ ERROR_BITS = {
     4: "batch index outside [0, batch)",
     8: "page slot past kv_indices or page id outside the cache",
     16: "slot past the end of the cache",
+    32: "placeholder -1 - r past the previous step's samples",
 }
 
 _lock = threading.Lock()

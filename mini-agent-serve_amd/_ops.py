@@ -116,17 +116,40 @@ def _(input_ids, weight):
     return weight.new_empty(tuple(input_ids.shape) + (weight.shape[1],))
 
 
+@custom_op("mas::embedding_fill_placeholders", mutates_args=("input_ids",))
+def _embedding_fill(input_ids: Tensor, weight: Tensor, last_tokens: Tensor) -> Tensor:
+    out = torch.empty(tuple(input_ids.shape) + (weight.shape[1],), dtype=weight.dtype, device=weight.device)
+    embedding._embedding(input_ids, weight, out, None, last_tokens)
+    return out
+
+
+@_embedding_fill.register_fake
+def _(input_ids, weight, last_tokens):
+    return weight.new_empty(tuple(input_ids.shape) + (weight.shape[1],))
+
+
+@custom_op("mas::fill_placeholders", mutates_args=("input_ids",))
+def _fill(input_ids: Tensor, last_tokens: Tensor) -> None:
+    embedding._fill_placeholders(input_ids, last_tokens)
+
+
+@_fill.register_fake
+def _(input_ids, last_tokens):
+    return None
+
+
 @custom_op("mas::apply_rope_and_append_paged_kv_cache", mutates_args=("query", "key", "k_cache", "v_cache"))
 def _rope_append(positions: Tensor, query: Tensor, key: Tensor, value: Tensor, head_size: int, cos_sin_cache: Tensor,
                  is_neox: bool, batch_indices: Tensor, k_cache: Tensor, v_cache: Tensor, kv_indices: Tensor,
-                 kv_indptr: Tensor, kv_layout: str) -> None:
+                 kv_indptr: Tensor, kv_layout: str, llama_4_scaling_beta: float = 0.0,
+                 original_max_position_embeddings: int = 0) -> None:
     fused._fused(positions, query, key, value, head_size, cos_sin_cache, is_neox, batch_indices, (k_cache, v_cache),
-                 kv_indices, kv_indptr, kv_layout, None)
+                 kv_indices, kv_indptr, kv_layout, None, llama_4_scaling_beta, original_max_position_embeddings)
 
 
 @_rope_append.register_fake
 def _(positions, query, key, value, head_size, cos_sin_cache, is_neox, batch_indices, k_cache, v_cache, kv_indices,
-      kv_indptr, kv_layout):
+      kv_indptr, kv_layout, llama_4_scaling_beta=0.0, original_max_position_embeddings=0):
     return None
 
 

@@ -10,6 +10,13 @@
 // table leaves that token's q/k unrotated (and the cache receives the unrotated k, as the separate
 // calls would); a destination out of range skips the cache write only.
 //
+// Optional llama-4 query scaling (devstral2.py:175-179): with a q-scale table S (bf16, row k =
+// bf16(1 + beta * log1p(k)), built by the caller with the reference's own torch expression), each q
+// element becomes bf16(f32(bf16(rope(q))) * f32(S[pos / interval])) - the reference's two roundings,
+// so q ends bit-identical to its query_states after line 179. A scale of exactly 1 (every position
+// below the interval) leaves the rotated value unchanged and is skipped. A position past the
+// scale table leaves q rotated but unscaled and is reported.
+//
 // Work item: one wavefront = one token x PASSES x (64 / LPH) heads of the list
 // [q heads | k heads | v heads], LPH = head_dim / 16 lanes per head. The rotary dimension equals
 // head_dim, so a lane's two 16-byte vectors (rotation pairs i and i + D/2, or 8 interleaved pairs)
@@ -39,6 +46,8 @@ struct FusedArgs {
   const int32_t* batch_indices;
   const float* table;
   int64_t table_stride, table_rows;
+  const uint16_t* q_scale;
+  int64_t q_scale_rows, q_scale_interval;
   uint16_t* k_cache;
   uint16_t* v_cache;
   int64_t page_stride, entry_stride, head_stride, num_pages, page_size;
@@ -117,6 +126,15 @@ __global__ __launch_bounds__(kBlock) void rope_append(FusedArgs a) {
   }
   int64_t dst_row = 0;
   const bool cache_ok = appends && resolve_page(a, t, pos, &dst_row);
+  float q_scale = 1.0f;
+  if (a.q_scale != nullptr && rope_ok && first < hq) {
+    const int64_t row = pos / a.q_scale_interval;
+    if (row < a.q_scale_rows) {
+      q_scale = bf16_lo(a.q_scale[row]);
+    } else if (lane == 0) {
+      report(a.err, MAS_ERRBIT_POSITION);
+    }
+  }
 
   float cs[8], sn[8];
   if (rope_ok) {
@@ -169,6 +187,18 @@ __global__ __launch_bounds__(kBlock) void rope_append(FusedArgs a) {
       }
       oa = pack8(ya);
       ob = pack8(yb);
+      if (is_q && q_scale != 1.0f) {
+        float za[8], zb[8];
+        unpack8(oa, za);
+        unpack8(ob, zb);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          za[i] *= q_scale;
+          zb[i] *= q_scale;
+        }
+        oa = pack8(za);
+        ob = pack8(zb);
+      }
       uint16_t* dst = const_cast<uint16_t*>(src[p]);  // q or k rows, rotated in place
       store_stream(dst + off_a, oa);
       store_stream(dst + off_b, ob);
@@ -216,8 +246,8 @@ extern "C" int mas_rope_append_paged_kv_cache_bf16(
     const int32_t* positions, const float* table, int64_t table_stride, int64_t table_rows, int64_t rows,
     int64_t head_dim, int is_neox, void* k_cache, void* v_cache, int64_t page_stride, int64_t entry_stride,
     int64_t head_stride, int64_t num_pages, int64_t page_size, const int32_t* batch_indices,
-    const int32_t* kv_indices, int64_t num_indices, const int32_t* kv_indptr, int64_t batch, uint32_t* err,
-    hipStream_t stream) {
+    const int32_t* kv_indices, int64_t num_indices, const int32_t* kv_indptr, int64_t batch,
+    const void* q_scale_table, int64_t q_scale_rows, int64_t q_scale_interval, uint32_t* err, hipStream_t stream) {
   using namespace mas;
   if (rows < 0 || num_q_heads < 0 || num_kv_heads < 0 || head_dim <= 0 || table_rows < 0 || num_pages < 0 ||
       page_size <= 0 || batch < 0 || num_indices < 0)
@@ -233,17 +263,20 @@ extern "C" int mas_rope_append_paged_kv_cache_bf16(
     return MAS_ERR_INVALID_VALUE;
   if (num_indices > 0 && kv_indices == nullptr) return MAS_ERR_INVALID_VALUE;
   if (table_stride < head_dim && table_rows > 1) return MAS_ERR_INVALID_VALUE;
+  if (q_scale_table != nullptr && (q_scale_rows < 1 || q_scale_interval < 1)) return MAS_ERR_INVALID_VALUE;
   const bool q_ok = num_q_heads == 0 || (aligned16(q) && q_stride % 8 == 0 && q_head_stride % 8 == 0);
   const bool kv_ok = num_kv_heads == 0 ||
                      (aligned16(k) && aligned16(v) && aligned16(k_cache) && aligned16(v_cache) && k_stride % 8 == 0 &&
                       k_head_stride % 8 == 0 && v_stride % 8 == 0 && v_head_stride % 8 == 0 &&
                       page_stride % 8 == 0 && entry_stride % 8 == 0 && head_stride % 8 == 0);
-  if (!q_ok || !kv_ok || !aligned16(table) || table_stride % 4 != 0) return MAS_ERR_MISALIGNED;
+  if (!q_ok || !kv_ok || !aligned16(table) || table_stride % 4 != 0 ||
+      (reinterpret_cast<uintptr_t>(q_scale_table) & 1u) != 0)
+    return MAS_ERR_MISALIGNED;
   int cus = 0;
   if (const int st = device_cu_count(&cus); st != MAS_OK) return st;
   FusedArgs a{static_cast<uint16_t*>(q), q_stride, q_head_stride, static_cast<uint16_t*>(k), k_stride, k_head_stride,
               static_cast<const uint16_t*>(v), v_stride, v_head_stride, positions, batch_indices, table, table_stride,
-              table_rows, static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), page_stride, entry_stride,
+              table_rows, static_cast<const uint16_t*>(q_scale_table), q_scale_rows, q_scale_interval, static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), page_stride, entry_stride,
               head_stride, num_pages, page_size, kv_indices, num_indices, kv_indptr, batch, rows,
               static_cast<int>(num_q_heads), static_cast<int>(num_kv_heads), 0, err};
   const bool neox = is_neox != 0;

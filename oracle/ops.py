@@ -100,6 +100,23 @@ def rope(q_bits, k_bits, positions, table, is_neox: bool = True):
     return apply(q_bits), apply(k_bits)
 
 
+def llama_4_q_scale_table(beta: float, original_max_position: int, rows: int) -> np.ndarray:
+    """devstral2.py:176-178 on k = floor(pos / original_max) (an integer, so floor(pos.float() /
+    original_max) = pos // original_max for pos < 2^24): bf16(1 + f32(beta) * f32(log1p(k))), with
+    log1p evaluated in fp64 and rounded to fp32. Returns bf16 bits [rows]."""
+    k = np.arange(rows, dtype=np.float64)
+    lg = np.log1p(k).astype(F32)
+    return f32_to_bf16(F32(1.0) + F32(beta) * lg)
+
+
+def llama_4_scale_q(q_bits, positions, scale_table, original_max_position: int):
+    """devstral2.py:179: q * bf16(scale)[:, None, None] in bf16 arithmetic:
+    bf16(f32(q) * f32(S[pos // original_max])). q_bits [N, Hq, D]; returns bf16 bits."""
+    pos = np.asarray(positions, dtype=np.int64)
+    s = bf16_to_f32(np.asarray(scale_table, dtype=np.uint16)[pos // original_max_position])
+    return f32_to_bf16(bf16_to_f32(q_bits) * s[:, None, None])
+
+
 def paged_destinations(batch_indices, positions, kv_indices, kv_indptr, page_size: int):
     """(page, entry) per token for the block-table form, devstral2.py:170-173 with kv_indptr from
     :289: page = kv_indices[kv_indptr[b] + p // page_size], entry = p % page_size."""
@@ -135,6 +152,15 @@ def store_kv_slots(k_cache, v_cache, key, value, slot_mapping):
 def embedding(weight_bits, ids):
     """nn.Embedding at devstral2.py:260,282: rows of the table selected by the ids."""
     return np.asarray(weight_bits)[np.asarray(ids, dtype=np.int64)]
+
+
+def fill_placeholders(ids, last_tokens):
+    """ModelRunner.fill_placeholders (model_runner.py:149-154): every id -1 - r becomes
+    last_tokens[r]; other ids stay. Returns the new int64 ids."""
+    ids = np.asarray(ids, dtype=np.int64)
+    last = np.asarray(last_tokens, dtype=np.int64)
+    rows = np.clip(-1 - ids, 0, None)
+    return np.where(ids < 0, last[rows], ids)
 
 
 def rope_inv_freq(rotary_dim: int, theta: float) -> np.ndarray:

@@ -375,6 +375,51 @@ def test_embedding_out_of_range_ids_and_module(mas, dev):
     assert torch.equal(emb(ids2), table.to(dev)[ids2])
 
 
+@pytest.mark.parametrize("rows,vocab,hidden", [(64, 131072, 5120), (256, 4096, 5120), (9, 50, 100)])
+def test_embedding_with_placeholders(mas, dev, rows, vocab, hidden):
+    """The step-input path (model_runner.py:149-154 then devstral2.py:282) in one launch: the ids
+    after the call equal fill_placeholders' result and the rows those ids select."""
+    g = torch.Generator().manual_seed(rows + hidden)
+    table = _randn_bf16(g, vocab, hidden)
+    last = torch.randint(0, vocab, (rows + 3,), generator=g).to(torch.int32)
+    ids = torch.randint(0, vocab, (rows,), generator=g)
+    holders = torch.rand(rows, generator=g) < 0.5
+    ids[holders] = -1 - torch.randint(0, rows + 3, (int(holders.sum()),), generator=g)
+    ids[0] = -1                                              # row 0 of the samples
+    want_ids = ops.fill_placeholders(ids.numpy(), last.numpy())
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    ids_d = ids.to(dev)
+    out = mas.embedding.embedding(ids_d, table.to(dev), last_tokens=last.to(dev), error_flags=flags)
+    assert np.array_equal(ids_d.cpu().numpy(), want_ids)
+    assert np.array_equal(bits(out), ops.embedding(bits(table), want_ids))
+    assert int(flags.item()) == 0
+    # fill_placeholders alone
+    ids_d = ids.to(dev)
+    mas.embedding.fill_placeholders(ids_d, last.to(dev))
+    assert np.array_equal(ids_d.cpu().numpy(), want_ids)
+
+
+def test_embedding_placeholder_errors(mas, dev):
+    g = torch.Generator().manual_seed(5)
+    table = _randn_bf16(g, 50, 256)
+    last = torch.tensor([7, 60, 2], dtype=torch.int32)       # 60 is past the vocab
+    ids = torch.tensor([-1, -4, -2, 3, -3])                   # -4: row 3 is past the samples
+    for hidden in (256, 100):                                 # vector and scalar kernels
+        flags = torch.zeros(1, dtype=torch.int32, device=dev)
+        ids_d = ids.to(dev)
+        tab = table[:, :hidden].contiguous()
+        out = mas.embedding.embedding(ids_d, tab.to(dev), last_tokens=last.to(dev), error_flags=flags)
+        assert ids_d.tolist() == [7, -4, 60, 3, 2]
+        assert int(flags.item()) == 1 | 32
+        ob = bits(out)
+        assert np.array_equal(ob[[0, 3, 4]], bits(tab)[[7, 3, 2]])
+        assert not ob[[1, 2]].any()
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    ids_d = ids.to(dev)
+    mas.embedding.fill_placeholders(ids_d, last.to(dev), error_flags=flags)
+    assert ids_d.tolist() == [7, -4, 60, 3, 2] and int(flags.item()) == 32
+
+
 # ---- empty inputs -------------------------------------------------------------------------------------
 
 def test_empty_inputs_are_no_ops(mas, dev):
@@ -483,6 +528,54 @@ def test_rope_append_fused_matches_separate_calls(mas, dev, neox, n, hq, hk, d, 
                                                  pos.numpy(), tables.flatten().numpy(), indptr.numpy())
     assert np.array_equal(bits(fb[:, : hq * d]).reshape(n, hq, d), want_q)
     assert np.array_equal(bits(fk), want_kc) and np.array_equal(bits(fv), want_vc)
+
+
+@pytest.mark.parametrize("beta,interval", [(0.1, 16), (0.5, 7), (1.0, 1)])
+def test_rope_append_fused_llama_4_q_scale(mas, dev, beta, interval):
+    """RoPE + KV append + llama-4 query scale in one kernel against the reference's three steps
+    (devstral2.py:163-179: rope in place, append, then q * bf16(1 + beta * log1p(floor(pos / M))))
+    run with the separate ops and the reference's own torch expression: bit-identical q, k and caches.
+    Then against the oracle, with the wrapper's scale table checked against the closed form."""
+    g = torch.Generator().manual_seed(int(beta * 100) + interval)
+    n, hq, hk, d, page_size = 48, 8, 2, 128, 16
+    lens = [20, 28]
+    bidx = torch.cat([torch.full((m,), b) for b, m in enumerate(lens)]).to(torch.int32)
+    pos = (torch.cat([torch.arange(m) for m in lens]) * 3 + 1).to(torch.int32)   # spans several scale intervals
+    table = mas.rope.cos_sin_cache(int(pos.max()) + 5, d, 1e6)
+    width = -(-(int(pos.max()) + 1) // page_size) + 1
+    pages = len(lens) * width + 2
+    tables = torch.randperm(pages, generator=g)[: len(lens) * width].to(torch.int32).reshape(len(lens), width)
+    indptr = torch.arange(len(lens) + 1, dtype=torch.int32) * width
+    qkv = _randn_bf16(g, n, (hq + 2 * hk) * d)
+    k0 = torch.randn(pages, page_size, hk, d, generator=g).bfloat16()
+    v0 = torch.randn(pages, page_size, hk, d, generator=g).bfloat16()
+    pd, bd, ind, ptr_, tab = pos.to(dev), bidx.to(dev), tables.flatten().to(dev), indptr.to(dev), table.to(dev)
+
+    buf = qkv.to(dev)
+    q, k, v = buf.split([hq * d, hk * d, hk * d], dim=-1)
+    kc, vc = k0.to(dev), v0.to(dev)
+    mas.apply_rope_and_append_paged_kv_cache(pd, q, k, v.view(n, hk, d), d, tab, True, bd, (kc, vc), ind, ptr_,
+                                             llama_4_scaling_beta=beta, original_max_position_embeddings=interval)
+
+    sbuf = qkv.to(dev)
+    sq, sk, sv = sbuf.split([hq * d, hk * d, hk * d], dim=-1)
+    skc, svc = k0.to(dev), v0.to(dev)
+    mas.apply_rope_with_cos_sin_cache_inplace(pd, sq, sk, d, tab, True)
+    mas.append_paged_kv_cache(sk.view(n, hk, d), sv.view(n, hk, d), bd, pd, (skc, svc), ind, ptr_)
+    attn_scale = 1 + beta * torch.log1p(torch.floor(pd.float() / interval))
+    ref_q = sq.view(n, hq, d) * attn_scale[:, None, None].to(torch.bfloat16)
+    assert torch.equal(q.view(n, hq, d), ref_q)
+    assert torch.equal(k, sk) and torch.equal(kc, skc) and torch.equal(vc, svc)
+
+    rows = -(-table.shape[0] // interval)
+    scale_table = bits(mas.fused.llama_4_q_scale_table(beta, interval, rows, dev))
+    closed = ops.llama_4_q_scale_table(beta, interval, rows)
+    assert scale_table[0] == 0x3F80                         # 1.0
+    assert np.all(np.abs(scale_table.astype(np.int32) - closed.astype(np.int32)) <= 1)
+    q_rot, _ = ops.rope(bits(qkv[:, : hq * d]).reshape(n, hq, d), bits(qkv[:, hq * d:(hq + hk) * d]).reshape(n, hk, d),
+                        pos.numpy(), table.numpy())
+    want_q = ops.llama_4_scale_q(q_rot, pos.numpy(), scale_table, interval)
+    assert np.array_equal(bits(q).reshape(n, hq, d), want_q)
 
 
 def test_rope_append_fused_error_paths(mas, dev):

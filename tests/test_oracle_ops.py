@@ -321,3 +321,31 @@ def test_embedding_matches_torch():
     table = _randn_bf16(g, 50, 24)
     ids = torch.tensor([0, 49, 7, 7, 0, 31])
     assert np.array_equal(ops.embedding(bits(table), ids.numpy()), bits(F.embedding(ids, table)))
+
+
+@pytest.mark.parametrize("beta,interval", [(0.1, 8192), (0.5, 16), (1.0, 1)])
+def test_llama_4_q_scale_matches_hf(beta, interval):
+    """The oracle's llama-4 query scale (devstral2.py:175-179) against transformers' Ministral3
+    get_llama_4_attn_scale (1 + beta * log(1 + floor(pos / M)), fp32) at every position of 48
+    intervals, both rounded to bf16 as the reference does before the multiply; k = 0 gives 1."""
+    from transformers.models.ministral3.modeling_ministral3 import get_llama_4_attn_scale
+
+    rows = 48
+    table = ops.llama_4_q_scale_table(beta, interval, rows)
+    assert table[0] == 0x3F80
+    step = max(interval // 64, 1)
+    pos = torch.arange(0, rows * interval, step)
+    hf = get_llama_4_attn_scale(pos[None], beta, interval)[0, 0, :, 0].to(torch.bfloat16)
+    assert np.array_equal(table[pos.numpy() // interval], bits(hf))
+    # the multiply: bf16(f32(q) * f32(scale)) is torch's bf16 product
+    g = torch.Generator().manual_seed(interval)
+    q = torch.randn(pos.shape[0], 4, 32, generator=g).bfloat16()
+    want = q * from_bits(table[pos.numpy() // interval])[:, None, None]
+    assert np.array_equal(ops.llama_4_scale_q(bits(q), pos.numpy(), table, interval), bits(want))
+
+
+def test_fill_placeholders_closed_form():
+    """model_runner.py:149-154: -1 - r is row r of the previous samples; other ids pass through."""
+    last = np.array([10, 20, 30], dtype=np.int32)
+    assert ops.fill_placeholders([5, -1, -3, 0, -2], last).tolist() == [5, 10, 30, 0, 20]
+    assert ops.fill_placeholders(np.zeros(0, dtype=np.int64), last).shape == (0,)
