@@ -42,7 +42,7 @@ COLD_BYTES = 768 << 20         # working set cycled by the cold protocol (3x the
 # HBM bytes per launch of a workload's dominant kernel, from two rocprofv3 counter passes
 # (FETCH_SIZE, then WRITE_SIZE) over `bench.py --pmc-probe`, each calibrated by the same counter on
 # a 256 MiB device copy (fetch factor 1.9997, write factor 1.0000). Re-measure when the kernel changes.
-MEASURED_TRAFFIC = {("decode64_24b", "silu_and_mul"): 12_622_649}
+MEASURED_TRAFFIC = {("decode64_24b", "silu_and_mul"): 12_612_523}
 
 
 def parse_args():
@@ -107,10 +107,11 @@ def op_launcher(mas, b, op):
     raise ValueError(op)
 
 
-def time_ops(mas, layer_sets, launches: int, ops: tuple[str, ...]) -> dict[str, float]:
+def time_ops(mas, layer_sets, launches: int, ops: tuple[str, ...], replays: int = 5) -> dict[str, float]:
     """Average launch duration (µs) of each kernel: a HIP graph of ``launches`` back-to-back launches
     of that kernel alone, cycling the layer sets, bracketed by two HIP events on the stream the
-    graph replays on."""
+    graph replays on. The graph is replayed once untimed, then ``replays`` times, each between its
+    own pair of events; the median replay is reported (GPU clocks vary between phases of a run)."""
     out = {}
     for op in ops:
         fns = [op_launcher(mas, layer_sets[i % len(layer_sets)], op) for i in range(launches)]
@@ -121,12 +122,15 @@ def time_ops(mas, layer_sets, launches: int, ops: tuple[str, ...]) -> dict[str, 
 
         g = capture(body)
         g.replay()
-        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        g.replay()
-        stop.record()
+        events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(replays)]
+        for start, stop in events:
+            start.record()
+            g.replay()
+            stop.record()
         torch.cuda.synchronize()
-        out[op] = 1000.0 * start.elapsed_time(stop) / launches
+        times = sorted(start.elapsed_time(stop) for start, stop in events)
+        out[op] = 1000.0 * times[len(times) // 2] / launches
         del g
     return out
 

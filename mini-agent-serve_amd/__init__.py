@@ -9,7 +9,10 @@ Drop-ins for the calls the reference's layer modules make
 - ``rope.apply_rope_with_cos_sin_cache_inplace``                    (flashinfer.rope, :163-166)
 - ``page.append_paged_kv_cache`` (+ ``page.store_kv_slots``)        (flashinfer.page, :170-173)
 - ``embedding.embedding`` / ``embedding.Embedding``                 (nn.Embedding, :260, :282)
-- ``fused.apply_rope_and_append_paged_kv_cache``                    (the :163-166 + :170-173 pair, one kernel)
+- ``embedding.fill_placeholders`` / ``embedding(..., last_tokens=)`` (ModelRunner.fill_placeholders,
+  miniagentserve/engine/model_runner.py:149-154, alone or fused with the gather)
+- ``fused.apply_rope_and_append_paged_kv_cache``                    (:163-166 + :170-173 + the llama-4
+  query scale at :175-179, one kernel)
 
 Each op validates its tensors, then calls hand-written HIP kernels in ``libmas_kernels.so``
 through the C ABI of ``include/mas_kernels.h`` on torch's current stream. There is no CPU or

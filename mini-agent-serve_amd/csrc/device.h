@@ -84,18 +84,20 @@ __device__ __forceinline__ uint32_t fp8x4_saturate_encode(float a, float b, floa
 
 __device__ __forceinline__ uint32_t fp8_saturate_encode(float v) { return fp8x4_saturate_encode(v, v, v, v) & 0xffu; }
 
-// y / s rounded as IEEE division rounds it, from r = 1/s (one division per thread): q0 = y * r is
-// within an ulp of the quotient, the residual q0 * s - y is exact in one fma, and q0 minus the
-// residual times r rounds to the correctly rounded quotient (Markstein, IBM J. Res. Dev. 34(1),
-// 1990). Holds while the residual does not underflow, i.e. for every |y / s| >= 2^-100 - far
-// below fp8's smallest subnormal 2^-9. The residual is formed as q0 * s - y so that a zero
-// quotient keeps its sign (-0 - (+0) * r = -0). A non-finite q0 (y infinite or NaN, or overflow)
-// is returned as is.
+// y / s rounded as IEEE division rounds it, from r = 1/s (one division per thread), for the fp8
+// epilogues: q0 = y * r is within an ulp of the quotient, the residual q0 * s - y is exact in one
+// fma, and q0 minus the residual times r rounds to the correctly rounded quotient (Markstein, IBM J.
+// Res. Dev. 34(1), 1990). Holds while the residual does not underflow, i.e. for every
+// |y / s| >= 2^-100 - far below fp8's smallest subnormal 2^-9. Before the correction q0 is clamped
+// to +-896 (one v_med3): values that far out saturate to +-448 whatever their rounding, and the
+// clamp keeps the residual finite when y * r overflows or y is infinite (the result is then
+// +-inf or a value past 896, which the fp8 clamp saturates). A NaN y returns NaN through -y. The
+// residual is formed as q0 * s - y so that a zero quotient keeps its sign (-0 - (+0) * r = -0).
+// s must be a positive normal number (an activation scale).
 __device__ __forceinline__ float div_by_scale(float y, float s, float r) {
-  const float q0 = y * r;
+  const float q0 = __builtin_amdgcn_fmed3f(y * r, -896.0f, 896.0f);
   const float e = __builtin_fmaf(q0, s, -y);
-  const float q1 = __builtin_fmaf(-e, r, q0);
-  return __builtin_isfinite(q0) ? q1 : q0;
+  return __builtin_fmaf(-e, r, q0);
 }
 
 // ---- wavefront / block reductions ----------------------------------------------------------
