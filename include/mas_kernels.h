@@ -207,6 +207,39 @@ int mas_embedding_fill_placeholders_bf16(void* out, int64_t out_stride, const vo
                                          const int32_t* last_tokens, int64_t num_last, uint32_t* err,
                                          hipStream_t stream);
 
+/*
+ * Paged decode attention: for each row b and query head h (kv head h / (num_q_heads /
+ * num_kv_heads)), over the positions p < seq_lens[b] whose key/value rows sit at
+ * page = block_tables[b * block_table_stride + p / page_size], entry = p % page_size:
+ *   out[b, h] = bmm2_scale * sum_p softmax_p(bmm1_scale * q[b, h] . k_p) * v_p   (fp32, bf16 out).
+ * q, out: [batch, num_q_heads, head_dim] with row / head strides; caches as for the append above
+ * (page, entry, head strides); block_tables int32 [batch, max_blocks]; seq_lens int32 [batch].
+ * head_dim in {64, 128, 256}; num_q_heads / num_kv_heads <= 16; page_size a power of two.
+ * `workspace` (16-byte aligned, workspace_bytes long) holds the per-split partials: the split
+ * length is the smallest multiple of 256 positions (doubling) whose partials fit, at most
+ * mas_paged_decode_attention_workspace_bytes(...) for one split per 256 positions. A page id
+ * outside [0, num_pages) skips its position (MAS_ERRBIT_PAGE); a seq_len outside
+ * [0, max_blocks * page_size] is clamped (MAS_ERRBIT_POSITION); a row with no position gets zeros.
+ * Replaces flashinfer.decode.trtllm_batch_decode_with_kv_cache at
+ * miniagentserve/models/devstral2/devstral2.py:184-196 (kv_layout "NHD", no sliding window).
+ */
+int mas_paged_decode_attention_bf16(void* out, int64_t out_stride, int64_t out_head_stride, const void* q,
+                                    int64_t q_stride, int64_t q_head_stride, const void* k_cache, const void* v_cache,
+                                    int64_t page_stride, int64_t entry_stride, int64_t head_stride, int64_t num_pages,
+                                    int64_t page_size, const int32_t* block_tables, int64_t block_table_stride,
+                                    int64_t max_blocks, const int32_t* seq_lens, int64_t batch, int64_t num_q_heads,
+                                    int64_t num_kv_heads, int64_t head_dim, float bmm1_scale, float bmm2_scale,
+                                    void* workspace, int64_t workspace_bytes, uint32_t* err, hipStream_t stream);
+
+/*
+ * Workspace bytes mas_paged_decode_attention_bf16 needs when each split covers
+ * chunks_per_split * 256 positions (1: the most parallel split). -1 for invalid arguments.
+ * No counterpart in the reference (its caller passes a fixed 128 MiB workspace,
+ * miniagentserve/models/devstral2/devstral2.py:36-42).
+ */
+int64_t mas_paged_decode_attention_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t head_dim,
+                                                   int64_t max_blocks, int64_t page_size, int64_t chunks_per_split);
+
 #ifdef __cplusplus
 }
 #endif

@@ -11,6 +11,7 @@ Drop-ins for the calls the reference's layer modules make
 - ``embedding.embedding`` / ``embedding.Embedding``                 (nn.Embedding, :260, :282)
 - ``embedding.fill_placeholders`` / ``embedding(..., last_tokens=)`` (ModelRunner.fill_placeholders,
   miniagentserve/engine/model_runner.py:149-154, alone or fused with the gather)
+- ``attention.trtllm_batch_decode_with_kv_cache``                   (flashinfer.decode, :184-196)
 - ``fused.apply_rope_and_append_paged_kv_cache``                    (:163-166 + :170-173 + the llama-4
   query scale at :175-179, one kernel)
 
@@ -23,7 +24,7 @@ imports it as ``mini_agent_serve_amd``.
 """
 from __future__ import annotations
 
-from . import _lib, activation, embedding, fused, norm, page, rope, workloads
+from . import _lib, activation, attention, embedding, fused, norm, page, rope, workloads
 from . import layer_pass
 from . import _ops  # noqa: F401  (registers the torch.library ops)
 from .activation import silu_and_mul, silu_and_mul_quant
@@ -34,7 +35,7 @@ from .page import append_paged_kv_cache, store_kv_slots
 from .rope import apply_rope_with_cos_sin_cache_inplace
 
 __all__ = [
-    "activation", "embedding", "fused", "norm", "page", "rope", "workloads", "layer_pass",
+    "activation", "attention", "embedding", "fused", "norm", "page", "rope", "workloads", "layer_pass",
     "apply_rope_and_append_paged_kv_cache",
     "silu_and_mul", "silu_and_mul_quant", "Embedding", "fused_add_rmsnorm", "fused_add_rmsnorm_quant", "append_paged_kv_cache",
     "store_kv_slots", "apply_rope_with_cos_sin_cache_inplace", "load_library", "library_version",

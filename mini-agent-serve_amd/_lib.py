@@ -44,8 +44,13 @@ _SIGNATURES: dict[str, list] = {
     "mas_embedding_bf16": [_c_void_p, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _c_void_p],
     "mas_embedding_fill_placeholders_bf16": [_c_void_p, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64, _i64,
                                              _c_void_p, _i64, _c_void_p, _c_void_p],
+    "mas_paged_decode_attention_bf16": [_c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64,
+                                        _i64, _i64, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _i64,
+                                        _i64, ctypes.c_float, ctypes.c_float, _c_void_p, _i64, _c_void_p,
+                                        _c_void_p],
+    "mas_paged_decode_attention_workspace_bytes": [_i64, _i64, _i64, _i64, _i64, _i64],
 }
-_RESTYPES = {"mas_status_string": ctypes.c_char_p}
+_RESTYPES = {"mas_status_string": ctypes.c_char_p, "mas_paged_decode_attention_workspace_bytes": ctypes.c_int64}
 
 ERROR_BITS = {
     1: "token id outside [0, vocab)",

@@ -10,7 +10,7 @@ from __future__ import annotations
 import torch
 from torch.library import custom_op
 
-from . import activation, embedding, fused, norm, page, rope
+from . import activation, attention, embedding, fused, norm, page, rope
 
 Tensor = torch.Tensor
 
@@ -135,6 +135,19 @@ def _fill(input_ids: Tensor, last_tokens: Tensor) -> None:
 
 @_fill.register_fake
 def _(input_ids, last_tokens):
+    return None
+
+
+@custom_op("mas::paged_decode_attention", mutates_args=("workspace", "out"))
+def _paged_decode_attention(query: Tensor, k_cache: Tensor, v_cache: Tensor, workspace: Tensor, block_tables: Tensor,
+                            seq_lens: Tensor, bmm1_scale: float, bmm2_scale: float, out: Tensor,
+                            kv_layout: str) -> None:
+    attention._decode(query, (k_cache, v_cache), workspace, block_tables, seq_lens, bmm1_scale, bmm2_scale, out,
+                      kv_layout, None)
+
+
+@_paged_decode_attention.register_fake
+def _(query, k_cache, v_cache, workspace, block_tables, seq_lens, bmm1_scale, bmm2_scale, out, kv_layout):
     return None
 
 

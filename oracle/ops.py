@@ -149,6 +149,36 @@ def store_kv_slots(k_cache, v_cache, key, value, slot_mapping):
     return k_out, v_out
 
 
+def paged_decode_attention(q_bits, k_cache_bits, v_cache_bits, block_tables, seq_lens, bmm1_scale: float,
+                           bmm2_scale: float = 1.0):
+    """trtllm_batch_decode_with_kv_cache (devstral2.py:184-196) on NHD caches [pages, page_size, Hk, D]:
+    for row b, query head h (kv head h // (Hq // Hk)) and positions p < seq_lens[b] at page
+    block_tables[b, p // page_size], entry p % page_size:
+    out = bf16(bmm2_scale * sum_p softmax_p(bmm1_scale * q . k_p) v_p), fp32 math. Rows with no
+    position give zeros. q_bits [B, Hq, D]; returns bf16 bits [B, Hq, D]."""
+    q = bf16_to_f32(np.asarray(q_bits))
+    batch, hq, dim = q.shape
+    page_size, hk = k_cache_bits.shape[1], k_cache_bits.shape[2]
+    group = hq // hk
+    tables = np.asarray(block_tables, dtype=np.int64)
+    out = np.zeros((batch, hq, dim), dtype=np.uint16)
+    for b in range(batch):
+        length = int(seq_lens[b])
+        if length <= 0:
+            continue
+        pos = np.arange(length)
+        pages = tables[b, pos // page_size]
+        k = bf16_to_f32(k_cache_bits[pages, pos % page_size])          # [L, Hk, D]
+        v = bf16_to_f32(v_cache_bits[pages, pos % page_size])
+        for h in range(hq):
+            kvh = h // group
+            s = (k[:, kvh, :] @ q[b, h]).astype(F32) * F32(bmm1_scale)
+            e = np.exp(s - s.max(), dtype=F32)
+            o = (e @ v[:, kvh, :]).astype(F32) / np.sum(e, dtype=F32) * F32(bmm2_scale)
+            out[b, h] = f32_to_bf16(o.astype(F32))
+    return out
+
+
 def embedding(weight_bits, ids):
     """nn.Embedding at devstral2.py:260,282: rows of the table selected by the ids."""
     return np.asarray(weight_bits)[np.asarray(ids, dtype=np.int64)]

@@ -1,0 +1,151 @@
+"""Paged decode attention (trtllm_batch_decode_with_kv_cache, devstral2.py:184-196) on the GPU
+against the oracle, through the C ABI. bf16 outputs within rtol 1.6e-2 / atol 1e-2, most of them
+bit-identical (the fp32 sums run in a different order than numpy's)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import ATOL, RTOL, bits
+from oracle import numerics as on
+from oracle import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(seed, batch, hq, hk, dim, page_size, lens, extra_pages=3):
+    g = torch.Generator().manual_seed(seed)
+    width = max(1, max(-(-n // page_size) for n in lens))
+    pages = batch * width + extra_pages
+    q = torch.randn(batch, hq, dim, generator=g).bfloat16()
+    kc = torch.randn(pages, page_size, hk, dim, generator=g).bfloat16()
+    vc = torch.randn(pages, page_size, hk, dim, generator=g).bfloat16()
+    tables = torch.randperm(pages, generator=g)[: batch * width].reshape(batch, width).to(torch.int32)
+    return q, kc, vc, tables, torch.tensor(lens, dtype=torch.int32)
+
+
+def _check(got, want, min_exact=0.9):
+    gv, wv = on.bf16_to_f32(got), on.bf16_to_f32(want)
+    np.testing.assert_allclose(gv, wv, rtol=RTOL, atol=ATOL)
+    assert np.mean(got == want) >= min_exact
+
+
+def _run(mas, dev, q, kc, vc, tables, seq, scale, workspace_bytes=None, out=None, flags=None, scale2=1.0):
+    if workspace_bytes is None:
+        workspace_bytes = 128 << 20
+    ws = torch.zeros(workspace_bytes, dtype=torch.uint8, device=dev)
+    return mas.attention.trtllm_batch_decode_with_kv_cache(
+        q.to(dev) if q.device.type == "cpu" else q, (kc.to(dev), vc.to(dev)), ws, tables.to(dev), seq.to(dev),
+        0, scale, scale2, out=out, kv_layout="NHD", error_flags=flags)
+
+
+CASES = [
+    (4, 32, 8, 128, 256, [1, 255, 256, 5000]),      # Devstral-Small-2 heads, chunk edges, a long row
+    (3, 96, 8, 128, 256, [700, 3, 1300]),          # the 123B head group (12 per kv head)
+    (5, 8, 8, 128, 16, [17, 1, 64, 300, 0]),       # one head per kv head, small pages, an empty row
+    (2, 16, 2, 64, 32, [100, 1000]),               # head_dim 64, 8 per kv head
+    (2, 16, 1, 256, 64, [513, 77]),                # head_dim 256, 16 per kv head
+    (3, 6, 2, 128, 4, [9, 40, 2]),                 # 3 per kv head (padded), pages of 4
+]
+
+
+@pytest.mark.parametrize("batch,hq,hk,dim,page_size,lens", CASES)
+def test_decode_attention_matches_oracle(mas, dev, batch, hq, hk, dim, page_size, lens):
+    q, kc, vc, tables, seq = _case(batch * 7 + dim + hq, batch, hq, hk, dim, page_size, lens)
+    scale = dim ** -0.5
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = _run(mas, dev, q, kc, vc, tables, seq, scale, flags=flags)
+    want = ops.paged_decode_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), scale)
+    _check(bits(out), want)
+    assert int(flags.item()) == 0
+    if 0 in lens:
+        assert not out[lens.index(0)].any()
+
+
+def test_decode_attention_long_splits_and_bmm2_scale(mas, dev):
+    """A workspace too small for one split per 256 positions makes each wavefront walk several
+    chunks, merging them with the running max: same results as the oracle."""
+    batch, hq, hk, dim, ps, lens = 3, 32, 8, 128, 256, [3000, 1, 2049]
+    q, kc, vc, tables, seq = _case(11, batch, hq, hk, dim, ps, lens)
+    full = mas.attention.decode_workspace_bytes(batch, hq, dim, tables.shape[1], ps, 1)
+    four = mas.attention.decode_workspace_bytes(batch, hq, dim, tables.shape[1], ps, 4)
+    assert four < full
+    out = _run(mas, dev, q, kc, vc, tables, seq, 0.09, workspace_bytes=four, scale2=0.5)
+    want = ops.paged_decode_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), 0.09, 0.5)
+    _check(bits(out), want)
+    with pytest.raises(mas._lib.KernelError):
+        _run(mas, dev, q, kc, vc, tables, seq, 0.09, workspace_bytes=16)
+
+
+def test_decode_attention_strided_query_and_out(mas, dev):
+    """q as the column view of the qkv rows (row stride (Hq + 2 Hk) * D), out as a strided view."""
+    batch, hq, hk, dim, ps, lens = 4, 32, 8, 128, 16, [33, 70, 5, 16]
+    _, kc, vc, tables, seq = _case(5, batch, hq, hk, dim, ps, lens)
+    g = torch.Generator().manual_seed(6)
+    qkv = torch.randn(batch, (hq + 2 * hk) * dim, generator=g).bfloat16().to(dev)
+    q = qkv[:, : hq * dim].view(batch, hq, dim)
+    out_base = torch.full((batch, hq + 1, dim), 3.0, dtype=torch.bfloat16, device=dev)
+    out = out_base[:, 1:]
+    _run(mas, dev, q, kc, vc, tables, seq, 0.1, out=out)
+    want = ops.paged_decode_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), 0.1)
+    _check(bits(out), want)
+    assert torch.all(out_base[:, 0] == 3.0)
+
+
+def test_decode_attention_error_paths(mas, dev):
+    batch, hq, hk, dim, ps = 3, 8, 2, 128, 16
+    q, kc, vc, tables, _ = _case(9, batch, hq, hk, dim, ps, [40, 40, 40])
+    pages = kc.shape[0]
+    bad = tables.clone()
+    bad[0, 1] = pages + 5                               # positions 16..31 of row 0 point past the cache
+    seq = torch.tensor([40, 10_000, 20], dtype=torch.int32)   # row 1 past the table's reach (3 pages = 48)
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = _run(mas, dev, q, kc, vc, bad, seq, 0.1, flags=flags)
+    assert int(flags.item()) == 2 | 8
+    # row 0 without positions 16..31: the oracle on the remaining rows
+    keep = [p for p in range(40) if not 16 <= p < 32]
+    kc2 = torch.cat([kc, torch.zeros(1, ps, hk, dim, dtype=torch.bfloat16)])
+    vc2 = torch.cat([vc, torch.zeros(1, ps, hk, dim, dtype=torch.bfloat16)])
+    # rebuild row 0's keys as a contiguous sequence in fresh pages
+    k_rows = kc[tables[0, torch.tensor(keep) // ps].long(), torch.tensor(keep) % ps]
+    v_rows = vc[tables[0, torch.tensor(keep) // ps].long(), torch.tensor(keep) % ps]
+    n = len(keep)
+    kc3 = torch.zeros(2, ps, hk, dim, dtype=torch.bfloat16)
+    vc3 = torch.zeros_like(kc3)
+    kc3.view(-1, hk, dim)[:n] = k_rows
+    vc3.view(-1, hk, dim)[:n] = v_rows
+    want0 = ops.paged_decode_attention(bits(q[:1]), bits(kc3), bits(vc3), np.array([[0, 1]]), np.array([n]), 0.1)
+    _check(bits(out[:1]), want0)
+    # row 1 clamped to 48 positions, row 2 untouched
+    want = ops.paged_decode_attention(bits(q), bits(kc2), bits(vc2), tables.numpy(), np.array([40, 48, 20]), 0.1)
+    _check(bits(out[1:]), want[1:])
+
+
+def test_decode_attention_in_graph_replays(mas, dev):
+    batch, hq, hk, dim, ps, lens = 4, 32, 8, 128, 256, [300, 1, 2000, 17]
+    q, kc, vc, tables, seq = _case(21, batch, hq, hk, dim, ps, lens)
+    qd, kd, vd, td, sd = q.to(dev), kc.to(dev), vc.to(dev), tables.to(dev), seq.to(dev)
+    ws = torch.zeros(64 << 20, dtype=torch.uint8, device=dev)
+    out = torch.empty(batch, hq, dim, dtype=torch.bfloat16, device=dev)
+
+    def call():
+        mas.attention.trtllm_batch_decode_with_kv_cache(qd, (kd, vd), ws, td, sd, 0, 0.088, 1.0, out=out)
+
+    call()
+    torch.cuda.synchronize()
+    want = out.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    for _ in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want)

@@ -18,7 +18,7 @@ HEADER = ROOT / "include" / "mas_kernels.h"
 
 def declared_entry_points() -> list[str]:
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return re.findall(r"^\s*(?:int|const char\s*\*)\s+(mas_\w+)\s*\(", text, flags=re.M)
+    return re.findall(r"^\s*(?:int64_t|int|const char\s*\*)\s+(mas_\w+)\s*\(", text, flags=re.M)
 
 
 def test_header_declares_the_bound_entry_points(mas):

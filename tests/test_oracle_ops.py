@@ -349,3 +349,54 @@ def test_fill_placeholders_closed_form():
     last = np.array([10, 20, 30], dtype=np.int32)
     assert ops.fill_placeholders([5, -1, -3, 0, -2], last).tolist() == [5, 10, 30, 0, 20]
     assert ops.fill_placeholders(np.zeros(0, dtype=np.int64), last).shape == (0,)
+
+
+def _attention_case(seed, batch, hq, hk, dim, page_size, lens, pages):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(batch, hq, dim, generator=g).bfloat16()
+    kc = torch.randn(pages, page_size, hk, dim, generator=g).bfloat16()
+    vc = torch.randn(pages, page_size, hk, dim, generator=g).bfloat16()
+    width = max(1, max(-(-n // page_size) for n in lens))
+    tables = torch.randperm(pages, generator=g)[: batch * width].reshape(batch, width).to(torch.int32)
+    return q, kc, vc, tables, torch.tensor(lens, dtype=torch.int32)
+
+
+@pytest.mark.parametrize("batch,hq,hk,dim,page_size,lens", [(3, 8, 2, 64, 16, [1, 37, 100]),
+                                                             (2, 12, 1, 128, 8, [50, 9]),
+                                                             (2, 4, 4, 32, 4, [13, 3])])
+def test_paged_decode_attention_matches_sdpa(batch, hq, hk, dim, page_size, lens):
+    """The oracle's decode attention against torch's scaled_dot_product_attention (fp32, grouped
+    query heads) on the gathered rows of each sequence."""
+    pages = batch * max(-(-n // page_size) for n in lens) + 3
+    q, kc, vc, tables, seq = _attention_case(batch + dim, batch, hq, hk, dim, page_size, lens, pages)
+    scale = dim ** -0.5
+    got = on.bf16_to_f32(ops.paged_decode_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), scale))
+    for b, n in enumerate(lens):
+        pos = torch.arange(n)
+        pg = tables[b, pos // page_size].long()
+        k = kc[pg, pos % page_size].float().permute(1, 0, 2)[None]        # [1, Hk, L, D]
+        v = vc[pg, pos % page_size].float().permute(1, 0, 2)[None]
+        ref = F.scaled_dot_product_attention(q[b].float()[None, :, None, :], k, v, scale=scale, enable_gqa=True)
+        want = on.bf16_to_f32(bits(ref[0, :, 0, :].bfloat16()))
+        np.testing.assert_allclose(got[b], want, rtol=2 ** -7, atol=1e-3)
+
+
+def test_paged_decode_attention_closed_forms():
+    q, kc, vc, tables, _ = _attention_case(3, 2, 4, 2, 32, 4, [8, 8], 8)
+    # one position: softmax is 1, the output is that value row exactly
+    out = ops.paged_decode_attention(bits(q), bits(kc), bits(vc), tables.numpy(), np.array([1, 1]), 0.3)
+    for b in range(2):
+        page = int(tables[b, 0])
+        for h in range(4):
+            assert np.array_equal(out[b, h], bits(vc)[page, 0, h // 2])
+    # scale 0 (or identical keys): the plain mean of the value rows
+    out = on.bf16_to_f32(ops.paged_decode_attention(bits(q), bits(kc), bits(vc), tables.numpy(), np.array([8, 5]), 0.0))
+    for b, n in enumerate([8, 5]):
+        pos = np.arange(n)
+        v = vc[tables[b, pos // 4].long(), pos % 4].float().numpy()
+        np.testing.assert_allclose(out[b], np.repeat(v.mean(axis=0), 2, axis=0), rtol=2 ** -7, atol=1e-6)
+    # an empty row gives zeros; bmm2_scale multiplies the output
+    out = ops.paged_decode_attention(bits(q), bits(kc), bits(vc), tables.numpy(), np.array([0, 3]), 0.5, 2.0)
+    half = ops.paged_decode_attention(bits(q), bits(kc), bits(vc), tables.numpy(), np.array([0, 3]), 0.5, 1.0)
+    assert not out[0].any()
+    np.testing.assert_allclose(on.bf16_to_f32(out[1]), 2 * on.bf16_to_f32(half[1]), rtol=2 ** -7)
