@@ -328,6 +328,76 @@ def run_pass_workload(mas, args, shape, dev) -> dict:
             "us_per_layer": ms_per_step * 1e3 / shape.layers}
 
 
+def run_attention_workload(mas, args, shape, dev) -> dict:
+    """Paged decode attention (both kernels of one call) on the workload's rows; the step is one call."""
+    wl = mas.workloads
+    inp = wl.make_attention_inputs(shape, dev, seed=0)
+    per_step = wl.attention_credited_bytes(inp)
+    out = torch.empty_like(inp.q)
+    scale = shape.head_dim ** -0.5
+
+    def call():
+        mas.attention.trtllm_batch_decode_with_kv_cache(inp.q, (inp.k_cache, inp.v_cache), inp.workspace,
+                                                        inp.block_tables, inp.seq_lens, 0, scale, 1.0, out=out)
+
+    steps = args.steps if args.steps is not None else 50
+    warmup = args.warmup if args.warmup is not None else 5
+    call()
+    g = capture(call)
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        g.replay()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    # per-call duration: HIP events around graphs of back-to-back calls, median of five replays
+    graph_calls = 10
+    gb = capture(lambda: [call() for _ in range(graph_calls)])
+    gb.replay()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(5)]
+    for start, stop in events:
+        start.record()
+        gb.replay()
+        stop.record()
+    torch.cuda.synchronize()
+    call_us = 1000.0 * sorted(a.elapsed_time(b) for a, b in events)[2] / graph_calls
+    ms_per_step = elapsed / steps * 1e3
+    lens = inp.seq_lens.cpu()
+    return {"steps": steps, "warmup": warmup, "ms_per_step": ms_per_step, "per_step_bytes": per_step,
+            "value": per_step / (ms_per_step * 1e-3) / 1e9, "sets": 1, "dominant": "paged_decode_attention",
+            "dominant_bytes": per_step, "dominant_us": call_us,
+            "ops": {"paged_decode_attention": {"us": round(call_us, 3), "GB/s": round(per_step / call_us / 1e3, 1),
+                                               "frac": round(per_step / call_us / 1e3 / PEAK_HBM_GBS, 4)}},
+            "attention": {"mean_len": round(float(lens.float().mean()), 1), "longest": int(lens.max()),
+                          "positions": int(lens.sum()), "kv_pages": inp.k_cache.shape[0]},
+            "inputs": inp}
+
+
+def cpu_baseline_attention(inp, seconds: float) -> dict:
+    """The oracle's decode attention on the host, one row at a time over the workload's rows (cycling),
+    for about ``seconds``; credited bytes of the rows done per second."""
+    from oracle import ops as oops
+
+    s = inp.shape
+    q = inp.q.cpu().view(torch.int16).numpy().view(np.uint16)
+    kc = inp.k_cache.cpu().view(torch.int16).numpy().view(np.uint16)
+    vc = inp.v_cache.cpu().view(torch.int16).numpy().view(np.uint16)
+    tables = inp.block_tables.cpu().numpy()
+    lens = inp.seq_lens.cpu().numpy()
+    done_bytes, rows, t0 = 0, 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        b = rows % s.batch
+        oops.paged_decode_attention(q[b:b + 1], kc, vc, tables[b:b + 1], lens[b:b + 1], s.head_dim ** -0.5)
+        n = int(lens[b])
+        done_bytes += n * s.kv_heads * s.head_dim * 4 + 2 * s.q_heads * s.head_dim * 2 + 4 * (-(-n // s.page_size)) + 4
+        rows += 1
+    elapsed = time.perf_counter() - t0
+    return {"value": round(done_bytes / elapsed / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{rows} rows of the workload's decode attention, single-threaded numpy ({elapsed:.1f} s)"}
+
+
 def pmc_probe(mas, args, shape, dev) -> None:
     """Launches only what a counter pass needs: the workload's dominant kernel (SiluAndMul, or the
     norm for the norm-only case) 20 times across the cold layer sets, then 4 copies of 256 MiB."""
@@ -364,6 +434,8 @@ def main() -> int:
     mas.load_library()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.workload in mas.workloads.ATTENTION_SHAPES:
+        return attention_main(mas, args, mas.workloads.ATTENTION_SHAPES[args.workload], dev)
     shape = mas.workloads.SHAPES[args.workload]
     if args.pmc_probe:
         pmc_probe(mas, args, shape, dev)
@@ -408,6 +480,30 @@ def main() -> int:
     line["copy_ceiling_GBps"] = round(copy_ceiling_gbs(dev), 1)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_layer(shape, args.cpu_seconds, args.fp8)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def attention_main(mas, args, shape, dev) -> int:
+    res = run_attention_workload(mas, args, shape, dev)
+    dom_gbs = res["dominant_bytes"] / res["dominant_us"] / 1e3
+    line = {
+        "metric": METRIC, "value": round(res["value"], 2), "unit": "GB/s", "n_gpus": 1, "steps": res["steps"],
+        "warmup": res["warmup"], "ms_per_step": round(res["ms_per_step"], 6), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": shape.name, "batch": shape.batch, "q_heads": shape.q_heads,
+                   "kv_heads": shape.kv_heads, "head_dim": shape.head_dim, "page_size": shape.page_size,
+                   "max_len": shape.max_len, **res["attention"], "launch": "hip-graph"},
+        "us_per_call": round(res["ms_per_step"] * 1e3, 3),
+        "frac_of_peak": round(res["value"] / PEAK_HBM_GBS, 4),
+        "ops": res["ops"],
+        "roofline": {"bound": "hbm", "kernel": res["dominant"], "achieved": round(dom_gbs, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(dom_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "bytes_per_launch": res["dominant_bytes"], "avg_launch_us": round(res["dominant_us"], 3)},
+        "copy_ceiling_GBps": round(copy_ceiling_gbs(dev), 1),
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline_attention(res["inputs"], args.cpu_seconds)
     print(json.dumps(line), flush=True)
     return 0
 

@@ -215,9 +215,9 @@ int mas_embedding_fill_placeholders_bf16(void* out, int64_t out_stride, const vo
  * q, out: [batch, num_q_heads, head_dim] with row / head strides; caches as for the append above
  * (page, entry, head strides); block_tables int32 [batch, max_blocks]; seq_lens int32 [batch].
  * head_dim in {64, 128, 256}; num_q_heads / num_kv_heads <= 16; page_size a power of two.
- * `workspace` (16-byte aligned, workspace_bytes long) holds the per-split partials: the split
- * length is the smallest multiple of 256 positions (doubling) whose partials fit, at most
- * mas_paged_decode_attention_workspace_bytes(...) for one split per 256 positions. A page id
+ * `workspace` (16-byte aligned, workspace_bytes long) holds the per-split partials: a split is
+ * chunks_per_split chunks of 256 positions, with chunks_per_split the smallest power of two whose
+ * partials fit (mas_paged_decode_attention_workspace_bytes). A page id
  * outside [0, num_pages) skips its position (MAS_ERRBIT_PAGE); a seq_len outside
  * [0, max_blocks * page_size] is clamped (MAS_ERRBIT_POSITION); a row with no position gets zeros.
  * Replaces flashinfer.decode.trtllm_batch_decode_with_kv_cache at
@@ -232,8 +232,8 @@ int mas_paged_decode_attention_bf16(void* out, int64_t out_stride, int64_t out_h
                                     void* workspace, int64_t workspace_bytes, uint32_t* err, hipStream_t stream);
 
 /*
- * Workspace bytes mas_paged_decode_attention_bf16 needs when each split covers
- * chunks_per_split * 256 positions (1: the most parallel split). -1 for invalid arguments.
+ * Workspace bytes mas_paged_decode_attention_bf16 needs when each split covers chunks_per_split
+ * chunks of 256 positions (1: the most parallel split). -1 for invalid arguments.
  * No counterpart in the reference (its caller passes a fixed 128 MiB workspace,
  * miniagentserve/models/devstral2/devstral2.py:36-42).
  */

@@ -27,8 +27,8 @@ SUPPORTED_HEAD_DIMS = (64, 128, 256)
 
 def decode_workspace_bytes(batch: int, num_q_heads: int, head_dim: int, max_blocks: int, page_size: int,
                            chunks_per_split: int = 1) -> int:
-    """Workspace bytes the kernel needs for splits of ``chunks_per_split * 256`` positions (1: the most
-    parallel split; a smaller workspace makes the kernel pick longer splits)."""
+    """Workspace bytes the kernel needs for splits of ``chunks_per_split`` chunks of 256 positions
+    (1: the most parallel split; a smaller workspace makes the kernel pick longer splits)."""
     n = _lib.load().mas_paged_decode_attention_workspace_bytes(batch, num_q_heads, head_dim, max_blocks, page_size,
                                                                 chunks_per_split)
     if n < 0:

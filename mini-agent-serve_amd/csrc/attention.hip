@@ -40,7 +40,7 @@ struct DecodeArgs {
   const int32_t* block_tables;
   int64_t bt_stride, max_blocks;
   const int32_t* seq_lens;
-  int hq, group, log2_page, chunks_per_split, max_splits;
+  int hq, hk, group, log2_page, chunks_per_split, max_splits;
   float scale_log2;  // bmm1_scale * log2(e)
   float out_scale;   // bmm2_scale
   float* part_o;     // [batch][hq][max_splits][D]
@@ -79,28 +79,125 @@ __device__ __forceinline__ int64_t kv_row(const DecodeArgs& a, int b, int kvh, i
          static_cast<int64_t>(p & ((1 << a.log2_page) - 1)) * a.entry_stride + kvh * a.head_stride;
 }
 
-template <int GP, int D>
-__global__ __launch_bounds__(64) void decode_attn_split(DecodeArgs a) {
-  constexpr int KS = D / 32;     // MFMA k-steps per tile
-  constexpr int LPP = D / 8;     // P.V layout: lanes per position
-  constexpr int PPW = 64 / LPP;  // P.V layout: positions per wavefront step
-  constexpr int RG = GP / 4;     // MFMA result rows of 4 heads that hold query heads
-  constexpr int U = 32 / PPW;    // P.V: positions per lane per load group (32 per wavefront)
-  constexpr int TG = KS <= 4 ? 4 : 2;  // pass 1: tiles per load group (KS * TG 16-byte loads in flight)
-  __shared__ __align__(16) float p_lds[kChunk * GP];  // softmax numerators, [position][head]
-  __shared__ int64_t row_lds[kChunk];                 // each chunk position's row offset, -1 if masked
-  __shared__ float alpha_lds[GP];                     // rescale of the running O for this chunk
+// Key loads: a wavefront's load instruction reads 64 bytes of each of 16 key rows, so the other
+// half of each 128-byte line comes with the next instruction; value loads read whole rows.
+#ifndef MAS_ATTN_K_NT
+#define MAS_ATTN_K_NT 0
+#endif
+#ifndef MAS_ATTN_V_NT
+#define MAS_ATTN_V_NT 1
+#endif
+__device__ __forceinline__ u32x4 attn_load_k(const uint16_t* p) {
+  if constexpr (MAS_ATTN_K_NT) return load_stream(p);
+  return load_cached(p);
+}
+__device__ __forceinline__ u32x4 attn_load_v(const uint16_t* p) {
+  if constexpr (MAS_ATTN_V_NT) return load_stream(p);
+  return load_cached(p);
+}
 
-  const int lane = threadIdx.x;
-  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+// Wavefronts per workgroup of the split kernel: consecutive kv heads of one split, so one CU reads
+// whole 2 KB position blocks ([kv head][head dim]) together. Each wavefront works on its own; LDS
+// traffic is ordered within the wavefront only.
+#ifndef MAS_ATTN_WG_WAVES
+#define MAS_ATTN_WG_WAVES 1
+#endif
+constexpr int kAttnWaves = MAS_ATTN_WG_WAVES;
+
+// Orders this wavefront's LDS writes before its later reads (and reads before later writes).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// One step: 32 positions - two MFMA tiles of keys, and the value rows in the 16-byte layout.
+template <int D>
+struct StepLoads {
+  static constexpr int KS = D / 32;
+  static constexpr int VPS = 32 / (64 / (D / 8));  // value rows per lane per step
+  u32x4 k[2][KS];
+  u32x4 v[VPS];
+  bool kok[2];
+  bool vok[VPS];
+};
+
+// Issues the key and value loads of the step at position ps. Page ids come from pg (the chunk's
+// block-table entries in LDS, first = the chunk's first block index); rows of masked positions
+// (past `end`, or with a page id outside the cache) are loaded from row 0 of page 0 and flagged.
+template <int D>
+__device__ __forceinline__ void issue_step(const DecodeArgs& a, StepLoads<D>& st, int ps, int end, int kvh,
+                                           const int32_t* pg, int first, int n, int r, int pv_d, int pv_grp) {
+  constexpr int PPW = 64 / (D / 8);
+  const int mask = (1 << a.log2_page) - 1;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int p = ps + 16 * t + n;
+    const bool valid = p < end;
+    const int pc = valid ? p : end - 1;
+    const int32_t page = pg[(pc >> a.log2_page) - first];
+    const bool ok = page >= 0 && page < a.num_pages;
+    if (valid && !ok && r == 0) report(a.err, MAS_ERRBIT_PAGE);
+    st.kok[t] = valid && ok;
+    const int64_t row = (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
+                        static_cast<int64_t>(pc & mask) * a.entry_stride + kvh * a.head_stride;
+#pragma unroll
+    for (int ks = 0; ks < StepLoads<D>::KS; ++ks) st.k[t][ks] = attn_load_k(a.k_cache + row + 32 * ks + 8 * r);
+  }
+#pragma unroll
+  for (int u = 0; u < StepLoads<D>::VPS; ++u) {
+    const int p = ps + PPW * u + pv_grp;
+    const bool valid = p < end;
+    const int pc = valid ? p : end - 1;
+    const int32_t page = pg[(pc >> a.log2_page) - first];
+    const bool ok = page >= 0 && page < a.num_pages;
+    st.vok[u] = valid && ok;
+    const int64_t row = (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
+                        static_cast<int64_t>(pc & mask) * a.entry_stride + kvh * a.head_stride;
+    st.v[u] = attn_load_v(a.v_cache + row + 8 * pv_d);
+  }
+}
+
+// One wavefront per (kv head, split, row); a split is chunks_per_split chunks of 256 positions,
+// walked in steps of 32 with the next step's loads in flight (head_dim <= 128). Per step:
+// Q.K^T on MFMA -> online softmax (the running max, sum and O rescale live in the MFMA result
+// layout: lane (n, r) holds heads 4r..4r+3) -> P and the value rows through LDS, where they are
+// read back transposed as MFMA operands -> P.V on MFMA (16x16x32: the 32 positions of the step are
+// the reduction). P enters as two bf16 terms, hi = bf16(P) and lo = bf16(P - hi), two MFMAs per
+// tile, so it keeps ~16 significant bits (one bf16 term alone rounds it to 8). O stays in
+// 4 * D / 16 accumulator registers whatever the group size.
+template <int GP, int D>
+__global__ __launch_bounds__(64 * kAttnWaves) void decode_attn_split(DecodeArgs a) {
+  constexpr int KS = D / 32;
+  constexpr int DT = D / 16;               // MFMA tiles over the head dim for P.V
+  constexpr int LPP = D / 8;               // value-row layout: lanes per row
+  constexpr int PPW = 64 / LPP;            // value-row layout: rows per wavefront load
+  constexpr int kStep = 32;
+  constexpr int VPS = kStep / PPW;
+  constexpr int RG = GP / 4;
+  constexpr bool kPrefetch = D <= 128;
+  constexpr int VROW = D + 4;              // bf16 per LDS value row: rows 8 apart start 16 banks apart
+  constexpr int PROW = kStep + 8;          // bf16 per LDS P row: 16-byte aligned, conflict-free reads
+  constexpr int kChunkPages = 257;         // block-table entries one 256-position chunk can touch
+  __shared__ __align__(16) uint16_t v_lds_all[kAttnWaves][kStep * VROW];
+  __shared__ __align__(16) uint16_t p_lds_all[kAttnWaves][2][16 * PROW];  // P as hi and lo bf16 terms
+  __shared__ int32_t pg_lds_all[kAttnWaves][kChunkPages];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id_uniform();
+  const int kvh = blockIdx.x * kAttnWaves + wave;  // kv heads adjacent: one 2 KB position block
+  const int split = blockIdx.y, b = blockIdx.z;
+  if (kvh >= a.hk) return;
+  uint16_t* v_lds = v_lds_all[wave];
+  uint16_t(*p_lds)[16 * PROW] = p_lds_all[wave];
+  int32_t* pg_lds = pg_lds_all[wave];
   const int L = kv_len(a, b);
   const int start = split * a.chunks_per_split * kChunk;
   if (start >= L) return;
   const int end = min(start + a.chunks_per_split * kChunk, L);
   const int G = a.group;
   const int n = lane & 15, r = lane >> 4;
+  const int pv_d = lane % LPP, pv_grp = lane / LPP;
 
-  // A operand: query head (lane & 15) of this kv head's group, k = 32 * ks + 8 * (lane >> 4) + 0..7.
   bf16x8 qa[KS];
   {
     const int g = n < G ? n : 0;
@@ -113,145 +210,138 @@ __global__ __launch_bounds__(64) void decode_attn_split(DecodeArgs a) {
     }
   }
 
-  float m_run[4], l_run[4];  // score layout: head 4 * r + i
+  // The block-table entries of the chunk starting at cs, into LDS (clamped to the table).
+  const int32_t* bt = a.block_tables + b * a.bt_stride;
+  auto load_pages = [&](int cs) {
+    const int first = cs >> a.log2_page;
+    const int last = min((cs + kChunk - 1) >> a.log2_page, static_cast<int>(a.max_blocks) - 1);
+    for (int i = lane; i <= last - first; i += 64) pg_lds[i] = bt[first + i];
+    wave_lds_sync();
+    return first;
+  };
+
+  float m_run[4], l_run[4];
+  f32x4 acc[DT];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     m_run[i] = kNegInf;
     l_run[i] = 0.f;
   }
-  float o[GP][8];  // P.V layout: head g, head-dim 8 * (lane % LPP) + e
 #pragma unroll
-  for (int g = 0; g < GP; ++g)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[g][e] = 0.f;
-  const int pv_d = lane % LPP, pv_grp = lane / LPP;
+  for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int cstart = start; cstart < end; cstart += kChunk) {
-    __syncthreads();  // the previous chunk's P.V reads are done before the LDS is rewritten
-
-    // ---- pass 1: scores, TG tiles of 16 positions per load group; lane holds heads 4r+i at
-    // position cstart + 16 t + n (the MFMA result layout).
-    f32x4 s[kTiles];
-#pragma unroll
-    for (int t0 = 0; t0 < kTiles; t0 += TG) {
-      int64_t rows[TG];
-      bool oks[TG];
-#pragma unroll
-      for (int j = 0; j < TG; ++j) {
-        const int p = cstart + 16 * (t0 + j) + n;
-        const bool valid = p < end;
-        bool ok;
-        rows[j] = kv_row(a, b, kvh, valid ? p : end - 1, &ok);
-        if (valid && !ok && r == 0) report(a.err, MAS_ERRBIT_PAGE);
-        oks[j] = valid && ok;
-      }
-      u32x4 kb[TG][KS];
-#pragma unroll
-      for (int j = 0; j < TG; ++j)
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) kb[j][ks] = load_stream(a.k_cache + rows[j] + 32 * ks + 8 * r);
-      load_fence();
-#pragma unroll
-      for (int j = 0; j < TG; ++j) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[ks], __builtin_bit_cast(bf16x8, kb[j][ks]), acc, 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s[t0 + j][i] = oks[j] ? acc[i] * a.scale_log2 : kNegInf;
-        if (r == 0) row_lds[16 * (t0 + j) + n] = oks[j] ? rows[j] : -1;
+  const int nsteps = (end - start + kStep - 1) / kStep;
+  int first = load_pages(start);
+  StepLoads<D> cur, nxt;
+  issue_step<D>(a, cur, start, end, kvh, pg_lds, first, n, r, pv_d, pv_grp);
+  for (int i = 0; i < nsteps; ++i) {
+    const int ps = start + i * kStep;
+    if constexpr (kPrefetch) {
+      if (i + 1 < nsteps) {
+        if (((i + 1) & 7) == 0) first = load_pages(ps + kStep);  // the next step opens a new chunk
+        issue_step<D>(a, nxt, ps + kStep, end, kvh, pg_lds, first, n, r, pv_d, pv_grp);
       }
     }
 
-    // ---- softmax over the chunk, merged into the split's running max and sum
+    // ---- scores (lane: heads 4r+i at positions ps + 16 t + n)
+    f32x4 s[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float mx = kNegInf;
+    for (int t = 0; t < 2; ++t) {
+      f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int t = 0; t < kTiles; ++t) mx = fmaxf(mx, s[t][i]);
-      mx = row_max16(mx);
-      const float m_new = fmaxf(m_run[i], mx);
+      for (int ks = 0; ks < KS; ++ks)
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[ks], __builtin_bit_cast(bf16x8, cur.k[t][ks]), c, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s[t][j] = cur.kok[t] ? c[j] * a.scale_log2 : kNegInf;
+    }
+
+    // ---- online softmax; O (same layout) rescaled by alpha
+    wave_lds_sync();  // the previous step's LDS reads are done
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float mx = row_max16(fmaxf(s[0][j], s[1][j]));
+      const float m_new = fmaxf(m_run[j], mx);
       const float m_use = m_new == kNegInf ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run[i] - m_use);
-      float sum = 0.f;
+      const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_use);
+      s[0][j] = __builtin_amdgcn_exp2f(s[0][j] - m_use);
+      s[1][j] = __builtin_amdgcn_exp2f(s[1][j] - m_use);
+      l_run[j] = l_run[j] * alpha + row_sum16(s[0][j] + s[1][j]);
+      m_run[j] = m_new;
 #pragma unroll
-      for (int t = 0; t < kTiles; ++t) {
-        s[t][i] = __builtin_amdgcn_exp2f(s[t][i] - m_use);
-        sum += s[t][i];
+      for (int dt = 0; dt < DT; ++dt) acc[dt][j] *= alpha;
+      if (r < RG) {
+        const uint32_t hi = pack_bf16x2(s[0][j], s[1][j]);
+        const uint32_t lo = pack_bf16x2(s[0][j] - bf16_lo(hi), s[1][j] - bf16_hi(hi));
+        uint16_t* row_hi = p_lds[0] + (4 * r + j) * PROW;
+        uint16_t* row_lo = p_lds[1] + (4 * r + j) * PROW;
+        row_hi[n] = static_cast<uint16_t>(hi);
+        row_hi[16 + n] = static_cast<uint16_t>(hi >> 16);
+        row_lo[n] = static_cast<uint16_t>(lo);
+        row_lo[16 + n] = static_cast<uint16_t>(lo >> 16);
       }
-      l_run[i] = l_run[i] * alpha + row_sum16(sum);
-      m_run[i] = m_new;
-      if (n == 0 && r < RG) alpha_lds[4 * r + i] = alpha;
     }
-    if (r < RG) {
+    // value rows into LDS (masked rows zeroed)
 #pragma unroll
-      for (int t = 0; t < kTiles; ++t) *reinterpret_cast<f32x4*>(&p_lds[(16 * t + n) * GP + 4 * r]) = s[t];
+    for (int u = 0; u < VPS; ++u) {
+      const u32x4 v = cur.vok[u] ? cur.v[u] : u32x4{0u, 0u, 0u, 0u};
+      uint16_t* dst = v_lds + (PPW * u + pv_grp) * VROW + 8 * pv_d;
+      *reinterpret_cast<u32x2*>(dst) = u32x2{v[0], v[1]};
+      *reinterpret_cast<u32x2*>(dst + 4) = u32x2{v[2], v[3]};
     }
-    __syncthreads();
+    wave_lds_sync();
 
-    // ---- pass 2: P.V; masked positions have P = 0 and their (in-bounds) value row zeroed
+    // ---- P.V: A = P[head][32 positions], B = V[32 positions][16 of the head dim], per dim tile
+    const bf16x8 pa_hi = *reinterpret_cast<const bf16x8*>(p_lds[0] + n * PROW + 8 * r);
+    const bf16x8 pa_lo = *reinterpret_cast<const bf16x8*>(p_lds[1] + n * PROW + 8 * r);
 #pragma unroll
-    for (int g = 0; g < GP; ++g) {
-      const float al = alpha_lds[g];
+    for (int dt = 0; dt < DT; ++dt) {
+      uint16_t e[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[g][e] *= al;
+      for (int j = 0; j < 8; ++j) e[j] = v_lds[(8 * r + j) * VROW + 16 * dt + n];
+      const u32x4 packed = {e[0] | (static_cast<uint32_t>(e[1]) << 16), e[2] | (static_cast<uint32_t>(e[3]) << 16),
+                            e[4] | (static_cast<uint32_t>(e[5]) << 16), e[6] | (static_cast<uint32_t>(e[7]) << 16)};
+      const bf16x8 vb = __builtin_bit_cast(bf16x8, packed);
+      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa_lo, vb, acc[dt], 0, 0, 0);
+      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa_hi, vb, acc[dt], 0, 0, 0);
     }
-    const int npos = min(kChunk, end - cstart);
-    for (int j0 = 0; j0 < npos; j0 += 32) {
-      int64_t vrow[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) vrow[u] = row_lds[j0 + PPW * u + pv_grp];
-      u32x4 vv[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) vv[u] = load_stream(a.v_cache + (vrow[u] >= 0 ? vrow[u] : 0) + 8 * pv_d);
-      load_fence();
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int pl = j0 + PPW * u + pv_grp;
-        if (vrow[u] < 0) vv[u] = u32x4{0u, 0u, 0u, 0u};
-        float vf[8];
-        unpack8(vv[u], vf);
-        const float* prow = &p_lds[pl * GP];
-#pragma unroll
-        for (int g = 0; g < GP; ++g) {
-          const float pg = prow[g];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) o[g][e] = __builtin_fmaf(pg, vf[e], o[g][e]);
-        }
-      }
+
+    if constexpr (kPrefetch) {
+      cur = nxt;
+    } else if (i + 1 < nsteps) {
+      if (((i + 1) & 7) == 0) first = load_pages(ps + kStep);
+      issue_step<D>(a, cur, ps + kStep, end, kvh, pg_lds, first, n, r, pv_d, pv_grp);
     }
   }
 
-  // ---- sum O over the PPW position groups, then write the split's partials
-#pragma unroll
-  for (int off = LPP; off < 64; off <<= 1)
-#pragma unroll
-    for (int g = 0; g < GP; ++g)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[g][e] += __shfl_xor(o[g][e], off);
+  // ---- partials: lane (n, r) holds O[head 4r+j][16 dt + n]
   const int64_t base = (static_cast<int64_t>(b) * a.hq + kvh * G) * a.max_splits + split;
-  if (lane < LPP) {
 #pragma unroll
-    for (int g = 0; g < GP; ++g) {
-      if (g < G) {
-        float* dst = a.part_o + (base + static_cast<int64_t>(g) * a.max_splits) * D + 8 * lane;
-        *reinterpret_cast<f32x4*>(dst) = f32x4{o[g][0], o[g][1], o[g][2], o[g][3]};
-        *reinterpret_cast<f32x4*>(dst + 4) = f32x4{o[g][4], o[g][5], o[g][6], o[g][7]};
-      }
-    }
-  }
-  if (n == 0) {
+  for (int j = 0; j < 4; ++j) {
+    const int g = 4 * r + j;
+    if (g < G) {
+      float* dst = a.part_o + (base + static_cast<int64_t>(g) * a.max_splits) * D + n;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int g = 4 * r + i;
-      if (g < G) {
+      for (int dt = 0; dt < DT; ++dt) dst[16 * dt] = acc[dt][j];
+      if (n == 0) {
         *reinterpret_cast<f32x2*>(a.part_ml + (base + static_cast<int64_t>(g) * a.max_splits) * 2) =
-            f32x2{m_run[i], l_run[i]};
+            f32x2{m_run[j], l_run[j]};
       }
     }
   }
 }
 
+// Max over the 64 lanes of a wavefront.
+__device__ __forceinline__ float wave_max(float v) {
+  v = row_max16(v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// One wavefront per (query head, row): lane s reads split s's (max, sum) (64 splits per pass), the
+// weights are broadcast with readlane, and each lane accumulates D / 64 head-dim elements.
 template <int D>
 __global__ __launch_bounds__(64) void decode_attn_combine(DecodeArgs a) {
   constexpr int DPL = D / 64;  // head-dim elements per lane
@@ -264,21 +354,30 @@ __global__ __launch_bounds__(64) void decode_attn_combine(DecodeArgs a) {
   const int nsplit = (L + split_len - 1) / split_len;
   const int64_t base = (static_cast<int64_t>(b) * a.hq + h) * a.max_splits;
   float mx = kNegInf;
-  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, a.part_ml[(base + s) * 2]);
+  for (int s = lane; s < nsplit; s += 64) mx = fmaxf(mx, a.part_ml[(base + s) * 2]);
+  mx = wave_max(mx);
   float acc[DPL];
 #pragma unroll
   for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
-  float denom = 0.f;
+  float lsum = 0.f;
   if (mx != kNegInf) {
-    for (int s = 0; s < nsplit; ++s) {
-      const f32x2 ml = *reinterpret_cast<const f32x2*>(a.part_ml + (base + s) * 2);
-      const float w = __builtin_amdgcn_exp2f(ml[0] - mx);
-      denom += w * ml[1];
-      const float* po = a.part_o + (base + s) * D + DPL * lane;
+    for (int s0 = 0; s0 < nsplit; s0 += 64) {
+      float wgt = 0.f;
+      if (s0 + lane < nsplit) {
+        const f32x2 ml = *reinterpret_cast<const f32x2*>(a.part_ml + (base + s0 + lane) * 2);
+        wgt = __builtin_amdgcn_exp2f(ml[0] - mx);
+        lsum = __builtin_fmaf(wgt, ml[1], lsum);
+      }
+      const int cnt = min(64, nsplit - s0);
+      const float* po = a.part_o + (base + s0) * D + DPL * lane;
+      for (int j = 0; j < cnt; ++j) {
+        const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wgt), j));
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) acc[e] = __builtin_fmaf(w, po[e], acc[e]);
+        for (int e = 0; e < DPL; ++e) acc[e] = __builtin_fmaf(wj, po[j * D + e], acc[e]);
+      }
     }
   }
+  const float denom = wave_sum(lsum);
   const float scale = denom > 0.f ? a.out_scale / denom : 0.f;
   uint16_t* dst = a.out + b * a.out_stride + h * a.out_head_stride + DPL * lane;
   if constexpr (DPL == 1) {
@@ -294,8 +393,9 @@ __global__ __launch_bounds__(64) void decode_attn_combine(DecodeArgs a) {
 template <int GP, int D>
 int launch(const DecodeArgs& a, int64_t batch, int64_t hk, hipStream_t s) {
   hipLaunchKernelGGL((decode_attn_split<GP, D>),
-                     dim3(static_cast<uint32_t>(a.max_splits), static_cast<uint32_t>(hk), static_cast<uint32_t>(batch)),
-                     dim3(64), 0, s, a);
+                     dim3(static_cast<uint32_t>(cdiv(hk, kAttnWaves)), static_cast<uint32_t>(a.max_splits),
+                          static_cast<uint32_t>(batch)),
+                     dim3(64 * kAttnWaves), 0, s, a);
   if (const int st = launch_status(); st != MAS_OK) return st;
   hipLaunchKernelGGL((decode_attn_combine<D>), dim3(static_cast<uint32_t>(a.hq), static_cast<uint32_t>(batch)),
                      dim3(64), 0, s, a);
@@ -357,10 +457,14 @@ extern "C" int mas_paged_decode_attention_bf16(void* out, int64_t out_stride, in
 
   // The smallest split (most parallelism) whose partials fit the workspace.
   const int64_t chunks = cdiv(cap, kChunk);
-  int64_t per_split = 1;
+#ifndef MAS_ATTN_MIN_CHUNKS
+#define MAS_ATTN_MIN_CHUNKS 1
+#endif
+  int64_t per_split = MAS_ATTN_MIN_CHUNKS;
   while (per_split < chunks &&
-         mas_paged_decode_attention_workspace_bytes(batch, num_q_heads, head_dim, max_blocks, page_size, per_split) >
-             workspace_bytes)
+         (mas_paged_decode_attention_workspace_bytes(batch, num_q_heads, head_dim, max_blocks, page_size, per_split) >
+              workspace_bytes ||
+          cdiv(chunks, per_split) > 65535))
     per_split *= 2;
   if (per_split > chunks) per_split = chunks > 0 ? chunks : 1;
   if (mas_paged_decode_attention_workspace_bytes(batch, num_q_heads, head_dim, max_blocks, page_size, per_split) >
@@ -386,6 +490,7 @@ extern "C" int mas_paged_decode_attention_bf16(void* out, int64_t out_stride, in
   a.max_blocks = max_blocks;
   a.seq_lens = seq_lens;
   a.hq = static_cast<int>(num_q_heads);
+  a.hk = static_cast<int>(num_kv_heads);
   a.group = static_cast<int>(group);
   a.log2_page = log2_page;
   a.chunks_per_split = static_cast<int>(per_split);

@@ -16,7 +16,9 @@ import torch
 
 from .rope import cos_sin_cache
 
-__all__ = ["Shape", "SHAPES", "LayerInputs", "make_layer_inputs", "credited_bytes", "layer_credited_bytes"]
+__all__ = ["Shape", "SHAPES", "LayerInputs", "make_layer_inputs", "credited_bytes", "layer_credited_bytes",
+           "AttentionShape", "ATTENTION_SHAPES", "AttentionInputs", "make_attention_inputs",
+           "attention_credited_bytes"]
 
 
 @dataclass(frozen=True)
@@ -190,3 +192,75 @@ def credited_bytes(shape: Shape) -> dict[str, int]:
         "rope_append": 4 * n * heads * d + 4 * n + 6 * n * shape.kv_heads * d + 4 * n,
         "embedding": 4 * n * h + 8 * n,
     }
+
+
+# ---- paged decode attention -------------------------------------------------------------------------
+
+@dataclass(frozen=True)
+class AttentionShape:
+    name: str
+    batch: int                  # decode rows, one query token each
+    q_heads: int
+    kv_heads: int
+    head_dim: int
+    page_size: int
+    max_len: int                # seq_lens drawn uniformly from [1, max_len]; block-table width max_len / page_size
+
+
+ATTENTION_SHAPES: dict[str, AttentionShape] = {s.name: s for s in [
+    # Devstral-Small-2 decode attention: 64 rows, lengths up to 8192 (the runner's graph width,
+    # max_model_len 8192 / 256-slot blocks), 4 query heads per kv head
+    AttentionShape("decode_attn_64x8192_24b", 64, 32, 8, 128, 256, 8192),
+    # Devstral-2 123B: 12 query heads per kv head
+    AttentionShape("decode_attn_64x8192_123b", 64, 96, 8, 128, 256, 8192),
+]}
+
+
+@dataclass
+class AttentionInputs:
+    shape: AttentionShape
+    q: torch.Tensor             # [batch, Hq, D] bf16
+    k_cache: torch.Tensor       # [pages, page_size, Hk, D] bf16 (NHD)
+    v_cache: torch.Tensor
+    block_tables: torch.Tensor  # [batch, max_len / page_size] int32
+    seq_lens: torch.Tensor      # [batch] int32
+    workspace: torch.Tensor     # uint8, the reference's 128 MiB
+
+
+def make_attention_inputs(shape: AttentionShape | str, device="cpu", seed: int = 0) -> AttentionInputs:
+    """Each row gets ceil(len / page_size) distinct pages of a pool sized to hold them all (pages in
+    random order); caches, q ~ N(0, 1), drawn on ``device``."""
+    if isinstance(shape, str):
+        shape = ATTENTION_SHAPES[shape]
+    device = torch.device(device)
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(1, shape.max_len + 1, (shape.batch,), generator=g)
+    width = shape.max_len // shape.page_size
+    need = [-(-int(n) // shape.page_size) for n in lens]
+    pages = sum(need) + 1
+    perm = torch.randperm(pages, generator=g)
+    tables = torch.zeros(shape.batch, width, dtype=torch.int32)
+    at = 0
+    for b, k in enumerate(need):
+        tables[b, :k] = perm[at:at + k].to(torch.int32)
+        at += k
+    dg = torch.Generator(device=device).manual_seed(seed)
+    kv = (pages, shape.page_size, shape.kv_heads, shape.head_dim)
+    return AttentionInputs(
+        shape=shape,
+        q=torch.randn(shape.batch, shape.q_heads, shape.head_dim, generator=dg, device=device).bfloat16(),
+        k_cache=torch.randn(kv, generator=dg, device=device).bfloat16(),
+        v_cache=torch.randn(kv, generator=dg, device=device).bfloat16(),
+        block_tables=tables.to(device), seq_lens=lens.to(torch.int32).to(device),
+        workspace=torch.zeros(128 << 20, dtype=torch.uint8, device=device))
+
+
+def attention_credited_bytes(inputs: AttentionInputs) -> int:
+    """Each key and value row of every position read once (2 * Hk * D * 2 bytes per position), q
+    read and out written once, one block-table entry per page and one seq_len per row. The split
+    partials in the workspace are not credited."""
+    s = inputs.shape
+    lens = inputs.seq_lens.cpu().long()
+    positions = int(lens.sum())
+    pages = int(((lens + s.page_size - 1) // s.page_size).sum())
+    return positions * s.kv_heads * s.head_dim * 4 + 2 * s.batch * s.q_heads * s.head_dim * 2 + pages * 4 + s.batch * 4
