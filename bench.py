@@ -42,7 +42,8 @@ COLD_BYTES = 768 << 20         # working set cycled by the cold protocol (3x the
 # HBM bytes per launch of a workload's dominant kernel, from two rocprofv3 counter passes
 # (FETCH_SIZE, then WRITE_SIZE) over `bench.py --pmc-probe`, each calibrated by the same counter on
 # a 256 MiB device copy (fetch factor 1.9997, write factor 1.0000). Re-measure when the kernel changes.
-MEASURED_TRAFFIC = {("decode64_24b", "silu_and_mul"): 12_612_523}
+MEASURED_TRAFFIC = {("decode64_24b", "silu_and_mul"): 12_612_523,
+                    ("decode_attn_64x8192_24b", "paged_decode_attention"): 1_114_384_294}
 
 
 def parse_args():
@@ -485,6 +486,25 @@ def main() -> int:
 
 
 def attention_main(mas, args, shape, dev) -> int:
+    if args.pmc_probe:
+        # 5 calls of the op, then 4 copies of 256 MiB (the counters' calibration reference)
+        wl = mas.workloads
+        inp = wl.make_attention_inputs(shape, dev, seed=0)
+        out = torch.empty_like(inp.q)
+        for _ in range(5):
+            mas.attention.trtllm_batch_decode_with_kv_cache(inp.q, (inp.k_cache, inp.v_cache), inp.workspace,
+                                                            inp.block_tables, inp.seq_lens, 0,
+                                                            shape.head_dim ** -0.5, 1.0, out=out)
+        torch.cuda.synchronize()
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"pmc_probe": "paged_decode_attention", "launches": 5,
+                          "bytes_per_launch": wl.attention_credited_bytes(inp),
+                          "calibration_copy_bytes": 256 << 20}), flush=True)
+        return 0
     res = run_attention_workload(mas, args, shape, dev)
     dom_gbs = res["dominant_bytes"] / res["dominant_us"] / 1e3
     line = {
@@ -498,7 +518,8 @@ def attention_main(mas, args, shape, dev) -> int:
         "frac_of_peak": round(res["value"] / PEAK_HBM_GBS, 4),
         "ops": res["ops"],
         "roofline": {"bound": "hbm", "kernel": res["dominant"], "achieved": round(dom_gbs, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(dom_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(dom_gbs / PEAK_HBM_GBS, 4),
+                     "traffic": MEASURED_TRAFFIC.get((shape.name, res["dominant"])),
                      "bytes_per_launch": res["dominant_bytes"], "avg_launch_us": round(res["dominant_us"], 3)},
         "copy_ceiling_GBps": round(copy_ceiling_gbs(dev), 1),
     }
