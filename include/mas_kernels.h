@@ -232,6 +232,30 @@ int mas_paged_decode_attention_bf16(void* out, int64_t out_stride, int64_t out_h
                                     void* workspace, int64_t workspace_bytes, uint32_t* err, hipStream_t stream);
 
 /*
+ * Paged causal attention of prompt rows (context / chunked prefill): row j owns query tokens
+ * [cu_seqlens_q[j], cu_seqlens_q[j + 1]) (q_len) of q and out ([tokens, num_q_heads, head_dim],
+ * row / head strides) and seq_lens[j] = kv_len positions in the cache, the last q_len of them its
+ * own tokens: token i sits at position kv_len - q_len + i and attends to positions 0..that.
+ * For query head h (kv head h / (num_q_heads / num_kv_heads)):
+ *   out[t, h] = bmm2_scale * sum_p softmax_p(bmm1_scale * q[t, h] . k_p) * v_p
+ * with fp32 accumulation and P rounded to bf16 for the P.V product. max_q_len bounds q_len (it
+ * sizes the grid). head_dim 64 or 128; page_size a power of two. A seq_len outside
+ * [q_len, max_blocks * page_size] is clamped (MAS_ERRBIT_POSITION; tokens left before position 0
+ * get zeros); a page id outside [0, num_pages) skips its position (MAS_ERRBIT_PAGE).
+ * Replaces flashinfer.prefill.trtllm_batch_context_with_kv_cache at
+ * miniagentserve/models/devstral2/devstral2.py:198-213 (kv_layout "NHD", no sliding window).
+ */
+int mas_paged_context_attention_bf16(void* out, int64_t out_stride, int64_t out_head_stride, const void* q,
+                                     int64_t q_stride, int64_t q_head_stride, const void* k_cache,
+                                     const void* v_cache, int64_t page_stride, int64_t entry_stride,
+                                     int64_t head_stride, int64_t num_pages, int64_t page_size,
+                                     const int32_t* block_tables, int64_t block_table_stride, int64_t max_blocks,
+                                     const int32_t* seq_lens, const int32_t* cu_seqlens_q, int64_t num_rows,
+                                     int64_t max_q_len, int64_t num_q_heads, int64_t num_kv_heads,
+                                     int64_t head_dim, float bmm1_scale, float bmm2_scale, uint32_t* err,
+                                     hipStream_t stream);
+
+/*
  * Workspace bytes mas_paged_decode_attention_bf16 needs when each split covers chunks_per_split
  * chunks of 256 positions (1: the most parallel split). -1 for invalid arguments.
  * No counterpart in the reference (its caller passes a fixed 128 MiB workspace,

@@ -151,6 +151,20 @@ def _(query, k_cache, v_cache, workspace, block_tables, seq_lens, bmm1_scale, bm
     return None
 
 
+@custom_op("mas::paged_context_attention", mutates_args=("out",))
+def _paged_context_attention(query: Tensor, k_cache: Tensor, v_cache: Tensor, block_tables: Tensor, seq_lens: Tensor,
+                             cu_seqlens_q: Tensor, max_q_len: int, bmm1_scale: float, bmm2_scale: float, out: Tensor,
+                             kv_layout: str) -> None:
+    attention._context(query, (k_cache, v_cache), block_tables, seq_lens, cu_seqlens_q, max_q_len, bmm1_scale,
+                       bmm2_scale, out, kv_layout, None)
+
+
+@_paged_context_attention.register_fake
+def _(query, k_cache, v_cache, block_tables, seq_lens, cu_seqlens_q, max_q_len, bmm1_scale, bmm2_scale, out,
+      kv_layout):
+    return None
+
+
 @custom_op("mas::apply_rope_and_append_paged_kv_cache", mutates_args=("query", "key", "k_cache", "v_cache"))
 def _rope_append(positions: Tensor, query: Tensor, key: Tensor, value: Tensor, head_size: int, cos_sin_cache: Tensor,
                  is_neox: bool, batch_indices: Tensor, k_cache: Tensor, v_cache: Tensor, kv_indices: Tensor,

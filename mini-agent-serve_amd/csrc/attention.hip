@@ -8,14 +8,14 @@
 // in fp32 from the bf16 inputs, rounded once to bf16.
 //
 // Split-KV in two kernels:
-//  1. decode_attn_split - one wavefront per (split of chunks_per_split * 256 positions, kv head,
-//     row). Per 256-position chunk: Q.K^T on MFMA (v_mfma_f32_16x16x32_bf16: the kv head's G
-//     query heads are the rows of A, zero-padded to 16; a tile of 16 positions is the columns of B,
-//     each lane reading a 16-byte slice of one key row straight from the cache), then the exact
-//     max / exp / sum over the chunk in registers with DPP row reductions, merged into the split's
-//     running (max, sum), then P.V on the vector ALUs with each lane reading 16-byte slices of value
-//     rows (D / 8 lanes per position). The split writes its (max, sum) and unnormalised O to the
-//     caller's workspace.
+//  1. decode_attn_split - one wavefront per (kv head, split of chunks_per_split * 256 positions,
+//     row), kv heads adjacent in the grid so that the 256-byte slices of each 2 KB position block
+//     are read close together. The split is walked in steps of 32 positions with the next step's
+//     key and value loads in flight: Q.K^T on MFMA (v_mfma_f32_16x16x32_bf16; the kv head's G
+//     query heads are the rows of A, zero-padded to 16; 16 positions per tile are the
+//     columns of B, read straight from the cache rows), an online softmax in the MFMA result
+//     layout, then P.V on MFMA with P and the value rows passed through LDS (read back
+//     transposed). The split's running (max, sum) and unnormalised O go to the caller's workspace.
 //  2. decode_attn_combine - one wavefront per (query head, row) merges the splits and writes bf16.
 // Scores live in the log2 domain (bmm1_scale * log2 e folded in), so every exponential is one
 // v_exp_f32. A position whose page id is out of range is skipped (MAS_ERRBIT_PAGE); seq_lens past
@@ -28,7 +28,6 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kChunk = 256;          // positions per chunk
-constexpr int kTiles = kChunk / 16;  // MFMA tiles of 16 positions per chunk
 constexpr float kNegInf = -__builtin_huge_valf();
 
 struct DecodeArgs {
@@ -69,14 +68,6 @@ __device__ __forceinline__ int kv_len(const DecodeArgs& a, int b) {
   const int64_t L = a.seq_lens[b];
   const int64_t cap = a.max_blocks << a.log2_page;
   return static_cast<int>(L < 0 ? 0 : (L > cap ? cap : L));
-}
-
-// Element offset of position p's row for kv head kvh; page 0 (in bounds) when the page id is not.
-__device__ __forceinline__ int64_t kv_row(const DecodeArgs& a, int b, int kvh, int p, bool* ok) {
-  const int32_t page = a.block_tables[b * a.bt_stride + (p >> a.log2_page)];
-  *ok = page >= 0 && page < a.num_pages;
-  return (*ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
-         static_cast<int64_t>(p & ((1 << a.log2_page) - 1)) * a.entry_stride + kvh * a.head_stride;
 }
 
 // Key loads: a wavefront's load instruction reads 64 bytes of each of 16 key rows, so the other

@@ -1,0 +1,332 @@
+// context_attention.hip - causal paged attention of prompt rows over the KV cache.
+//
+// Semantics: flashinfer.prefill.trtllm_batch_context_with_kv_cache as called at
+// miniagentserve/models/devstral2/devstral2.py:198-213. Prompt row j owns query tokens
+// [cu_seqlens_q[j], cu_seqlens_q[j + 1]) (q_len of them) and seq_lens[j] cached + new positions
+// (kv_len); query token i sits at position kv_len - q_len + i and attends to the positions
+// 0..that, whose key / value rows are at page = block_tables[j, p / page_size],
+// entry = p % page_size. For query head h (kv head h / G):
+//   out[t, h] = bmm2_scale * sum_p softmax_p(bmm1_scale * q[t, h] . k_p) * v_p,
+// fp32 accumulation, P rounded to bf16 for the P.V product (as flash-attention kernels do), the
+// output rounded once to bf16.
+//
+// One workgroup of four wavefronts per (kv head, head group, token tile, prompt row). Each wavefront
+// owns 32 query rows: 32 consecutive tokens of one query head; the four wavefronts cover up to four
+// heads of the kv head's group (or, for groups of 1 or 2, more tokens of fewer heads), so every
+// 64-position key / value tile they stage in LDS serves 128 query rows. Per tile:
+//   S^T = K Q^T on MFMA (v_mfma_f32_16x16x32_bf16; A = 16 key rows read from LDS, B = the
+//   wavefront's query rows, held in registers), causal mask, online softmax per query row, then
+//   O^T += V^T P^T on MFMA, where P^T is packed to bf16 straight from the S^T accumulators and V^T
+//   is stored transposed in LDS, its columns in the order that packing implies.
+// The next tile's key and value loads are issued before the current tile's arithmetic.
+#include "device.h"
+
+namespace mas {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTileP = 64;        // key positions per tile
+constexpr int kRowsPerWave = 32;  // query rows (tokens of one head) per wavefront
+constexpr float kNegInf = -__builtin_huge_valf();
+
+struct ContextArgs {
+  const uint16_t* q;
+  int64_t q_stride, q_head_stride;
+  const uint16_t* k_cache;
+  const uint16_t* v_cache;
+  int64_t page_stride, entry_stride, head_stride, num_pages;
+  const int32_t* block_tables;
+  int64_t bt_stride, max_blocks;
+  const int32_t* seq_lens;
+  const int32_t* cu_seqlens_q;
+  int hq, hk, group, heads_per_wg, log2_page;
+  float scale_log2;
+  float out_scale;
+  uint16_t* out;
+  int64_t out_stride, out_head_stride;
+  uint32_t* err;
+};
+
+// Column of position p (0..63) of a tile in the transposed value rows: P.V k-step s = p / 32 takes
+// its 32 positions in the order the S^T accumulators pack them (lane group r, element j):
+// j < 4 -> position 16 * 0 + 4 r + j of the step, j >= 4 -> position 16 + 4 r + (j - 4).
+__device__ __forceinline__ int vt_column(int p) {
+  const int s = p >> 5, q = p & 31, half = q >> 4, rem = q & 15;
+  return 32 * s + 8 * (rem >> 2) + 4 * half + (rem & 3);
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void context_attn(ContextArgs a) {
+  constexpr int KS = D / 32;            // MFMA k-steps over the head dim (S^T)
+  constexpr int DT = D / 16;            // MFMA tiles over the head dim (O^T)
+  constexpr int KROW = D + 8;           // bf16 per LDS key row (+16 B: conflict-free A reads)
+  constexpr int VTROW = kTileP + 8;     // bf16 per LDS transposed value row (+16 B)
+  constexpr int CPR = D / 8;            // 16-byte chunks per key / value row
+  constexpr int LOADS = kTileP * CPR / 256;  // 16-byte chunks per thread per tile, each of K and V
+  __shared__ __align__(16) uint16_t k_lds[kTileP * KROW];
+  __shared__ __align__(16) uint16_t vt_lds[D * VTROW];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id_uniform();
+  const int n = lane & 15, r = lane >> 4;
+  const int hgroups = (a.group + a.heads_per_wg - 1) / a.heads_per_wg;
+  const int kvh = blockIdx.x / hgroups, hg = blockIdx.x - kvh * hgroups;
+  const int row = blockIdx.z;
+  const int q0 = a.cu_seqlens_q[row], q_len = a.cu_seqlens_q[row + 1] - q0;
+  const int tokens_per_wg = kRowsPerWave * (4 / a.heads_per_wg);
+  const int tile_tok = blockIdx.y * tokens_per_wg;
+  if (tile_tok >= q_len) return;  // uniform over the workgroup
+  // kv_len clamped to the block table's reach; a kv_len below q_len leaves the first tokens with
+  // negative positions: they see no key and get zeros.
+  const int64_t cap = a.max_blocks << a.log2_page;
+  const int64_t raw_len = a.seq_lens[row];
+  if ((raw_len < q_len || raw_len > cap) && tid == 0 && blockIdx.x == 0 && blockIdx.y == 0)
+    report(a.err, MAS_ERRBIT_POSITION);
+  const int kv_len = static_cast<int>(raw_len < 0 ? 0 : (raw_len > cap ? cap : raw_len));
+  const int shift = kv_len - q_len;  // position of query token i = shift + i
+
+  // This wavefront's head and tokens.
+  const int hsub = wave % a.heads_per_wg;
+  const int g = hg * a.heads_per_wg + hsub;
+  const bool head_ok = g < a.group;
+  const int h = kvh * a.group + (head_ok ? g : 0);
+  const int tok = tile_tok + kRowsPerWave * (wave / a.heads_per_wg);  // first of 32 tokens
+  const bool wave_live = head_ok && tok < q_len;
+
+  // B operands: query rows tok + 16 nt + n, head-dim 32 ks + 8 r + 0..7 (zero past q_len).
+  bf16x8 qb[2][KS];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int t = tok + 16 * nt + n;
+    const bool ok = wave_live && t < q_len;
+    const uint16_t* src = a.q + static_cast<int64_t>(q0 + (ok ? t : 0)) * a.q_stride + h * a.q_head_stride + 8 * r;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      u32x4 v = load_cached(src + 32 * ks);
+      if (!ok) v = u32x4{0u, 0u, 0u, 0u};
+      qb[nt][ks] = __builtin_bit_cast(bf16x8, v);
+    }
+  }
+
+  // Causal reach of the workgroup: positions 0 .. shift + last token.
+  const int last_tok = min(tile_tok + tokens_per_wg, q_len) - 1;
+  const int reach = shift + last_tok + 1;  // <= kv_len
+  const int ntiles = reach > 0 ? (reach + kTileP - 1) / kTileP : 0;
+
+  float m_run[2], l_run[2];  // per query row (lane n of row tile nt)
+  f32x4 acc[2][DT];          // O^T: lane (n, r) holds O[row 16 nt + n][16 dt + 4 r + i]
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    m_run[nt] = kNegInf;
+    l_run[nt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[nt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const int32_t* bt = a.block_tables + row * a.bt_stride;
+  const int pmask = (1 << a.log2_page) - 1;
+  // Thread's chunks of a tile: chunk c = tid + 256 u -> position c / CPR, head-dim chunk c % CPR.
+  // (Rows past kv_len or on a page id outside the cache load row 0 of page 0 and are zeroed when
+  // stored; the flag is kept so that the loads themselves are not waited on here.)
+  u32x4 kst[LOADS], vst[LOADS];
+  bool lok[LOADS];
+  auto issue_tile = [&](int base) {
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int c = tid + 256 * u;
+      const int p = base + c / CPR;
+      const int pc = p < kv_len ? p : kv_len - 1;
+      const int32_t page = bt[pc >> a.log2_page];
+      const bool ok = page >= 0 && page < a.num_pages;
+      if (!ok && p < kv_len && (c % CPR) == 0) report(a.err, MAS_ERRBIT_PAGE);
+      const int64_t off = (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
+                          static_cast<int64_t>(pc & pmask) * a.entry_stride + kvh * a.head_stride + 8 * (c % CPR);
+      kst[u] = load_cached(a.k_cache + off);
+      vst[u] = load_cached(a.v_cache + off);
+      lok[u] = ok && p < kv_len;
+    }
+  };
+  if (ntiles > 0) issue_tile(0);
+
+  for (int it = 0; it < ntiles; ++it) {
+    const int base = it * kTileP;
+    __syncthreads();  // the previous tile's LDS reads are done
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int c = tid + 256 * u;
+      const int p = c / CPR, dc = c % CPR;
+      const u32x4 kv = lok[u] ? kst[u] : u32x4{0u, 0u, 0u, 0u};
+      const u32x4 vv = lok[u] ? vst[u] : u32x4{0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4*>(k_lds + p * KROW + 8 * dc) = kv;
+      const int col = vt_column(p);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vt_lds[(8 * dc + 2 * e) * VTROW + col] = static_cast<uint16_t>(vv[e]);
+        vt_lds[(8 * dc + 2 * e + 1) * VTROW + col] = static_cast<uint16_t>(vv[e] >> 16);
+      }
+    }
+    __syncthreads();
+    if (it + 1 < ntiles) issue_tile(base + kTileP);
+    if (!wave_live) continue;
+
+    // ---- S^T = K Q^T: lane (n, r) holds S[row 16 nt + n][position base + 16 pt + 4 r + i]
+    f32x4 s[4][2];
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) {
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) s[pt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const bf16x8 ka = *reinterpret_cast<const bf16x8*>(k_lds + (16 * pt + n) * KROW + 32 * ks + 8 * r);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+          s[pt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[nt][ks], s[pt][nt], 0, 0, 0);
+      }
+    }
+
+    // ---- causal mask and online softmax per query row
+    bf16x8 pb[2][2];  // B operands of P.V: [row tile][k-step of 32 positions]
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int qpos = shift + tok + 16 * nt + n;  // this lane's query row position
+      float mx = kNegInf;
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int kp = base + 16 * pt + 4 * r + i;
+          const float v = kp <= qpos && kp < kv_len ? s[pt][nt][i] * a.scale_log2 : kNegInf;
+          s[pt][nt][i] = v;
+          mx = fmaxf(mx, v);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m_run[nt], mx);
+      const float m_use = m_new == kNegInf ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_run[nt] - m_use);
+      float sum = 0.f;
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          s[pt][nt][i] = __builtin_amdgcn_exp2f(s[pt][nt][i] - m_use);
+          sum += s[pt][nt][i];
+        }
+      sum += __shfl_xor(sum, 16);
+      sum += __shfl_xor(sum, 32);
+      l_run[nt] = l_run[nt] * alpha + sum;
+      m_run[nt] = m_new;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) acc[nt][dt] *= alpha;
+      // k-step ks2 takes position tiles 2 ks2 (elements 0..3) and 2 ks2 + 1 (elements 4..7)
+#pragma unroll
+      for (int ks2 = 0; ks2 < 2; ++ks2) {
+        const f32x4 lo = s[2 * ks2][nt], hi = s[2 * ks2 + 1][nt];
+        const u32x4 packed = {pack_bf16x2(lo[0], lo[1]), pack_bf16x2(lo[2], lo[3]), pack_bf16x2(hi[0], hi[1]),
+                              pack_bf16x2(hi[2], hi[3])};
+        pb[nt][ks2] = __builtin_bit_cast(bf16x8, packed);
+      }
+    }
+
+    // ---- O^T += V^T P^T: A = V^T[16 dims][32 positions] from LDS, B = P^T
+#pragma unroll
+    for (int ks2 = 0; ks2 < 2; ++ks2) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const bf16x8 va = *reinterpret_cast<const bf16x8*>(vt_lds + (16 * dt + n) * VTROW + 32 * ks2 + 8 * r);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+          acc[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[nt][ks2], acc[nt][dt], 0, 0, 0);
+      }
+    }
+  }
+
+  if (!wave_live) return;
+  // ---- out[token][h][16 dt + 4 r + i] = O / l * bmm2_scale
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int t = tok + 16 * nt + n;
+    if (t >= q_len) continue;
+    const float sc = l_run[nt] > 0.f ? a.out_scale / l_run[nt] : 0.f;
+    uint16_t* dst = a.out + static_cast<int64_t>(q0 + t) * a.out_stride + h * a.out_head_stride + 4 * r;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const f32x4 o = acc[nt][dt];
+      *reinterpret_cast<u32x2*>(dst + 16 * dt) = u32x2{pack_bf16x2(o[0] * sc, o[1] * sc), pack_bf16x2(o[2] * sc, o[3] * sc)};
+    }
+  }
+}
+
+}  // namespace
+}  // namespace mas
+
+extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, int64_t out_head_stride, const void* q,
+                                                int64_t q_stride, int64_t q_head_stride, const void* k_cache,
+                                                const void* v_cache, int64_t page_stride, int64_t entry_stride,
+                                                int64_t head_stride, int64_t num_pages, int64_t page_size,
+                                                const int32_t* block_tables, int64_t block_table_stride,
+                                                int64_t max_blocks, const int32_t* seq_lens,
+                                                const int32_t* cu_seqlens_q, int64_t num_rows, int64_t max_q_len,
+                                                int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                                                float bmm1_scale, float bmm2_scale, uint32_t* err,
+                                                hipStream_t stream) {
+  using namespace mas;
+  if (num_rows < 0 || max_q_len < 0 || num_q_heads < 0 || num_kv_heads < 0 || num_pages < 0 || page_size <= 0 ||
+      max_blocks < 0)
+    return MAS_ERR_INVALID_VALUE;
+  if (num_rows == 0 || max_q_len == 0 || num_q_heads == 0) return MAS_OK;
+  if (num_kv_heads == 0 || num_q_heads % num_kv_heads != 0) return MAS_ERR_INVALID_VALUE;
+  if ((head_dim != 64 && head_dim != 128) || (page_size & (page_size - 1)) != 0) return MAS_ERR_UNSUPPORTED;
+  const int64_t cap = max_blocks * page_size;
+  if (cap > (int64_t{1} << 30) || num_rows > 65535 || num_q_heads > 65535) return MAS_ERR_UNSUPPORTED;
+  if (out == nullptr || q == nullptr || seq_lens == nullptr || cu_seqlens_q == nullptr || k_cache == nullptr ||
+      v_cache == nullptr || block_tables == nullptr || num_pages == 0 || cap == 0)
+    return MAS_ERR_INVALID_VALUE;
+  const bool aligned = aligned16(q) && aligned16(out) && aligned16(k_cache) && aligned16(v_cache) &&
+                       q_stride % 8 == 0 && q_head_stride % 8 == 0 && out_stride % 8 == 0 &&
+                       out_head_stride % 8 == 0 && page_stride % 8 == 0 && entry_stride % 8 == 0 &&
+                       head_stride % 8 == 0;
+  if (!aligned) return MAS_ERR_MISALIGNED;
+  const int64_t group = num_q_heads / num_kv_heads;
+  const int heads_per_wg = group >= 4 ? 4 : (group == 2 ? 2 : 1);
+  const int64_t hgroups = cdiv(group, heads_per_wg);
+  const int64_t tokens_per_wg = kRowsPerWave * (4 / heads_per_wg);
+  const int64_t gx = num_kv_heads * hgroups, gy = cdiv(max_q_len, tokens_per_wg);
+  if (gx > INT32_MAX || gy > 65535) return MAS_ERR_UNSUPPORTED;
+  int log2_page = 0;
+  while ((int64_t{1} << log2_page) < page_size) ++log2_page;
+  ContextArgs a{};
+  a.q = static_cast<const uint16_t*>(q);
+  a.q_stride = q_stride;
+  a.q_head_stride = q_head_stride;
+  a.k_cache = static_cast<const uint16_t*>(k_cache);
+  a.v_cache = static_cast<const uint16_t*>(v_cache);
+  a.page_stride = page_stride;
+  a.entry_stride = entry_stride;
+  a.head_stride = head_stride;
+  a.num_pages = num_pages;
+  a.block_tables = block_tables;
+  a.bt_stride = block_table_stride;
+  a.max_blocks = max_blocks;
+  a.seq_lens = seq_lens;
+  a.cu_seqlens_q = cu_seqlens_q;
+  a.hq = static_cast<int>(num_q_heads);
+  a.hk = static_cast<int>(num_kv_heads);
+  a.group = static_cast<int>(group);
+  a.heads_per_wg = heads_per_wg;
+  a.log2_page = log2_page;
+  a.scale_log2 = bmm1_scale * 1.4426950408889634f;
+  a.out_scale = bmm2_scale;
+  a.out = static_cast<uint16_t*>(out);
+  a.out_stride = out_stride;
+  a.out_head_stride = out_head_stride;
+  a.err = err;
+  const dim3 grid(static_cast<uint32_t>(gx), static_cast<uint32_t>(gy), static_cast<uint32_t>(num_rows));
+  if (head_dim == 64) {
+    hipLaunchKernelGGL(context_attn<64>, grid, dim3(256), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL(context_attn<128>, grid, dim3(256), 0, stream, a);
+  }
+  return launch_status();
+}

@@ -179,6 +179,40 @@ def paged_decode_attention(q_bits, k_cache_bits, v_cache_bits, block_tables, seq
     return out
 
 
+def paged_context_attention(q_bits, k_cache_bits, v_cache_bits, block_tables, seq_lens, cu_seqlens_q,
+                            bmm1_scale: float, bmm2_scale: float = 1.0):
+    """trtllm_batch_context_with_kv_cache (devstral2.py:198-213): row j owns query tokens
+    cu[j]:cu[j+1] (q_len) and kv_len = seq_lens[j] positions; token i sits at kv_len - q_len + i and
+    attends to positions 0..that (causal, aligned to the end). fp32 math, output rounded to bf16;
+    tokens left before position 0 give zeros. q_bits [tokens, Hq, D]; returns bf16 bits."""
+    q = bf16_to_f32(np.asarray(q_bits))
+    tokens, hq, dim = q.shape
+    page_size, hk = k_cache_bits.shape[1], k_cache_bits.shape[2]
+    group = hq // hk
+    tables = np.asarray(block_tables, dtype=np.int64)
+    cu = np.asarray(cu_seqlens_q, dtype=np.int64)
+    out = np.zeros((tokens, hq, dim), dtype=np.uint16)
+    for j in range(len(cu) - 1):
+        q0, q_len, kv_len = int(cu[j]), int(cu[j + 1] - cu[j]), int(seq_lens[j])
+        if q_len <= 0 or kv_len <= 0:
+            continue
+        pos = np.arange(kv_len)
+        pages = tables[j, pos // page_size]
+        k = bf16_to_f32(k_cache_bits[pages, pos % page_size])
+        v = bf16_to_f32(v_cache_bits[pages, pos % page_size])
+        for i in range(q_len):
+            qpos = kv_len - q_len + i
+            if qpos < 0:
+                continue
+            for h in range(hq):
+                kvh = h // group
+                s = (k[: qpos + 1, kvh, :] @ q[q0 + i, h]).astype(F32) * F32(bmm1_scale)
+                e = np.exp(s - s.max(), dtype=F32)
+                o = (e @ v[: qpos + 1, kvh, :]).astype(F32) / np.sum(e, dtype=F32) * F32(bmm2_scale)
+                out[q0 + i, h] = f32_to_bf16(o.astype(F32))
+    return out
+
+
 def embedding(weight_bits, ids):
     """nn.Embedding at devstral2.py:260,282: rows of the table selected by the ids."""
     return np.asarray(weight_bits)[np.asarray(ids, dtype=np.int64)]

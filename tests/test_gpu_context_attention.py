@@ -1,0 +1,125 @@
+"""Causal paged context attention (trtllm_batch_context_with_kv_cache, devstral2.py:198-213) on the
+GPU against the oracle, through the C ABI: bf16 outputs within rtol 1.6e-2 / atol 1e-2 (P enters the
+P.V product as bf16, as in flash-attention kernels, so fewer outputs are bit-identical than for the
+other ops)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import ATOL, RTOL, bits
+from oracle import numerics as on
+from oracle import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(seed, q_lens, kv_lens, hq, hk, dim, page_size):
+    g = torch.Generator().manual_seed(seed)
+    tokens = sum(q_lens)
+    width = max(1, max(-(-n // page_size) for n in kv_lens))
+    pages = len(kv_lens) * width + 2
+    q = torch.randn(tokens, hq, dim, generator=g).bfloat16()
+    kc = torch.randn(pages, page_size, hk, dim, generator=g).bfloat16()
+    vc = torch.randn(pages, page_size, hk, dim, generator=g).bfloat16()
+    tables = torch.randperm(pages, generator=g)[: len(kv_lens) * width].reshape(len(kv_lens), width).to(torch.int32)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(q_lens)]), dtype=torch.int32)
+    return q, kc, vc, tables, torch.tensor(kv_lens, dtype=torch.int32), cu
+
+
+def _run(mas, dev, q, kc, vc, tables, seq, cu, scale, out=None, flags=None, scale2=1.0):
+    ws = torch.zeros(16, dtype=torch.uint8, device=dev)
+    max_q = int((cu[1:] - cu[:-1]).max()) if len(cu) > 1 else 0
+    return mas.attention.trtllm_batch_context_with_kv_cache(
+        q.to(dev) if q.device.type == "cpu" else q, (kc.to(dev), vc.to(dev)), ws, tables.to(dev), seq.to(dev),
+        max_q, 0, scale, scale2, len(cu) - 1, cu.to(dev), None, out=out, kv_layout="NHD", error_flags=flags)
+
+
+def _check(got, want, min_exact=0.6):
+    np.testing.assert_allclose(on.bf16_to_f32(got), on.bf16_to_f32(want), rtol=RTOL, atol=ATOL)
+    assert np.mean(got == want) >= min_exact
+
+
+CASES = [
+    ([100, 37], [100, 37], 32, 8, 128, 16),        # plain prefill, Devstral-Small-2 heads
+    ([64, 1, 9], [300, 77, 9], 32, 8, 128, 256),   # chunked prefill: new tokens after cached ones
+    ([70, 20], [70, 150], 96, 8, 128, 64),         # the 123B head group (12 per kv head)
+    ([40], [140], 8, 8, 128, 16),                  # one head per kv head
+    ([33, 90], [33, 95], 16, 8, 64, 32),           # 2 per kv head, head_dim 64
+    ([17, 5], [50, 5], 6, 2, 64, 4),               # 3 per kv head, pages of 4
+    ([200], [200], 8, 1, 128, 128),                # 8 per kv head, a longer row
+]
+
+
+@pytest.mark.parametrize("q_lens,kv_lens,hq,hk,dim,page_size", CASES)
+def test_context_attention_matches_oracle(mas, dev, q_lens, kv_lens, hq, hk, dim, page_size):
+    q, kc, vc, tables, seq, cu = _case(sum(kv_lens) + hq, q_lens, kv_lens, hq, hk, dim, page_size)
+    scale = dim ** -0.5
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = _run(mas, dev, q, kc, vc, tables, seq, cu, scale, flags=flags)
+    want = ops.paged_context_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), cu.numpy(), scale)
+    _check(bits(out), want)
+    assert int(flags.item()) == 0
+
+
+def test_context_attention_strided_views_and_bmm2_scale(mas, dev):
+    """query as the column view of the qkv rows, out as a strided view, bmm2_scale applied."""
+    q_lens, kv_lens, hq, hk, dim, ps = [48, 30], [60, 30], 32, 8, 128, 16
+    _, kc, vc, tables, seq, cu = _case(3, q_lens, kv_lens, hq, hk, dim, ps)
+    g = torch.Generator().manual_seed(4)
+    qkv = torch.randn(sum(q_lens), (hq + 2 * hk) * dim, generator=g).bfloat16().to(dev)
+    q = qkv[:, : hq * dim].view(-1, hq, dim)
+    out_base = torch.full((sum(q_lens), hq + 2, dim), 5.0, dtype=torch.bfloat16, device=dev)
+    out = out_base[:, 1:hq + 1]
+    _run(mas, dev, q, kc, vc, tables, seq, cu, 0.07, out=out, scale2=2.0)
+    want = ops.paged_context_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), cu.numpy(), 0.07, 2.0)
+    _check(bits(out), want)
+    assert torch.all(out_base[:, 0] == 5.0) and torch.all(out_base[:, hq + 1] == 5.0)
+
+
+def test_context_attention_error_paths(mas, dev):
+    q_lens, kv_lens, hq, hk, dim, ps = [20, 10], [40, 10], 8, 2, 64, 8
+    q, kc, vc, tables, _, cu = _case(8, q_lens, kv_lens, hq, hk, dim, ps)
+    seq = torch.tensor([40, 4], dtype=torch.int32)       # row 1: kv_len 4 < q_len 10
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = _run(mas, dev, q, kc, vc, tables, seq, cu, 0.1, flags=flags)
+    assert int(flags.item()) == 2
+    want = ops.paged_context_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), cu.numpy(), 0.1)
+    _check(bits(out), want)
+    assert not out[20:26].any()                           # the tokens before position 0 get zeros
+    bad = tables.clone()
+    bad[0, 2] = kc.shape[0] + 3                           # positions 16..23 of row 0 point past the cache
+    flags.zero_()
+    _run(mas, dev, q, kc, vc, bad, torch.tensor([40, 10], dtype=torch.int32), cu, 0.1, flags=flags)
+    assert int(flags.item()) == 8
+
+
+def test_context_attention_in_graph_replays(mas, dev):
+    q_lens, kv_lens, hq, hk, dim, ps = [128, 64], [256, 64], 32, 8, 128, 64
+    q, kc, vc, tables, seq, cu = _case(12, q_lens, kv_lens, hq, hk, dim, ps)
+    qd, kd, vd, td, sd, cd = q.to(dev), kc.to(dev), vc.to(dev), tables.to(dev), seq.to(dev), cu.to(dev)
+    ws = torch.zeros(16, dtype=torch.uint8, device=dev)
+    out = torch.empty_like(qd)
+
+    def call():
+        mas.attention.trtllm_batch_context_with_kv_cache(qd, (kd, vd), ws, td, sd, 128, 256, 0.088, 1.0, 2, cd,
+                                                         None, out=out)
+
+    call()
+    torch.cuda.synchronize()
+    want = out.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    for _ in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want)

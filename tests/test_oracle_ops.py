@@ -400,3 +400,32 @@ def test_paged_decode_attention_closed_forms():
     half = ops.paged_decode_attention(bits(q), bits(kc), bits(vc), tables.numpy(), np.array([0, 3]), 0.5, 1.0)
     assert not out[0].any()
     np.testing.assert_allclose(on.bf16_to_f32(out[1]), 2 * on.bf16_to_f32(half[1]), rtol=2 ** -7)
+
+
+@pytest.mark.parametrize("q_lens,kv_lens,hq,hk,dim,page_size", [([5, 12], [5, 30], 8, 2, 32, 4),
+                                                                 ([3, 1], [3, 9], 4, 4, 64, 8)])
+def test_paged_context_attention_matches_sdpa(q_lens, kv_lens, hq, hk, dim, page_size):
+    """The oracle's causal context attention against torch's scaled_dot_product_attention with an
+    explicit mask aligned to the end of each row's positions (query token i at kv_len - q_len + i)."""
+    g = torch.Generator().manual_seed(sum(kv_lens))
+    tokens = sum(q_lens)
+    width = max(-(-n // page_size) for n in kv_lens)
+    pages = len(kv_lens) * width + 2
+    q = torch.randn(tokens, hq, dim, generator=g).bfloat16()
+    kc = torch.randn(pages, page_size, hk, dim, generator=g).bfloat16()
+    vc = torch.randn(pages, page_size, hk, dim, generator=g).bfloat16()
+    tables = torch.randperm(pages, generator=g)[: len(kv_lens) * width].reshape(len(kv_lens), width).to(torch.int32)
+    cu = np.concatenate([[0], np.cumsum(q_lens)])
+    scale = dim ** -0.5
+    got = on.bf16_to_f32(ops.paged_context_attention(bits(q), bits(kc), bits(vc), tables.numpy(), np.array(kv_lens),
+                                                     cu, scale))
+    for j, (ql, kl) in enumerate(zip(q_lens, kv_lens)):
+        pos = torch.arange(kl)
+        pg = tables[j, pos // page_size].long()
+        k = kc[pg, pos % page_size].float().permute(1, 0, 2)[None]
+        v = vc[pg, pos % page_size].float().permute(1, 0, 2)[None]
+        qq = q[cu[j]:cu[j + 1]].float().permute(1, 0, 2)[None]              # [1, Hq, q_len, D]
+        mask = (torch.arange(kl)[None, :] <= (kl - ql + torch.arange(ql))[:, None])
+        ref = F.scaled_dot_product_attention(qq, k, v, attn_mask=mask, scale=scale, enable_gqa=True)
+        want = on.bf16_to_f32(bits(ref[0].permute(1, 0, 2).bfloat16()))
+        np.testing.assert_allclose(got[cu[j]:cu[j + 1]], want, rtol=2 ** -7, atol=1e-3)
