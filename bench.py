@@ -38,6 +38,7 @@ import __graft_entry__  # noqa: E402
 
 METRIC = "HBM GB/s & % of peak for layer kernels; µs/layer at 64-token decode"
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 COLD_BYTES = 768 << 20         # working set cycled by the cold protocol (3x the Infinity Cache)
 # HBM bytes per launch of a workload's dominant kernel, from two rocprofv3 counter passes
 # (FETCH_SIZE, then WRITE_SIZE) over `bench.py --pmc-probe`, each calibrated by the same counter on
@@ -376,6 +377,89 @@ def run_attention_workload(mas, args, shape, dev) -> dict:
             "inputs": inp}
 
 
+def context_main(mas, args, shape, dev) -> int:
+    """Causal context attention: a step is one call; the value is TFLOP/s of algorithmic flops."""
+    wl = mas.workloads
+    inp = wl.make_context_inputs(shape, dev, seed=0)
+    out = torch.empty_like(inp.q)
+    flops = wl.context_flops(shape)
+    scale = shape.head_dim ** -0.5
+    ws = torch.empty(16, dtype=torch.uint8, device=dev)
+
+    def call():
+        mas.attention.trtllm_batch_context_with_kv_cache(inp.q, (inp.k_cache, inp.v_cache), ws, inp.block_tables,
+                                                         inp.seq_lens, shape.q_len, shape.q_len + shape.cached,
+                                                         scale, 1.0, shape.rows, inp.cu_seqlens_q, None, out=out)
+
+    steps = args.steps if args.steps is not None else 20
+    warmup = args.warmup if args.warmup is not None else 3
+    call()
+    g = capture(call)
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        g.replay()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    gb = capture(lambda: [call() for _ in range(4)])
+    gb.replay()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(5)]
+    for start, stop in events:
+        start.record()
+        gb.replay()
+        stop.record()
+    torch.cuda.synchronize()
+    call_us = 1000.0 * sorted(x.elapsed_time(y) for x, y in events)[2] / 4
+    ms_per_step = elapsed / steps * 1e3
+    tflops = flops / (ms_per_step * 1e-3) / 1e12
+    kernel_tflops = flops / (call_us * 1e-6) / 1e12
+    line = {
+        "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps,
+        "warmup": warmup, "ms_per_step": round(ms_per_step, 6), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": shape.name, "rows": shape.rows, "q_len": shape.q_len, "cached": shape.cached,
+                   "q_heads": shape.q_heads, "kv_heads": shape.kv_heads, "head_dim": shape.head_dim,
+                   "page_size": shape.page_size, "flops": flops, "launch": "hip-graph"},
+        "us_per_call": round(ms_per_step * 1e3, 3),
+        "ops": {"paged_context_attention": {"us": round(call_us, 3), "TFLOP/s": round(kernel_tflops, 1),
+                                            "frac": round(kernel_tflops / PEAK_BF16_TFLOPS, 4)}},
+        "roofline": {"bound": "mfma", "kernel": "paged_context_attention", "achieved": round(kernel_tflops, 1),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(kernel_tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None, "flops_per_launch": flops, "avg_launch_us": round(call_us, 3)},
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline_context(inp, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def cpu_baseline_context(inp, seconds: float) -> dict:
+    """The oracle's causal attention on the host, on query tokens of the first row taken from its
+    end (the longest reach), for about ``seconds``; algorithmic flops done per second."""
+    from oracle import ops as oops
+
+    s = inp.shape
+    kv_len = s.cached + s.q_len
+    q = inp.q.cpu().view(torch.int16).numpy().view(np.uint16)
+    kc = inp.k_cache.cpu().view(torch.int16).numpy().view(np.uint16)
+    vc = inp.v_cache.cpu().view(torch.int16).numpy().view(np.uint16)
+    tables = inp.block_tables.cpu().numpy()[:1]
+    done, tokens, t0 = 0, 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds and tokens < s.q_len:
+        # one query token at a time (a row of one token whose kv_len is its position + 1)
+        i = s.q_len - 1 - tokens
+        pos = s.cached + i
+        oops.paged_context_attention(q[i:i + 1], kc, vc, tables, np.array([pos + 1]), np.array([0, 1]),
+                                     s.head_dim ** -0.5)
+        done += (pos + 1) * s.q_heads * s.head_dim * 4
+        tokens += 1
+    elapsed = time.perf_counter() - t0
+    return {"value": round(done / elapsed / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"{tokens} query tokens of one row (longest reach first), single-threaded numpy ({elapsed:.1f} s)"}
+
+
 def cpu_baseline_attention(inp, seconds: float) -> dict:
     """The oracle's decode attention on the host, one row at a time over the workload's rows (cycling),
     for about ``seconds``; credited bytes of the rows done per second."""
@@ -435,6 +519,8 @@ def main() -> int:
     mas.load_library()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.workload in mas.workloads.CONTEXT_SHAPES:
+        return context_main(mas, args, mas.workloads.CONTEXT_SHAPES[args.workload], dev)
     if args.workload in mas.workloads.ATTENTION_SHAPES:
         return attention_main(mas, args, mas.workloads.ATTENTION_SHAPES[args.workload], dev)
     shape = mas.workloads.SHAPES[args.workload]

@@ -17,7 +17,9 @@
 //   S^T = K Q^T on MFMA (v_mfma_f32_16x16x32_bf16; A = 16 key rows read from LDS, B = the
 //   wavefront's query rows, held in registers), causal mask, online softmax per query row, then
 //   O^T += V^T P^T on MFMA, where P^T is packed to bf16 straight from the S^T accumulators and V^T
-//   is stored transposed in LDS, its columns in the order that packing implies.
+//   is read from the row-major value tile with gfx950's transposing LDS read (ds_read_b64_tr_b16:
+//   in each group of 16 lanes, lane 4a + b receives element b of the 4-element rows that lanes
+//   a, a + 4, a + 8, a + 12 point at), two per operand, in the position order the packing implies.
 // The next tile's key and value loads are issued before the current tile's arithmetic.
 #include "device.h"
 
@@ -25,7 +27,8 @@ namespace mas {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr int kTileP = 64;        // key positions per tile
 constexpr int kRowsPerWave = 32;  // query rows (tokens of one head) per wavefront
@@ -49,24 +52,30 @@ struct ContextArgs {
   uint32_t* err;
 };
 
-// Column of position p (0..63) of a tile in the transposed value rows: P.V k-step s = p / 32 takes
-// its 32 positions in the order the S^T accumulators pack them (lane group r, element j):
-// j < 4 -> position 16 * 0 + 4 r + j of the step, j >= 4 -> position 16 + 4 r + (j - 4).
-__device__ __forceinline__ int vt_column(int p) {
-  const int s = p >> 5, q = p & 31, half = q >> 4, rem = q & 15;
-  return 32 * s + 8 * (rem >> 2) + 4 * half + (rem & 3);
+// Four values of one head-dim column from four consecutive value rows: in each group of 16 lanes,
+// lane k points at row first + k / 4, columns col0 + 4 (k % 4) .. + 3; lane n then holds rows
+// first .. first + 3 of column col0 + n.
+__device__ __forceinline__ i16x4 read_column4(const uint16_t* v_lds, int vrow, int first, int col0, int k) {
+  const uint16_t* p = v_lds + (first + (k >> 2)) * vrow + col0 + 4 * (k & 3);
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_i16x4*)(__attribute__((address_space(3))) uint16_t*)(p));
 }
 
+// Workgroups per CU the register allocation must allow (2: at most 256 VGPRs per lane).
+#ifndef MAS_CTX_MIN_WG
+#define MAS_CTX_MIN_WG 2
+#endif
+
 template <int D>
-__global__ __launch_bounds__(256) void context_attn(ContextArgs a) {
+__global__ __launch_bounds__(256, MAS_CTX_MIN_WG) void context_attn(ContextArgs a) {
   constexpr int KS = D / 32;            // MFMA k-steps over the head dim (S^T)
   constexpr int DT = D / 16;            // MFMA tiles over the head dim (O^T)
   constexpr int KROW = D + 8;           // bf16 per LDS key row (+16 B: conflict-free A reads)
-  constexpr int VTROW = kTileP + 8;     // bf16 per LDS transposed value row (+16 B)
+  constexpr int VROW = D + 16;          // bf16 per LDS value row (+32 B: conflict-free column reads)
   constexpr int CPR = D / 8;            // 16-byte chunks per key / value row
   constexpr int LOADS = kTileP * CPR / 256;  // 16-byte chunks per thread per tile, each of K and V
   __shared__ __align__(16) uint16_t k_lds[kTileP * KROW];
-  __shared__ __align__(16) uint16_t vt_lds[D * VTROW];
+  __shared__ __align__(16) uint16_t v_lds[kTileP * VROW];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id_uniform();
   const int n = lane & 15, r = lane >> 4;
@@ -75,7 +84,12 @@ __global__ __launch_bounds__(256) void context_attn(ContextArgs a) {
   const int row = blockIdx.z;
   const int q0 = a.cu_seqlens_q[row], q_len = a.cu_seqlens_q[row + 1] - q0;
   const int tokens_per_wg = kRowsPerWave * (4 / a.heads_per_wg);
-  const int tile_tok = blockIdx.y * tokens_per_wg;
+  // Token tiles in reverse launch order: the last tiles reach the most positions, so they start first.
+#ifndef MAS_CTX_REVERSE
+#define MAS_CTX_REVERSE 1
+#endif
+  const int tile_idx = MAS_CTX_REVERSE ? static_cast<int>(gridDim.y - 1 - blockIdx.y) : static_cast<int>(blockIdx.y);
+  const int tile_tok = tile_idx * tokens_per_wg;
   if (tile_tok >= q_len) return;  // uniform over the workgroup
   // kv_len clamped to the block table's reach; a kv_len below q_len leaves the first tokens with
   // negative positions: they see no key and get zeros.
@@ -126,25 +140,48 @@ __global__ __launch_bounds__(256) void context_attn(ContextArgs a) {
 
   const int32_t* bt = a.block_tables + row * a.bt_stride;
   const int pmask = (1 << a.log2_page) - 1;
-  // Thread's chunks of a tile: chunk c = tid + 256 u -> position c / CPR, head-dim chunk c % CPR.
-  // (Rows past kv_len or on a page id outside the cache load row 0 of page 0 and are zeroed when
-  // stored; the flag is kept so that the loads themselves are not waited on here.)
+  // Thread's chunks of a tile: chunk c = tid + 256 u -> position tid / CPR + (256 / CPR) u, head-dim
+  // chunk tid % CPR (the same for every u). Rows past kv_len or on a page id outside the cache load
+  // row 0 of page 0 and are zeroed when stored; the flags are kept so that the loads themselves are
+  // not waited on here. With pages of at least a tile, a tile lies in one page: one (wave-uniform)
+  // block-table read per tile and precomputed per-thread offsets.
+  constexpr int kPosStep = 256 / CPR;
+  const int dcol = tid % CPR, prow = tid / CPR;
+  const int64_t lane_off = static_cast<int64_t>(prow) * a.entry_stride + kvh * a.head_stride + 8 * dcol;
+  const bool tile_pages = (1 << a.log2_page) >= kTileP;
   u32x4 kst[LOADS], vst[LOADS];
   bool lok[LOADS];
+  bool tile_full = false;  // every chunk of the staged tile valid: stores need no zeroing
   auto issue_tile = [&](int base) {
-#pragma unroll
-    for (int u = 0; u < LOADS; ++u) {
-      const int c = tid + 256 * u;
-      const int p = base + c / CPR;
-      const int pc = p < kv_len ? p : kv_len - 1;
-      const int32_t page = bt[pc >> a.log2_page];
+    if (tile_pages) {
+      const int32_t page = bt[base >> a.log2_page];
       const bool ok = page >= 0 && page < a.num_pages;
-      if (!ok && p < kv_len && (c % CPR) == 0) report(a.err, MAS_ERRBIT_PAGE);
-      const int64_t off = (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
-                          static_cast<int64_t>(pc & pmask) * a.entry_stride + kvh * a.head_stride + 8 * (c % CPR);
-      kst[u] = load_cached(a.k_cache + off);
-      vst[u] = load_cached(a.v_cache + off);
-      lok[u] = ok && p < kv_len;
+      if (!ok && tid == 0) report(a.err, MAS_ERRBIT_PAGE);
+      const int64_t tile_off = (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
+                               static_cast<int64_t>(base & pmask) * a.entry_stride;
+      tile_full = ok && base + kTileP <= kv_len;
+#pragma unroll
+      for (int u = 0; u < LOADS; ++u) {
+        const int64_t off = tile_off + lane_off + static_cast<int64_t>(kPosStep * u) * a.entry_stride;
+        kst[u] = load_cached(a.k_cache + off);
+        vst[u] = load_cached(a.v_cache + off);
+        lok[u] = ok && base + prow + kPosStep * u < kv_len;
+      }
+    } else {
+      tile_full = false;
+#pragma unroll
+      for (int u = 0; u < LOADS; ++u) {
+        const int p = base + prow + kPosStep * u;
+        const int pc = p < kv_len ? p : kv_len - 1;
+        const int32_t page = bt[pc >> a.log2_page];
+        const bool ok = page >= 0 && page < a.num_pages;
+        if (!ok && p < kv_len && dcol == 0) report(a.err, MAS_ERRBIT_PAGE);
+        const int64_t off = (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
+                            static_cast<int64_t>(pc & pmask) * a.entry_stride + kvh * a.head_stride + 8 * dcol;
+        kst[u] = load_cached(a.k_cache + off);
+        vst[u] = load_cached(a.v_cache + off);
+        lok[u] = ok && p < kv_len;
+      }
     }
   };
   if (ntiles > 0) issue_tile(0);
@@ -152,23 +189,26 @@ __global__ __launch_bounds__(256) void context_attn(ContextArgs a) {
   for (int it = 0; it < ntiles; ++it) {
     const int base = it * kTileP;
     __syncthreads();  // the previous tile's LDS reads are done
+    if (tile_full) {
 #pragma unroll
-    for (int u = 0; u < LOADS; ++u) {
-      const int c = tid + 256 * u;
-      const int p = c / CPR, dc = c % CPR;
-      const u32x4 kv = lok[u] ? kst[u] : u32x4{0u, 0u, 0u, 0u};
-      const u32x4 vv = lok[u] ? vst[u] : u32x4{0u, 0u, 0u, 0u};
-      *reinterpret_cast<u32x4*>(k_lds + p * KROW + 8 * dc) = kv;
-      const int col = vt_column(p);
+      for (int u = 0; u < LOADS; ++u) {
+        const int p = prow + kPosStep * u;
+        *reinterpret_cast<u32x4*>(k_lds + p * KROW + 8 * dcol) = kst[u];
+        *reinterpret_cast<u32x4*>(v_lds + p * VROW + 8 * dcol) = vst[u];
+      }
+    } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        vt_lds[(8 * dc + 2 * e) * VTROW + col] = static_cast<uint16_t>(vv[e]);
-        vt_lds[(8 * dc + 2 * e + 1) * VTROW + col] = static_cast<uint16_t>(vv[e] >> 16);
+      for (int u = 0; u < LOADS; ++u) {
+        const int p = prow + kPosStep * u;
+        const u32x4 kv = lok[u] ? kst[u] : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 vv = lok[u] ? vst[u] : u32x4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(k_lds + p * KROW + 8 * dcol) = kv;
+        *reinterpret_cast<u32x4*>(v_lds + p * VROW + 8 * dcol) = vv;
       }
     }
     __syncthreads();
-    if (it + 1 < ntiles) issue_tile(base + kTileP);
-    if (!wave_live) continue;
+    if (it + 1 < ntiles) issue_tile(base + kTileP);  // in flight during this tile's arithmetic
+    if (wave_live) {
 
     // ---- S^T = K Q^T: lane (n, r) holds S[row 16 nt + n][position base + 16 pt + 4 r + i]
     f32x4 s[4][2];
@@ -185,40 +225,50 @@ __global__ __launch_bounds__(256) void context_attn(ContextArgs a) {
       }
     }
 
-    // ---- causal mask and online softmax per query row
+    // ---- causal mask (only tiles that cross the diagonal of the wavefront's first row, or the end
+    // of the sequence; a wavefront-uniform branch) and online softmax per query row. Scores stay
+    // in raw units; the scale enters the exponent through one fma: p = 2^(s c - m c).
+    if (base + kTileP - 1 > shift + tok || base + kTileP > kv_len) {
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const int qpos = shift + tok + 16 * nt + n;  // this lane's query row position
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int kp = base + 16 * pt + 4 * r + i;
+            if (kp > qpos || kp >= kv_len) s[pt][nt][i] = kNegInf;
+          }
+      }
+    }
+    const float c = a.scale_log2;
     bf16x8 pb[2][2];  // B operands of P.V: [row tile][k-step of 32 positions]
+    float alpha[2];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-      const int qpos = shift + tok + 16 * nt + n;  // this lane's query row position
       float mx = kNegInf;
 #pragma unroll
       for (int pt = 0; pt < 4; ++pt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int kp = base + 16 * pt + 4 * r + i;
-          const float v = kp <= qpos && kp < kv_len ? s[pt][nt][i] * a.scale_log2 : kNegInf;
-          s[pt][nt][i] = v;
-          mx = fmaxf(mx, v);
-        }
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[pt][nt][i]);
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       const float m_new = fmaxf(m_run[nt], mx);
       const float m_use = m_new == kNegInf ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run[nt] - m_use);
+      const float mc = m_use * c;
+      alpha[nt] = __builtin_amdgcn_exp2f(__builtin_fmaf(m_run[nt], c, -mc));
       float sum = 0.f;
 #pragma unroll
       for (int pt = 0; pt < 4; ++pt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          s[pt][nt][i] = __builtin_amdgcn_exp2f(s[pt][nt][i] - m_use);
+          s[pt][nt][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[pt][nt][i], c, -mc));
           sum += s[pt][nt][i];
         }
       sum += __shfl_xor(sum, 16);
       sum += __shfl_xor(sum, 32);
-      l_run[nt] = l_run[nt] * alpha + sum;
+      l_run[nt] = l_run[nt] * alpha[nt] + sum;
       m_run[nt] = m_new;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) acc[nt][dt] *= alpha;
       // k-step ks2 takes position tiles 2 ks2 (elements 0..3) and 2 ks2 + 1 (elements 4..7)
 #pragma unroll
       for (int ks2 = 0; ks2 < 2; ++ks2) {
@@ -228,18 +278,29 @@ __global__ __launch_bounds__(256) void context_attn(ContextArgs a) {
         pb[nt][ks2] = __builtin_bit_cast(bf16x8, packed);
       }
     }
+    // O rescale, skipped when no row's max moved (common once the running max has settled)
+    if (__builtin_amdgcn_ballot_w64(alpha[0] != 1.f || alpha[1] != 1.f) != 0) {
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[nt][dt] *= alpha[nt];
+    }
 
-    // ---- O^T += V^T P^T: A = V^T[16 dims][32 positions] from LDS, B = P^T
+    // ---- O^T += V^T P^T: A = V^T[16 dims][32 positions] (element j < 4: position 32 ks2 + 4 r + j,
+    // j >= 4: position 32 ks2 + 16 + 4 r + j - 4, as packed into pb), B = P^T
 #pragma unroll
     for (int ks2 = 0; ks2 < 2; ++ks2) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const bf16x8 va = *reinterpret_cast<const bf16x8*>(vt_lds + (16 * dt + n) * VTROW + 32 * ks2 + 8 * r);
+        const i16x4 lo = read_column4(v_lds, VROW, 32 * ks2 + 4 * r, 16 * dt, n);
+        const i16x4 hi = read_column4(v_lds, VROW, 32 * ks2 + 16 + 4 * r, 16 * dt, n);
+        const bf16x8 va = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt)
           acc[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[nt][ks2], acc[nt][dt], 0, 0, 0);
       }
     }
+    }  // wave_live
   }
 
   if (!wave_live) return;
@@ -277,6 +338,7 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
     return MAS_ERR_INVALID_VALUE;
   if (num_rows == 0 || max_q_len == 0 || num_q_heads == 0) return MAS_OK;
   if (num_kv_heads == 0 || num_q_heads % num_kv_heads != 0) return MAS_ERR_INVALID_VALUE;
+  if (!(bmm1_scale > 0.f)) return MAS_ERR_INVALID_VALUE;  // the row max is taken over unscaled scores
   if ((head_dim != 64 && head_dim != 128) || (page_size & (page_size - 1)) != 0) return MAS_ERR_UNSUPPORTED;
   const int64_t cap = max_blocks * page_size;
   if (cap > (int64_t{1} << 30) || num_rows > 65535 || num_q_heads > 65535) return MAS_ERR_UNSUPPORTED;

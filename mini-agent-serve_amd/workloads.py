@@ -18,7 +18,8 @@ from .rope import cos_sin_cache
 
 __all__ = ["Shape", "SHAPES", "LayerInputs", "make_layer_inputs", "credited_bytes", "layer_credited_bytes",
            "AttentionShape", "ATTENTION_SHAPES", "AttentionInputs", "make_attention_inputs",
-           "attention_credited_bytes"]
+           "attention_credited_bytes", "ContextShape", "CONTEXT_SHAPES", "ContextInputs", "make_context_inputs",
+           "context_flops"]
 
 
 @dataclass(frozen=True)
@@ -264,3 +265,64 @@ def attention_credited_bytes(inputs: AttentionInputs) -> int:
     positions = int(lens.sum())
     pages = int(((lens + s.page_size - 1) // s.page_size).sum())
     return positions * s.kv_heads * s.head_dim * 4 + 2 * s.batch * s.q_heads * s.head_dim * 2 + pages * 4 + s.batch * 4
+
+
+# ---- paged context (prefill) attention ---------------------------------------------------------------
+
+@dataclass(frozen=True)
+class ContextShape:
+    name: str
+    rows: int                   # prompt rows
+    q_len: int                  # new tokens per row
+    cached: int                 # positions already in the cache before them (kv_len = cached + q_len)
+    q_heads: int
+    kv_heads: int
+    head_dim: int
+    page_size: int
+
+
+CONTEXT_SHAPES: dict[str, ContextShape] = {s.name: s for s in [
+    # the prefill-8192 step's attention: 4 prompts of 2048 tokens, Devstral-Small-2 heads
+    ContextShape("context_attn_4x2048_24b", 4, 2048, 0, 32, 8, 128, 256),
+    # the prefill-16384 step's attention: 4 prompts of 4096 tokens, Devstral-2 123B heads
+    ContextShape("context_attn_4x4096_123b", 4, 4096, 0, 96, 8, 128, 256),
+]}
+
+
+@dataclass
+class ContextInputs:
+    shape: ContextShape
+    q: torch.Tensor             # [rows * q_len, Hq, D]
+    k_cache: torch.Tensor
+    v_cache: torch.Tensor
+    block_tables: torch.Tensor  # [rows, pages per row] int32
+    seq_lens: torch.Tensor      # [rows] int32 (kv_len)
+    cu_seqlens_q: torch.Tensor  # [rows + 1] int32
+
+
+def make_context_inputs(shape: ContextShape | str, device="cpu", seed: int = 0) -> ContextInputs:
+    if isinstance(shape, str):
+        shape = CONTEXT_SHAPES[shape]
+    device = torch.device(device)
+    kv_len = shape.cached + shape.q_len
+    width = -(-kv_len // shape.page_size)
+    pages = shape.rows * width + 1
+    g = torch.Generator().manual_seed(seed)
+    tables = torch.randperm(pages, generator=g)[: shape.rows * width].reshape(shape.rows, width).to(torch.int32)
+    dg = torch.Generator(device=device).manual_seed(seed)
+    kv = (pages, shape.page_size, shape.kv_heads, shape.head_dim)
+    return ContextInputs(
+        shape=shape,
+        q=torch.randn(shape.rows * shape.q_len, shape.q_heads, shape.head_dim, generator=dg, device=device).bfloat16(),
+        k_cache=torch.randn(kv, generator=dg, device=device).bfloat16(),
+        v_cache=torch.randn(kv, generator=dg, device=device).bfloat16(),
+        block_tables=tables.to(device),
+        seq_lens=torch.full((shape.rows,), kv_len, dtype=torch.int32, device=device),
+        cu_seqlens_q=(torch.arange(shape.rows + 1, dtype=torch.int32) * shape.q_len).to(device))
+
+
+def context_flops(shape: ContextShape) -> int:
+    """Algorithmic flops of causal attention: each (query token, head) scores and weighs the
+    positions up to its own, 2 * D flops each for Q.K and for P.V."""
+    positions = sum(shape.cached + i + 1 for i in range(shape.q_len))
+    return shape.rows * positions * shape.q_heads * shape.head_dim * 4
