@@ -12,6 +12,7 @@ Drop-ins for the calls the reference's layer modules make
 - ``embedding.fill_placeholders`` / ``embedding(..., last_tokens=)`` (ModelRunner.fill_placeholders,
   miniagentserve/engine/model_runner.py:149-154, alone or fused with the gather)
 - ``attention.trtllm_batch_decode_with_kv_cache``                   (flashinfer.decode, :184-196)
+- ``attention.trtllm_batch_context_with_kv_cache``                  (flashinfer.prefill, :198-213)
 - ``fused.apply_rope_and_append_paged_kv_cache``                    (:163-166 + :170-173 + the llama-4
   query scale at :175-179, one kernel)
 
