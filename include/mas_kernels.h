@@ -220,6 +220,10 @@ int mas_embedding_fill_placeholders_bf16(void* out, int64_t out_stride, const vo
  * partials fit (mas_paged_decode_attention_workspace_bytes). A page id
  * outside [0, num_pages) skips its position (MAS_ERRBIT_PAGE); a seq_len outside
  * [0, max_blocks * page_size] is clamped (MAS_ERRBIT_POSITION); a row with no position gets zeros.
+ * With out_fp8, `out` receives e4m3fn codes (strides in elements, as for bf16): the output is
+ * rounded to bf16, then quantized as the reference quantizes the o_proj input
+ * (devstral2.py:93-95,110-111): e4m3fn(clamp(bf16(O) / scale, -448, 448)), scale read from
+ * out_scale_dev (an fp32 device scalar) or, when that is NULL, out_scale_host.
  * Replaces flashinfer.decode.trtllm_batch_decode_with_kv_cache at
  * miniagentserve/models/devstral2/devstral2.py:184-196 (kv_layout "NHD", no sliding window).
  */
@@ -229,7 +233,8 @@ int mas_paged_decode_attention_bf16(void* out, int64_t out_stride, int64_t out_h
                                     int64_t page_size, const int32_t* block_tables, int64_t block_table_stride,
                                     int64_t max_blocks, const int32_t* seq_lens, int64_t batch, int64_t num_q_heads,
                                     int64_t num_kv_heads, int64_t head_dim, float bmm1_scale, float bmm2_scale,
-                                    void* workspace, int64_t workspace_bytes, uint32_t* err, hipStream_t stream);
+                                    int out_fp8, const float* out_scale_dev, float out_scale_host, void* workspace,
+                                    int64_t workspace_bytes, uint32_t* err, hipStream_t stream);
 
 /*
  * Paged causal attention of prompt rows (context / chunked prefill): row j owns query tokens
@@ -242,6 +247,7 @@ int mas_paged_decode_attention_bf16(void* out, int64_t out_stride, int64_t out_h
  * sizes the grid). head_dim 64 or 128; page_size a power of two. A seq_len outside
  * [q_len, max_blocks * page_size] is clamped (MAS_ERRBIT_POSITION; tokens left before position 0
  * get zeros); a page id outside [0, num_pages) skips its position (MAS_ERRBIT_PAGE).
+ * out_fp8 / out_scale_dev / out_scale_host: the fp8 output as for mas_paged_decode_attention_bf16.
  * Replaces flashinfer.prefill.trtllm_batch_context_with_kv_cache at
  * miniagentserve/models/devstral2/devstral2.py:198-213 (kv_layout "NHD", no sliding window).
  */
@@ -252,7 +258,8 @@ int mas_paged_context_attention_bf16(void* out, int64_t out_stride, int64_t out_
                                      const int32_t* block_tables, int64_t block_table_stride, int64_t max_blocks,
                                      const int32_t* seq_lens, const int32_t* cu_seqlens_q, int64_t num_rows,
                                      int64_t max_q_len, int64_t num_q_heads, int64_t num_kv_heads,
-                                     int64_t head_dim, float bmm1_scale, float bmm2_scale, uint32_t* err,
+                                     int64_t head_dim, float bmm1_scale, float bmm2_scale, int out_fp8,
+                                     const float* out_scale_dev, float out_scale_host, uint32_t* err,
                                      hipStream_t stream);
 
 /*

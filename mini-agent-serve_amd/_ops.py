@@ -7,12 +7,21 @@ keeps each kernel as one opaque node instead of breaking its graph at a ctypes c
 """
 from __future__ import annotations
 
+from typing import Optional
+
 import torch
 from torch.library import custom_op
 
 from . import activation, attention, embedding, fused, norm, page, rope
 
 Tensor = torch.Tensor
+
+
+def _quant_scale(tensor: Optional[Tensor], host: float):
+    """The attention ops' fp8 output scale: a device scalar, a positive host float, or none (0)."""
+    if tensor is not None:
+        return tensor
+    return host if host > 0.0 else None
 
 
 @custom_op("mas::fused_add_rmsnorm", mutates_args=("input", "residual"))
@@ -140,28 +149,30 @@ def _(input_ids, last_tokens):
 
 @custom_op("mas::paged_decode_attention", mutates_args=("workspace", "out"))
 def _paged_decode_attention(query: Tensor, k_cache: Tensor, v_cache: Tensor, workspace: Tensor, block_tables: Tensor,
-                            seq_lens: Tensor, bmm1_scale: float, bmm2_scale: float, out: Tensor,
-                            kv_layout: str) -> None:
+                            seq_lens: Tensor, bmm1_scale: float, bmm2_scale: float, out: Tensor, kv_layout: str,
+                            quant_scale: Optional[Tensor] = None, quant_scale_host: float = 0.0) -> None:
     attention._decode(query, (k_cache, v_cache), workspace, block_tables, seq_lens, bmm1_scale, bmm2_scale, out,
-                      kv_layout, None)
+                      kv_layout, None, _quant_scale(quant_scale, quant_scale_host))
 
 
 @_paged_decode_attention.register_fake
-def _(query, k_cache, v_cache, workspace, block_tables, seq_lens, bmm1_scale, bmm2_scale, out, kv_layout):
+def _(query, k_cache, v_cache, workspace, block_tables, seq_lens, bmm1_scale, bmm2_scale, out, kv_layout,
+      quant_scale=None, quant_scale_host=0.0):
     return None
 
 
 @custom_op("mas::paged_context_attention", mutates_args=("out",))
 def _paged_context_attention(query: Tensor, k_cache: Tensor, v_cache: Tensor, block_tables: Tensor, seq_lens: Tensor,
                              cu_seqlens_q: Tensor, max_q_len: int, bmm1_scale: float, bmm2_scale: float, out: Tensor,
-                             kv_layout: str) -> None:
+                             kv_layout: str, quant_scale: Optional[Tensor] = None,
+                             quant_scale_host: float = 0.0) -> None:
     attention._context(query, (k_cache, v_cache), block_tables, seq_lens, cu_seqlens_q, max_q_len, bmm1_scale,
-                       bmm2_scale, out, kv_layout, None)
+                       bmm2_scale, out, kv_layout, None, _quant_scale(quant_scale, quant_scale_host))
 
 
 @_paged_context_attention.register_fake
 def _(query, k_cache, v_cache, block_tables, seq_lens, cu_seqlens_q, max_q_len, bmm1_scale, bmm2_scale, out,
-      kv_layout):
+      kv_layout, quant_scale=None, quant_scale_host=0.0):
     return None
 
 

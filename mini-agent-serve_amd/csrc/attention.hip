@@ -44,8 +44,11 @@ struct DecodeArgs {
   float out_scale;   // bmm2_scale
   float* part_o;     // [batch][hq][max_splits][D]
   float* part_ml;    // [batch][hq][max_splits][2]: running max (log2 domain), sum
-  uint16_t* out;
+  void* out;                // bf16, or fp8 e4m3fn codes when out_fp8
   int64_t out_stride, out_head_stride;
+  int out_fp8;              // out = e4m3fn(clamp(bf16(O) / quant scale, +-448)): the o_proj input quantize
+  const float* quant_scale_dev;
+  float quant_scale_host;
   uint32_t* err;
 };
 
@@ -370,14 +373,43 @@ __global__ __launch_bounds__(64) void decode_attn_combine(DecodeArgs a) {
   }
   const float denom = wave_sum(lsum);
   const float scale = denom > 0.f ? a.out_scale / denom : 0.f;
-  uint16_t* dst = a.out + b * a.out_stride + h * a.out_head_stride + DPL * lane;
+  const int64_t at = b * a.out_stride + h * a.out_head_stride + DPL * lane;
+  uint32_t y[(DPL + 1) / 2];  // bf16 pairs
   if constexpr (DPL == 1) {
-    dst[0] = static_cast<uint16_t>(pack_bf16x2(acc[0] * scale, 0.f));
-  } else if constexpr (DPL == 2) {
-    *reinterpret_cast<uint32_t*>(dst) = pack_bf16x2(acc[0] * scale, acc[1] * scale);
+    y[0] = pack_bf16x2(acc[0] * scale, 0.f);
   } else {
-    *reinterpret_cast<u32x2*>(dst) =
-        u32x2{pack_bf16x2(acc[0] * scale, acc[1] * scale), pack_bf16x2(acc[2] * scale, acc[3] * scale)};
+#pragma unroll
+    for (int e = 0; e < DPL / 2; ++e) y[e] = pack_bf16x2(acc[2 * e] * scale, acc[2 * e + 1] * scale);
+  }
+  if (a.out_fp8) {
+    // the quantize the reference applies to the bf16 attention output (devstral2.py:93-95,110-111)
+    const float qs = a.quant_scale_dev != nullptr ? *a.quant_scale_dev : a.quant_scale_host;
+    const float rcp = 1.0f / qs;
+    float qv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int ee = e < DPL ? e : 0;
+      const float v = (ee & 1) ? bf16_hi(y[ee / 2]) : bf16_lo(y[ee / 2]);
+      qv[e] = div_by_scale(v, qs, rcp);
+    }
+    const uint32_t codes = fp8x4_saturate_encode(qv[0], qv[1], qv[2], qv[3]);
+    uint8_t* dst = static_cast<uint8_t*>(a.out) + at;
+    if constexpr (DPL == 1) {
+      dst[0] = static_cast<uint8_t>(codes);
+    } else if constexpr (DPL == 2) {
+      *reinterpret_cast<uint16_t*>(dst) = static_cast<uint16_t>(codes);
+    } else {
+      *reinterpret_cast<uint32_t*>(dst) = codes;
+    }
+  } else {
+    uint16_t* dst = static_cast<uint16_t*>(a.out) + at;
+    if constexpr (DPL == 1) {
+      dst[0] = static_cast<uint16_t>(y[0]);
+    } else if constexpr (DPL == 2) {
+      *reinterpret_cast<uint32_t*>(dst) = y[0];
+    } else {
+      *reinterpret_cast<u32x2*>(dst) = u32x2{y[0], y[1]};
+    }
   }
 }
 
@@ -422,7 +454,8 @@ extern "C" int mas_paged_decode_attention_bf16(void* out, int64_t out_stride, in
                                                const int32_t* block_tables, int64_t block_table_stride,
                                                int64_t max_blocks, const int32_t* seq_lens, int64_t batch,
                                                int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
-                                               float bmm1_scale, float bmm2_scale, void* workspace,
+                                               float bmm1_scale, float bmm2_scale, int out_fp8,
+                                               const float* out_scale_dev, float out_scale_host, void* workspace,
                                                int64_t workspace_bytes, uint32_t* err, hipStream_t stream) {
   using namespace mas;
   if (batch < 0 || num_q_heads < 0 || num_kv_heads < 0 || num_pages < 0 || page_size <= 0 || max_blocks < 0 ||
@@ -439,6 +472,7 @@ extern "C" int mas_paged_decode_attention_bf16(void* out, int64_t out_stride, in
   if (out == nullptr || q == nullptr || seq_lens == nullptr || (cap > 0 && (k_cache == nullptr || v_cache == nullptr ||
                                                                             block_tables == nullptr || num_pages == 0)))
     return MAS_ERR_INVALID_VALUE;
+  if (out_fp8 && out_scale_dev == nullptr && !(out_scale_host > 0.f)) return MAS_ERR_INVALID_VALUE;
   const bool aligned = aligned16(q) && aligned16(out) && q_stride % 8 == 0 && q_head_stride % 8 == 0 &&
                        out_stride % 8 == 0 && out_head_stride % 8 == 0 &&
                        (cap == 0 || (aligned16(k_cache) && aligned16(v_cache) && page_stride % 8 == 0 &&
@@ -490,9 +524,12 @@ extern "C" int mas_paged_decode_attention_bf16(void* out, int64_t out_stride, in
   a.out_scale = bmm2_scale;
   a.part_o = static_cast<float*>(workspace);
   a.part_ml = a.part_o + batch * num_q_heads * splits * head_dim;
-  a.out = static_cast<uint16_t*>(out);
+  a.out = out;
   a.out_stride = out_stride;
   a.out_head_stride = out_head_stride;
+  a.out_fp8 = out_fp8 != 0;
+  a.quant_scale_dev = out_scale_dev;
+  a.quant_scale_host = out_scale_host;
   a.err = err;
   switch (head_dim) {
     case 64: return dispatch_group<64>(a, batch, num_kv_heads, stream);

@@ -47,8 +47,11 @@ struct ContextArgs {
   int hq, hk, group, heads_per_wg, log2_page;
   float scale_log2;
   float out_scale;
-  uint16_t* out;
+  void* out;                // bf16, or fp8 e4m3fn codes when out_fp8
   int64_t out_stride, out_head_stride;
+  int out_fp8;              // out = e4m3fn(clamp(bf16(O) / quant scale, +-448)): the o_proj input quantize
+  const float* quant_scale_dev;
+  float quant_scale_host;
   uint32_t* err;
 };
 
@@ -304,17 +307,27 @@ __global__ __launch_bounds__(256, MAS_CTX_MIN_WG) void context_attn(ContextArgs 
   }
 
   if (!wave_live) return;
-  // ---- out[token][h][16 dt + 4 r + i] = O / l * bmm2_scale
+  // ---- out[token][h][16 dt + 4 r + i] = O / l * bmm2_scale (bf16), or its fp8 quantize
+  const float qs = a.out_fp8 ? (a.quant_scale_dev != nullptr ? *a.quant_scale_dev : a.quant_scale_host) : 1.f;
+  const float rcp = 1.0f / qs;
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     const int t = tok + 16 * nt + n;
     if (t >= q_len) continue;
     const float sc = l_run[nt] > 0.f ? a.out_scale / l_run[nt] : 0.f;
-    uint16_t* dst = a.out + static_cast<int64_t>(q0 + t) * a.out_stride + h * a.out_head_stride + 4 * r;
+    const int64_t at = static_cast<int64_t>(q0 + t) * a.out_stride + h * a.out_head_stride + 4 * r;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       const f32x4 o = acc[nt][dt];
-      *reinterpret_cast<u32x2*>(dst + 16 * dt) = u32x2{pack_bf16x2(o[0] * sc, o[1] * sc), pack_bf16x2(o[2] * sc, o[3] * sc)};
+      const uint32_t y0 = pack_bf16x2(o[0] * sc, o[1] * sc), y1 = pack_bf16x2(o[2] * sc, o[3] * sc);
+      if (a.out_fp8) {
+        // the quantize the reference applies to the bf16 attention output (devstral2.py:93-95,110-111)
+        *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.out) + at + 16 * dt) =
+            fp8x4_saturate_encode(div_by_scale(bf16_lo(y0), qs, rcp), div_by_scale(bf16_hi(y0), qs, rcp),
+                                  div_by_scale(bf16_lo(y1), qs, rcp), div_by_scale(bf16_hi(y1), qs, rcp));
+      } else {
+        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.out) + at + 16 * dt) = u32x2{y0, y1};
+      }
     }
   }
 }
@@ -330,7 +343,8 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
                                                 int64_t max_blocks, const int32_t* seq_lens,
                                                 const int32_t* cu_seqlens_q, int64_t num_rows, int64_t max_q_len,
                                                 int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
-                                                float bmm1_scale, float bmm2_scale, uint32_t* err,
+                                                float bmm1_scale, float bmm2_scale, int out_fp8,
+                                                const float* out_scale_dev, float out_scale_host, uint32_t* err,
                                                 hipStream_t stream) {
   using namespace mas;
   if (num_rows < 0 || max_q_len < 0 || num_q_heads < 0 || num_kv_heads < 0 || num_pages < 0 || page_size <= 0 ||
@@ -339,6 +353,7 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   if (num_rows == 0 || max_q_len == 0 || num_q_heads == 0) return MAS_OK;
   if (num_kv_heads == 0 || num_q_heads % num_kv_heads != 0) return MAS_ERR_INVALID_VALUE;
   if (!(bmm1_scale > 0.f)) return MAS_ERR_INVALID_VALUE;  // the row max is taken over unscaled scores
+  if (out_fp8 && out_scale_dev == nullptr && !(out_scale_host > 0.f)) return MAS_ERR_INVALID_VALUE;
   if ((head_dim != 64 && head_dim != 128) || (page_size & (page_size - 1)) != 0) return MAS_ERR_UNSUPPORTED;
   const int64_t cap = max_blocks * page_size;
   if (cap > (int64_t{1} << 30) || num_rows > 65535 || num_q_heads > 65535) return MAS_ERR_UNSUPPORTED;
@@ -380,9 +395,12 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   a.log2_page = log2_page;
   a.scale_log2 = bmm1_scale * 1.4426950408889634f;
   a.out_scale = bmm2_scale;
-  a.out = static_cast<uint16_t*>(out);
+  a.out = out;
   a.out_stride = out_stride;
   a.out_head_stride = out_head_stride;
+  a.out_fp8 = out_fp8 != 0;
+  a.quant_scale_dev = out_scale_dev;
+  a.quant_scale_host = out_scale_host;
   a.err = err;
   const dim3 grid(static_cast<uint32_t>(gx), static_cast<uint32_t>(gy), static_cast<uint32_t>(num_rows));
   if (head_dim == 64) {

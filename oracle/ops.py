@@ -58,12 +58,17 @@ def silu_and_mul(x_bits):
     return f32_to_bf16(y)
 
 
+def quantize_activation(y_bits, scale: float):
+    """The quantize FP8Linear.forward applies to a bf16 input (devstral2.py:93-95,110-111):
+    e4m3fn(clamp(f32(y) / scale, -448, 448)). Returns fp8 codes."""
+    with np.errstate(invalid="ignore"):
+        return f32_to_fp8_saturate(bf16_to_f32(y_bits) / F32(scale))
+
+
 def silu_and_mul_quant(x_bits, scale: float):
     """SiluAndMul (devstral2.py:224) followed by the quantize down_proj applies to its bf16 result
-    (devstral2.py:93-95,110-111): e4m3fn(clamp(f32(y) / scale, -448, 448)), y the bf16 SiluAndMul
-    output. Returns fp8 codes."""
-    y = bf16_to_f32(silu_and_mul(x_bits))
-    return f32_to_fp8_saturate(y / F32(scale))
+    (devstral2.py:93-95,110-111). Returns fp8 codes."""
+    return quantize_activation(silu_and_mul(x_bits), scale)
 
 
 def rope(q_bits, k_bits, positions, table, is_neox: bool = True):

@@ -149,3 +149,42 @@ def test_decode_attention_in_graph_replays(mas, dev):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, want)
+
+
+@pytest.mark.parametrize("dim,hq,hk,scale_kind", [(128, 32, 8, "tensor"), (64, 16, 2, "float"),
+                                                 (256, 16, 1, "tensor")])
+def test_decode_attention_fp8_output_is_the_o_proj_quantize(mas, dev, dim, hq, hk, scale_kind):
+    """With out_quant_scale the kernel writes fp8(clamp(bf16(O) / scale, -448, 448)): bit for bit the
+    o_proj input quantize (devstral2.py:93-95,110-111) of its own bf16 output. The small scale
+    saturates part of the outputs."""
+    batch, ps, lens = 3, 32, [300, 1, 77]
+    q, kc, vc, tables, seq = _case(dim + hq, batch, hq, hk, dim, ps, lens)
+    ref = _run(mas, dev, q, kc, vc, tables, seq, 0.3, scale2=4.0)
+    for s in (0.004, 0.37):
+        scale = torch.tensor([s], dtype=torch.float32, device=dev) if scale_kind == "tensor" else s
+        ws = torch.zeros(128 << 20, dtype=torch.uint8, device=dev)
+        out = mas.attention.trtllm_batch_decode_with_kv_cache(
+            q.to(dev), (kc.to(dev), vc.to(dev)), ws, tables.to(dev), seq.to(dev), 0, 0.3, 4.0,
+            kv_layout="NHD", out_quant_scale=scale)
+        assert out.dtype == torch.float8_e4m3fn and tuple(out.shape) == (batch, hq, dim)
+        codes = out.view(torch.uint8).cpu().numpy()
+        np.testing.assert_array_equal(codes, ops.quantize_activation(bits(ref), s))
+        torch_q = (ref.float() / s).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+        assert torch.equal(out.view(torch.uint8), torch_q.view(torch.uint8))
+    assert np.mean(np.abs(on.bf16_to_f32(bits(ref))) / 0.004 > 448.0) > 0.01
+
+
+def test_decode_attention_fp8_output_argument_checks(mas, dev):
+    batch, hq, hk, dim, ps, lens = 2, 8, 2, 128, 16, [20, 5]
+    q, kc, vc, tables, seq = _case(2, batch, hq, hk, dim, ps, lens)
+    ws = torch.zeros(1 << 20, dtype=torch.uint8, device=dev)
+    args = (q.to(dev), (kc.to(dev), vc.to(dev)), ws, tables.to(dev), seq.to(dev), 0, 0.1, 1.0)
+    with pytest.raises(ValueError):       # fp8 output without a scale
+        mas.attention.trtllm_batch_decode_with_kv_cache(*args, out_dtype=torch.float8_e4m3fn)
+    with pytest.raises(TypeError):        # a scale with a bf16 output
+        mas.attention.trtllm_batch_decode_with_kv_cache(*args, out=torch.empty(batch, hq, dim, dtype=torch.bfloat16,
+                                                                               device=dev), out_quant_scale=0.5)
+    with pytest.raises(ValueError):
+        mas.attention.trtllm_batch_decode_with_kv_cache(*args, out_quant_scale=0.0)
+    with pytest.raises(ValueError):
+        mas.attention.trtllm_batch_decode_with_kv_cache(*args, out_quant_scale=torch.ones(2, device=dev))

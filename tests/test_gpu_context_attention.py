@@ -123,3 +123,24 @@ def test_context_attention_in_graph_replays(mas, dev):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, want)
+
+
+@pytest.mark.parametrize("dim,hq,hk,scale_kind", [(128, 32, 8, "tensor"), (64, 6, 2, "float")])
+def test_context_attention_fp8_output_is_the_o_proj_quantize(mas, dev, dim, hq, hk, scale_kind):
+    """With out_quant_scale the kernel writes fp8(clamp(bf16(O) / scale, -448, 448)): bit for bit the
+    o_proj input quantize (devstral2.py:93-95,110-111) of its own bf16 output."""
+    q_lens, kv_lens, ps = [70, 3], [90, 3], 16
+    q, kc, vc, tables, seq, cu = _case(dim + hq, q_lens, kv_lens, hq, hk, dim, ps)
+    ref = _run(mas, dev, q, kc, vc, tables, seq, cu, 0.2, scale2=4.0)
+    ws = torch.zeros(16, dtype=torch.uint8, device=dev)
+    for s in (0.004, 0.37):
+        scale = torch.tensor(s, dtype=torch.float32, device=dev) if scale_kind == "tensor" else s
+        out = mas.attention.trtllm_batch_context_with_kv_cache(
+            q.to(dev), (kc.to(dev), vc.to(dev)), ws, tables.to(dev), seq.to(dev), max(q_lens), 0, 0.2, 4.0,
+            len(q_lens), cu.to(dev), None, kv_layout="NHD", out_quant_scale=scale)
+        assert out.dtype == torch.float8_e4m3fn and tuple(out.shape) == tuple(q.shape)
+        codes = out.view(torch.uint8).cpu().numpy()
+        np.testing.assert_array_equal(codes, ops.quantize_activation(bits(ref), s))
+        torch_q = (ref.float() / s).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+        assert torch.equal(out.view(torch.uint8), torch_q.view(torch.uint8))
+    assert np.mean(np.abs(on.bf16_to_f32(bits(ref))) / 0.004 > 448.0) > 0.01

@@ -150,6 +150,19 @@ def test_silu_and_mul_quant_matches_reference_quantize():
             assert np.any(np.abs(gv) == 448.0)
 
 
+
+def test_quantize_activation_matches_reference_quantize_exhaustively():
+    """The o_proj / down_proj input quantize on every finite bf16 value: bit for bit
+    (y.float() / scale).clamp(-448, 448).to(float8_e4m3fn), with saturation at both ends."""
+    y = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    yt = torch.from_numpy(y.view(np.int16)).view(torch.bfloat16)
+    finite = torch.isfinite(yt).numpy()
+    for scale in (0.0037, 0.5, 3.0):
+        got = ops.quantize_activation(y, scale)
+        want = (yt.float() / scale).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+        np.testing.assert_array_equal(got[finite], want[finite])
+        assert np.all(on.fp8_to_f32(got[finite]) <= 448.0)
+
 # ---- RoPE -----------------------------------------------------------------------------------------
 
 def _hf_rope(q, k, positions, table):
