@@ -345,6 +345,49 @@ def test_kv_duplicates_and_index_errors(mas, dev):
     assert int((kc != 0).sum()) == 2 * heads * dim - int((bits(key)[[0, 2]] == 0).sum())
 
 
+
+def test_kv_store_prefill_sized_skips_and_flags_bad_tokens(mas, dev):
+    """A prefill-sized step with bad tokens scattered through it: each bad token is skipped and
+    flagged, and every other row lands where the oracle puts it (block-table and slot forms)."""
+    g = torch.Generator().manual_seed(71)
+    ps, heads, dim, lens = 64, 8, 128, [1500, 700, 3]
+    width = -(-max(lens) // ps)
+    pages = len(lens) * width + 5
+    tables, indptr, bidx, pos = _kv_case(g, pages, ps, heads, dim, lens, width)
+    n = len(pos)
+    key, val = _randn_bf16(g, n, heads, dim), _randn_bf16(g, n, heads, dim)
+    k0 = torch.randn(pages, ps, heads, dim, generator=g).bfloat16()
+    v0 = torch.randn(pages, ps, heads, dim, generator=g).bfloat16()
+    keep = np.ones(n, dtype=bool)
+    bad_pos, bad_b, bad_idx = pos.clone(), bidx.clone(), tables.clone()
+    bad_pos[10] = -3                                   # negative position: bit 4
+    bad_b[700] = 3                                     # batch 3 of 3: bit 2
+    bad_pos[n - 1] = ps * width + 5                    # past its row's pages: bit 8
+    bad_idx[1, 2] = pages + 7                          # a page past the cache for 64 tokens of row 1: bit 8
+    keep[[10, 700, n - 1]] = False
+    keep[1500 + 2 * ps:1500 + 3 * ps] = False
+    want_k, want_v = ops.append_paged_kv_cache(bits(k0), bits(v0), bits(key)[keep], bits(val)[keep],
+                                               bidx.numpy()[keep], pos.numpy()[keep], tables.flatten().numpy(),
+                                               indptr.numpy())
+    kc, vc = k0.to(dev), v0.to(dev)
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    mas.append_paged_kv_cache(key.to(dev), val.to(dev), bad_b.to(dev), bad_pos.to(dev), (kc, vc),
+                              bad_idx.flatten().to(dev), indptr.to(dev), None, "NHD", error_flags=flags)
+    assert int(flags.item()) == 2 | 4 | 8
+    assert np.array_equal(bits(kc), want_k) and np.array_equal(bits(vc), want_v)
+    # slot form: negative slots skipped silently, slots past the cache flagged
+    slots = mas.page.slot_mapping_from_block_tables(tables, bidx, pos, ps)
+    slots[[5, 2100]] = -1
+    slots[[6, 2199]] = pages * ps + 1
+    skeep = (slots >= 0) & (slots < pages * ps)
+    want_k, want_v = ops.store_kv_slots(bits(k0), bits(v0), bits(key), bits(val),
+                                        np.where(skeep.numpy(), slots.numpy(), -1))
+    kc, vc = k0.to(dev), v0.to(dev)
+    flags.zero_()
+    mas.store_kv_slots(key.to(dev), val.to(dev), kc, vc, slots.to(dev), error_flags=flags)
+    assert int(flags.item()) == 16
+    assert np.array_equal(bits(kc), want_k) and np.array_equal(bits(vc), want_v)
+
 # ---- embedding ----------------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("rows,vocab,hidden", [(1, 10, 8), (7, 100, 5120), (256, 4096, 5120), (5, 30, 100),
