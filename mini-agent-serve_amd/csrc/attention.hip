@@ -25,8 +25,6 @@
 namespace mas {
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-
 constexpr int kChunk = 256;          // positions per chunk
 constexpr float kNegInf = -__builtin_huge_valf();
 
@@ -97,6 +95,10 @@ __device__ __forceinline__ u32x4 attn_load_v(const uint16_t* p) {
 #define MAS_ATTN_WG_WAVES 1
 #endif
 constexpr int kAttnWaves = MAS_ATTN_WG_WAVES;
+// Wavefronts per SIMD the split kernel's registers are capped for (two load buffers of a step each).
+#ifndef MAS_ATTN_MIN_WAVES
+#define MAS_ATTN_MIN_WAVES 2
+#endif
 
 // Orders this wavefront's LDS writes before its later reads (and reads before later writes).
 __device__ __forceinline__ void wave_lds_sync() {
@@ -115,12 +117,15 @@ struct StepLoads {
   bool vok[VPS];
 };
 
-// Issues the key and value loads of the step at position ps. Page ids come from pg (the chunk's
-// block-table entries in LDS, first = the chunk's first block index); rows of masked positions
-// (past `end`, or with a page id outside the cache) are loaded from row 0 of page 0 and flagged.
-template <int D>
+// Issues the key and value loads of the step at position ps. With kBig (pages of at least 256
+// positions) the step lies in one page, whose id `page_u` the caller read as a scalar; otherwise
+// page ids come from pg (the chunk's block-table entries in LDS, first = the chunk's first block
+// index). Rows of masked positions (past `end`, or with a page id outside the cache) are loaded
+// from row 0 of page 0 and flagged; `bad` collects out-of-range page ids of real positions.
+template <int D, bool kBig>
 __device__ __forceinline__ void issue_step(const DecodeArgs& a, StepLoads<D>& st, int ps, int end, int kvh,
-                                           const int32_t* pg, int first, int n, int r, int pv_d, int pv_grp) {
+                                           const int32_t* pg, int first, int32_t page_u, int n, int r, int pv_d,
+                                           int pv_grp, bool& bad) {
   constexpr int PPW = 64 / (D / 8);
   const int mask = (1 << a.log2_page) - 1;
 #pragma unroll
@@ -128,26 +133,43 @@ __device__ __forceinline__ void issue_step(const DecodeArgs& a, StepLoads<D>& st
     const int p = ps + 16 * t + n;
     const bool valid = p < end;
     const int pc = valid ? p : end - 1;
-    const int32_t page = pg[(pc >> a.log2_page) - first];
+    const int32_t page = kBig ? page_u : pg[(pc >> a.log2_page) - first];
     const bool ok = page >= 0 && page < a.num_pages;
-    if (valid && !ok && r == 0) report(a.err, MAS_ERRBIT_PAGE);
+    bad |= valid && !ok;
     st.kok[t] = valid && ok;
-    const int64_t row = (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
-                        static_cast<int64_t>(pc & mask) * a.entry_stride + kvh * a.head_stride;
+    if constexpr (kBig) {
+      // the page's base is wave-uniform; the in-page byte offset fits 32 bits (checked at launch)
+      const char* base = reinterpret_cast<const char*>(a.k_cache + (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
+                                                       kvh * a.head_stride);
+      const uint32_t off = 2u * (static_cast<uint32_t>(pc & mask) * static_cast<uint32_t>(a.entry_stride) + 8u * r);
 #pragma unroll
-    for (int ks = 0; ks < StepLoads<D>::KS; ++ks) st.k[t][ks] = attn_load_k(a.k_cache + row + 32 * ks + 8 * r);
+      for (int ks = 0; ks < StepLoads<D>::KS; ++ks)
+        st.k[t][ks] = attn_load_k(reinterpret_cast<const uint16_t*>(base + (off + 64u * ks)));
+    } else {
+      const int64_t row = (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
+                          static_cast<int64_t>(pc & mask) * a.entry_stride + kvh * a.head_stride;
+#pragma unroll
+      for (int ks = 0; ks < StepLoads<D>::KS; ++ks) st.k[t][ks] = attn_load_k(a.k_cache + row + 32 * ks + 8 * r);
+    }
   }
 #pragma unroll
   for (int u = 0; u < StepLoads<D>::VPS; ++u) {
     const int p = ps + PPW * u + pv_grp;
     const bool valid = p < end;
     const int pc = valid ? p : end - 1;
-    const int32_t page = pg[(pc >> a.log2_page) - first];
+    const int32_t page = kBig ? page_u : pg[(pc >> a.log2_page) - first];
     const bool ok = page >= 0 && page < a.num_pages;
     st.vok[u] = valid && ok;
-    const int64_t row = (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
-                        static_cast<int64_t>(pc & mask) * a.entry_stride + kvh * a.head_stride;
-    st.v[u] = attn_load_v(a.v_cache + row + 8 * pv_d);
+    if constexpr (kBig) {
+      const char* base = reinterpret_cast<const char*>(a.v_cache + (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
+                                                       kvh * a.head_stride);
+      const uint32_t off = 2u * (static_cast<uint32_t>(pc & mask) * static_cast<uint32_t>(a.entry_stride) + 8u * pv_d);
+      st.v[u] = attn_load_v(reinterpret_cast<const uint16_t*>(base + off));
+    } else {
+      const int64_t row = (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
+                          static_cast<int64_t>(pc & mask) * a.entry_stride + kvh * a.head_stride;
+      st.v[u] = attn_load_v(a.v_cache + row + 8 * pv_d);
+    }
   }
 }
 
@@ -159,8 +181,8 @@ __device__ __forceinline__ void issue_step(const DecodeArgs& a, StepLoads<D>& st
 // the reduction). P enters as two bf16 terms, hi = bf16(P) and lo = bf16(P - hi), two MFMAs per
 // tile, so it keeps ~16 significant bits (one bf16 term alone rounds it to 8). O stays in
 // 4 * D / 16 accumulator registers whatever the group size.
-template <int GP, int D>
-__global__ __launch_bounds__(64 * kAttnWaves) void decode_attn_split(DecodeArgs a) {
+template <int GP, int D, bool kBig>
+__global__ __launch_bounds__(64 * kAttnWaves, D <= 128 ? MAS_ATTN_MIN_WAVES : 1) void decode_attn_split(DecodeArgs a) {
   constexpr int KS = D / 32;
   constexpr int DT = D / 16;               // MFMA tiles over the head dim for P.V
   constexpr int LPP = D / 8;               // value-row layout: lanes per row
@@ -169,7 +191,8 @@ __global__ __launch_bounds__(64 * kAttnWaves) void decode_attn_split(DecodeArgs 
   constexpr int VPS = kStep / PPW;
   constexpr int RG = GP / 4;
   constexpr bool kPrefetch = D <= 128;
-  constexpr int VROW = D + 4;              // bf16 per LDS value row: rows 8 apart start 16 banks apart
+  constexpr int VROW = D + 16;             // bf16 per LDS value row: the 4 rows of a transposing read
+                                           // start 8 banks apart
   constexpr int PROW = kStep + 8;          // bf16 per LDS P row: 16-byte aligned, conflict-free reads
   constexpr int kChunkPages = 257;         // block-table entries one 256-position chunk can touch
   __shared__ __align__(16) uint16_t v_lds_all[kAttnWaves][kStep * VROW];
@@ -225,44 +248,45 @@ __global__ __launch_bounds__(64 * kAttnWaves) void decode_attn_split(DecodeArgs 
   for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int nsteps = (end - start + kStep - 1) / kStep;
-  int first = load_pages(start);
-  StepLoads<D> cur, nxt;
-  issue_step<D>(a, cur, start, end, kvh, pg_lds, first, n, r, pv_d, pv_grp);
-  for (int i = 0; i < nsteps; ++i) {
-    const int ps = start + i * kStep;
-    if constexpr (kPrefetch) {
-      if (i + 1 < nsteps) {
-        if (((i + 1) & 7) == 0) first = load_pages(ps + kStep);  // the next step opens a new chunk
-        issue_step<D>(a, nxt, ps + kStep, end, kvh, pg_lds, first, n, r, pv_d, pv_grp);
-      }
-    }
+  int first = kBig ? 0 : load_pages(start);
 
+  // One step over the loads of `c`: scores, online softmax, P.V.
+  auto compute = [&](const StepLoads<D>& c) {
     // ---- scores (lane: heads 4r+i at positions ps + 16 t + n)
     f32x4 s[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      f32x4 c = {0.f, 0.f, 0.f, 0.f};
+      f32x4 acc_s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[ks], __builtin_bit_cast(bf16x8, cur.k[t][ks]), c, 0, 0, 0);
+        acc_s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[ks], __builtin_bit_cast(bf16x8, c.k[t][ks]), acc_s, 0, 0, 0);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) s[t][j] = cur.kok[t] ? c[j] * a.scale_log2 : kNegInf;
+      for (int j = 0; j < 4; ++j) s[t][j] = c.kok[t] ? acc_s[j] * a.scale_log2 : kNegInf;
     }
 
     // ---- online softmax; O (same layout) rescaled by alpha
     wave_lds_sync();  // the previous step's LDS reads are done
+    float alpha[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float mx = row_max16(fmaxf(s[0][j], s[1][j]));
       const float m_new = fmaxf(m_run[j], mx);
       const float m_use = m_new == kNegInf ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_use);
+      alpha[j] = __builtin_amdgcn_exp2f(m_run[j] - m_use);
       s[0][j] = __builtin_amdgcn_exp2f(s[0][j] - m_use);
       s[1][j] = __builtin_amdgcn_exp2f(s[1][j] - m_use);
-      l_run[j] = l_run[j] * alpha + row_sum16(s[0][j] + s[1][j]);
+      l_run[j] = l_run[j] * alpha[j] + row_sum16(s[0][j] + s[1][j]);
       m_run[j] = m_new;
+    }
+    // O is rescaled only when some row's max moved (alpha == 1 leaves it unchanged anyway)
+    if (__builtin_amdgcn_ballot_w64(alpha[0] != 1.f || alpha[1] != 1.f || alpha[2] != 1.f || alpha[3] != 1.f)) {
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) acc[dt][j] *= alpha;
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[dt][j] *= alpha[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
       if (r < RG) {
         const uint32_t hi = pack_bf16x2(s[0][j], s[1][j]);
         const uint32_t lo = pack_bf16x2(s[0][j] - bf16_lo(hi), s[1][j] - bf16_hi(hi));
@@ -277,7 +301,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void decode_attn_split(DecodeArgs 
     // value rows into LDS (masked rows zeroed)
 #pragma unroll
     for (int u = 0; u < VPS; ++u) {
-      const u32x4 v = cur.vok[u] ? cur.v[u] : u32x4{0u, 0u, 0u, 0u};
+      const u32x4 v = c.vok[u] ? c.v[u] : u32x4{0u, 0u, 0u, 0u};
       uint16_t* dst = v_lds + (PPW * u + pv_grp) * VROW + 8 * pv_d;
       *reinterpret_cast<u32x2*>(dst) = u32x2{v[0], v[1]};
       *reinterpret_cast<u32x2*>(dst + 4) = u32x2{v[2], v[3]};
@@ -289,23 +313,55 @@ __global__ __launch_bounds__(64 * kAttnWaves) void decode_attn_split(DecodeArgs 
     const bf16x8 pa_lo = *reinterpret_cast<const bf16x8*>(p_lds[1] + n * PROW + 8 * r);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      uint16_t e[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) e[j] = v_lds[(8 * r + j) * VROW + 16 * dt + n];
-      const u32x4 packed = {e[0] | (static_cast<uint32_t>(e[1]) << 16), e[2] | (static_cast<uint32_t>(e[3]) << 16),
-                            e[4] | (static_cast<uint32_t>(e[5]) << 16), e[6] | (static_cast<uint32_t>(e[7]) << 16)};
-      const bf16x8 vb = __builtin_bit_cast(bf16x8, packed);
+      // lane (n, r): positions 8r .. 8r + 7 of head-dim column 16 dt + n, as P's operand holds them
+      const i16x4 lo = read_column4(v_lds, VROW, 8 * r, 16 * dt, n);
+      const i16x4 hi = read_column4(v_lds, VROW, 8 * r + 4, 16 * dt, n);
+      const bf16x8 vb = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa_lo, vb, acc[dt], 0, 0, 0);
       acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa_hi, vb, acc[dt], 0, 0, 0);
     }
+  };
+  // Issues step j's loads. Small pages: the chunk's block-table entries go to LDS when step j opens
+  // a chunk. Big pages: the step's page id is one scalar load, so no wait on the vector loads in
+  // flight is needed to find it.
+  bool bad = false;
+  auto issue = [&](StepLoads<D>& dst, int j) {
+    const int ps = start + j * kStep;
+    if constexpr (kBig) {
+      issue_step<D, true>(a, dst, ps, end, kvh, nullptr, 0, bt[ps >> a.log2_page], n, r, pv_d, pv_grp, bad);
+    } else {
+      if (j > 0 && (j & 7) == 0) first = load_pages(ps);
+      issue_step<D, false>(a, dst, ps, end, kvh, pg_lds, first, 0, n, r, pv_d, pv_grp, bad);
+    }
+  };
 
-    if constexpr (kPrefetch) {
-      cur = nxt;
-    } else if (i + 1 < nsteps) {
-      if (((i + 1) & 7) == 0) first = load_pages(ps + kStep);
-      issue_step<D>(a, cur, ps + kStep, end, kvh, pg_lds, first, n, r, pv_d, pv_grp);
+  if constexpr (kPrefetch) {
+    // Two load buffers used in turn (no copy between them) and no branch around a load inside the
+    // loop, so computing a step waits only for its own loads while the next step's are in flight.
+    StepLoads<D> ld0, ld1;
+    issue(ld0, 0);
+    int i = 0;
+    for (; i + 2 < nsteps; i += 2) {
+      issue(ld1, i + 1);
+      compute(ld0);
+      issue(ld0, i + 2);
+      compute(ld1);
+    }
+    if (i + 1 < nsteps) {
+      issue(ld1, i + 1);
+      compute(ld0);
+      compute(ld1);
+    } else {
+      compute(ld0);
+    }
+  } else {
+    StepLoads<D> cur;
+    for (int i = 0; i < nsteps; ++i) {
+      issue(cur, i);
+      compute(cur);
     }
   }
+  if (__builtin_amdgcn_ballot_w64(bad) != 0 && lane == 0) report(a.err, MAS_ERRBIT_PAGE);
 
   // ---- partials: lane (n, r) holds O[head 4r+j][16 dt + n]
   const int64_t base = (static_cast<int64_t>(b) * a.hq + kvh * G) * a.max_splits + split;
@@ -415,10 +471,16 @@ __global__ __launch_bounds__(64) void decode_attn_combine(DecodeArgs a) {
 
 template <int GP, int D>
 int launch(const DecodeArgs& a, int64_t batch, int64_t hk, hipStream_t s) {
-  hipLaunchKernelGGL((decode_attn_split<GP, D>),
-                     dim3(static_cast<uint32_t>(cdiv(hk, kAttnWaves)), static_cast<uint32_t>(a.max_splits),
-                          static_cast<uint32_t>(batch)),
-                     dim3(64 * kAttnWaves), 0, s, a);
+  const dim3 grid(static_cast<uint32_t>(cdiv(hk, kAttnWaves)), static_cast<uint32_t>(a.max_splits),
+                  static_cast<uint32_t>(batch));
+  // Pages of at least one chunk: every 32-position step lies in one page, addressed from its base
+  // with 32-bit byte offsets (the largest in-page offset is checked here).
+  const int64_t page_size = int64_t{1} << a.log2_page;
+  const int64_t in_page = 2 * ((page_size - 1) * a.entry_stride + D);
+  if (page_size >= kChunk && in_page <= INT32_MAX)
+    hipLaunchKernelGGL((decode_attn_split<GP, D, true>), grid, dim3(64 * kAttnWaves), 0, s, a);
+  else
+    hipLaunchKernelGGL((decode_attn_split<GP, D, false>), grid, dim3(64 * kAttnWaves), 0, s, a);
   if (const int st = launch_status(); st != MAS_OK) return st;
   hipLaunchKernelGGL((decode_attn_combine<D>), dim3(static_cast<uint32_t>(a.hq), static_cast<uint32_t>(batch)),
                      dim3(64), 0, s, a);

@@ -26,10 +26,6 @@
 namespace mas {
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-
 constexpr int kTileP = 64;        // key positions per tile
 constexpr int kRowsPerWave = 32;  // query rows (tokens of one head) per wavefront
 constexpr float kNegInf = -__builtin_huge_valf();
@@ -54,15 +50,6 @@ struct ContextArgs {
   float quant_scale_host;
   uint32_t* err;
 };
-
-// Four values of one head-dim column from four consecutive value rows: in each group of 16 lanes,
-// lane k points at row first + k / 4, columns col0 + 4 (k % 4) .. + 3; lane n then holds rows
-// first .. first + 3 of column col0 + n.
-__device__ __forceinline__ i16x4 read_column4(const uint16_t* v_lds, int vrow, int first, int col0, int k) {
-  const uint16_t* p = v_lds + (first + (k >> 2)) * vrow + col0 + 4 * (k & 3);
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (lds_i16x4*)(__attribute__((address_space(3))) uint16_t*)(p));
-}
 
 // Workgroups per CU the register allocation must allow (2: at most 256 VGPRs per lane).
 #ifndef MAS_CTX_MIN_WG

@@ -14,6 +14,9 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr int kWave = 64;
 
@@ -133,6 +136,15 @@ __device__ __forceinline__ float block_sum(float v, float* slots) {
   float t = 0.f;
   for (int i = 0; i < nwaves; ++i) t += slots[i];
   return t;
+}
+
+// Four values of one column of a row-major bf16 tile in LDS (rows vrow elements apart) from four
+// consecutive rows, with gfx950's transposing LDS read: in each group of 16 lanes, lane k points
+// at row first + k / 4, columns col0 + 4 (k % 4) .. + 3; lane n then holds rows first .. first + 3
+// of column col0 + n.
+__device__ __forceinline__ i16x4 read_column4(const uint16_t* lds_tile, int vrow, int first, int col0, int k) {
+  const uint16_t* p = lds_tile + (first + (k >> 2)) * vrow + col0 + 4 * (k & 3);
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(__attribute__((address_space(3))) uint16_t*)(p));
 }
 
 __device__ __forceinline__ void report(uint32_t* err, uint32_t bit) {
