@@ -14,8 +14,8 @@
 // owns 32 query rows: 32 consecutive tokens of one query head; the four wavefronts cover up to four
 // heads of the kv head's group (or, for groups of 1 or 2, more tokens of fewer heads), so every
 // 64-position key / value tile they stage in LDS serves 128 query rows. Per tile:
-//   S^T = K Q^T on MFMA (v_mfma_f32_16x16x32_bf16; A = 16 key rows read from LDS, B = the
-//   wavefront's query rows, held in registers), causal mask, online softmax per query row, then
+//   S^T = K Q^T on MFMA (v_mfma_f32_32x32x16_bf16; A = 32 key rows read from LDS, B = the
+//   wavefront's 32 query rows, held in registers), causal mask, online softmax per query row, then
 //   O^T += V^T P^T on MFMA, where P^T is packed to bf16 straight from the S^T accumulators and V^T
 //   is read from the row-major value tile with gfx950's transposing LDS read (ds_read_b64_tr_b16:
 //   in each group of 16 lanes, lane 4a + b receives element b of the 4-element rows that lanes
@@ -56,10 +56,18 @@ struct ContextArgs {
 #define MAS_CTX_MIN_WG 2
 #endif
 
-template <int D>
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// v_mfma_f32_32x32x16_bf16 (checked on MI355X): lane l, element e of A holds A[l % 32][8 (l / 32) + e],
+// of B holds B[8 (l / 32) + e][l % 32]; element j of the result holds D[8 (j / 4) + 4 (l / 32) + j % 4][l % 32].
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+template <int D, bool kTilePages>
 __global__ __launch_bounds__(256, MAS_CTX_MIN_WG) void context_attn(ContextArgs a) {
-  constexpr int KS = D / 32;            // MFMA k-steps over the head dim (S^T)
-  constexpr int DT = D / 16;            // MFMA tiles over the head dim (O^T)
+  constexpr int KS = D / 16;            // MFMA k-steps over the head dim (S^T)
+  constexpr int DB = D / 32;            // 32-dim blocks of O^T
   constexpr int KROW = D + 8;           // bf16 per LDS key row (+16 B: conflict-free A reads)
   constexpr int VROW = D + 16;          // bf16 per LDS value row (+32 B: conflict-free column reads)
   constexpr int CPR = D / 8;            // 16-byte chunks per key / value row
@@ -68,7 +76,7 @@ __global__ __launch_bounds__(256, MAS_CTX_MIN_WG) void context_attn(ContextArgs 
   __shared__ __align__(16) uint16_t v_lds[kTileP * VROW];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id_uniform();
-  const int n = lane & 15, r = lane >> 4;
+  const int n = lane & 31, hf = lane >> 5;  // this lane's query row (token) and lane half
   const int hgroups = (a.group + a.heads_per_wg - 1) / a.heads_per_wg;
   const int kvh = blockIdx.x / hgroups, hg = blockIdx.x - kvh * hgroups;
   const int row = blockIdx.z;
@@ -85,8 +93,9 @@ __global__ __launch_bounds__(256, MAS_CTX_MIN_WG) void context_attn(ContextArgs 
   // negative positions: they see no key and get zeros.
   const int64_t cap = a.max_blocks << a.log2_page;
   const int64_t raw_len = a.seq_lens[row];
-  if ((raw_len < q_len || raw_len > cap) && tid == 0 && blockIdx.x == 0 && blockIdx.y == 0)
-    report(a.err, MAS_ERRBIT_POSITION);
+  // Error bits are reported at the end: a global atomic before the tile loop would keep the
+  // compiler from reading the block table through the scalar cache.
+  const bool len_bad = raw_len < q_len || raw_len > cap;
   const int kv_len = static_cast<int>(raw_len < 0 ? 0 : (raw_len > cap ? cap : raw_len));
   const int shift = kv_len - q_len;  // position of query token i = shift + i
 
@@ -98,18 +107,17 @@ __global__ __launch_bounds__(256, MAS_CTX_MIN_WG) void context_attn(ContextArgs 
   const int tok = tile_tok + kRowsPerWave * (wave / a.heads_per_wg);  // first of 32 tokens
   const bool wave_live = head_ok && tok < q_len;
 
-  // B operands: query rows tok + 16 nt + n, head-dim 32 ks + 8 r + 0..7 (zero past q_len).
-  bf16x8 qb[2][KS];
-#pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    const int t = tok + 16 * nt + n;
+  // B operands of S^T = K Q^T: token tok + n, head-dim 16 ks + 8 hf + 0..7 (zero past q_len).
+  bf16x8 qb[KS];
+  {
+    const int t = tok + n;
     const bool ok = wave_live && t < q_len;
-    const uint16_t* src = a.q + static_cast<int64_t>(q0 + (ok ? t : 0)) * a.q_stride + h * a.q_head_stride + 8 * r;
+    const uint16_t* src = a.q + static_cast<int64_t>(q0 + (ok ? t : 0)) * a.q_stride + h * a.q_head_stride + 8 * hf;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      u32x4 v = load_cached(src + 32 * ks);
+      u32x4 v = load_cached(src + 16 * ks);
       if (!ok) v = u32x4{0u, 0u, 0u, 0u};
-      qb[nt][ks] = __builtin_bit_cast(bf16x8, v);
+      qb[ks] = __builtin_bit_cast(bf16x8, v);
     }
   }
 
@@ -118,15 +126,10 @@ __global__ __launch_bounds__(256, MAS_CTX_MIN_WG) void context_attn(ContextArgs 
   const int reach = shift + last_tok + 1;  // <= kv_len
   const int ntiles = reach > 0 ? (reach + kTileP - 1) / kTileP : 0;
 
-  float m_run[2], l_run[2];  // per query row (lane n of row tile nt)
-  f32x4 acc[2][DT];          // O^T: lane (n, r) holds O[row 16 nt + n][16 dt + 4 r + i]
+  float m_run = kNegInf, l_run = 0.f;  // token n's running max (raw score units) and sum
+  f32x16 acc[DB];                      // O^T: element j of block db holds O[token n][32 db + 8 (j/4) + 4 hf + j%4]
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    m_run[nt] = kNegInf;
-    l_run[nt] = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) acc[nt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
+  for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
 
   const int32_t* bt = a.block_tables + row * a.bt_stride;
   const int pmask = (1 << a.log2_page) - 1;
@@ -138,182 +141,187 @@ __global__ __launch_bounds__(256, MAS_CTX_MIN_WG) void context_attn(ContextArgs 
   constexpr int kPosStep = 256 / CPR;
   const int dcol = tid % CPR, prow = tid / CPR;
   const int64_t lane_off = static_cast<int64_t>(prow) * a.entry_stride + kvh * a.head_stride + 8 * dcol;
-  const bool tile_pages = (1 << a.log2_page) >= kTileP;
-  u32x4 kst[LOADS], vst[LOADS];
-  bool lok[LOADS];
-  bool tile_full = false;  // every chunk of the staged tile valid: stores need no zeroing
-  auto issue_tile = [&](int base) {
-    if (tile_pages) {
+  struct TileRegs {
+    u32x4 k[LOADS], v[LOADS];
+    bool lok[LOADS];
+    bool full;  // every chunk of the tile valid: stores need no zeroing
+  };
+  bool page_bad = false;  // a real position's page id outside the cache (reported once, at the end)
+  auto issue_tile = [&](TileRegs& tr, int base) {
+    if constexpr (kTilePages) {
       const int32_t page = bt[base >> a.log2_page];
       const bool ok = page >= 0 && page < a.num_pages;
-      if (!ok && tid == 0) report(a.err, MAS_ERRBIT_PAGE);
+      page_bad |= !ok;
       const int64_t tile_off = (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
                                static_cast<int64_t>(base & pmask) * a.entry_stride;
-      tile_full = ok && base + kTileP <= kv_len;
+      tr.full = ok && base + kTileP <= kv_len;
 #pragma unroll
       for (int u = 0; u < LOADS; ++u) {
         const int64_t off = tile_off + lane_off + static_cast<int64_t>(kPosStep * u) * a.entry_stride;
-        kst[u] = load_cached(a.k_cache + off);
-        vst[u] = load_cached(a.v_cache + off);
-        lok[u] = ok && base + prow + kPosStep * u < kv_len;
+        tr.k[u] = load_cached(a.k_cache + off);
+        tr.v[u] = load_cached(a.v_cache + off);
+        tr.lok[u] = ok && base + prow + kPosStep * u < kv_len;
       }
     } else {
-      tile_full = false;
+      tr.full = false;
 #pragma unroll
       for (int u = 0; u < LOADS; ++u) {
         const int p = base + prow + kPosStep * u;
         const int pc = p < kv_len ? p : kv_len - 1;
         const int32_t page = bt[pc >> a.log2_page];
         const bool ok = page >= 0 && page < a.num_pages;
-        if (!ok && p < kv_len && dcol == 0) report(a.err, MAS_ERRBIT_PAGE);
+        page_bad |= !ok && p < kv_len;
         const int64_t off = (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
                             static_cast<int64_t>(pc & pmask) * a.entry_stride + kvh * a.head_stride + 8 * dcol;
-        kst[u] = load_cached(a.k_cache + off);
-        vst[u] = load_cached(a.v_cache + off);
-        lok[u] = ok && p < kv_len;
+        tr.k[u] = load_cached(a.k_cache + off);
+        tr.v[u] = load_cached(a.v_cache + off);
+        tr.lok[u] = ok && p < kv_len;
       }
     }
   };
-  if (ntiles > 0) issue_tile(0);
-
-  for (int it = 0; it < ntiles; ++it) {
-    const int base = it * kTileP;
-    __syncthreads();  // the previous tile's LDS reads are done
-    if (tile_full) {
+  // The tile in `tr` into LDS, between the barriers that order it after the previous tile's reads
+  // and before this tile's.
+  auto stage = [&](const TileRegs& tr) {
+    __syncthreads();
+    if (tr.full) {
 #pragma unroll
       for (int u = 0; u < LOADS; ++u) {
         const int p = prow + kPosStep * u;
-        *reinterpret_cast<u32x4*>(k_lds + p * KROW + 8 * dcol) = kst[u];
-        *reinterpret_cast<u32x4*>(v_lds + p * VROW + 8 * dcol) = vst[u];
+        *reinterpret_cast<u32x4*>(k_lds + p * KROW + 8 * dcol) = tr.k[u];
+        *reinterpret_cast<u32x4*>(v_lds + p * VROW + 8 * dcol) = tr.v[u];
       }
     } else {
 #pragma unroll
       for (int u = 0; u < LOADS; ++u) {
         const int p = prow + kPosStep * u;
-        const u32x4 kv = lok[u] ? kst[u] : u32x4{0u, 0u, 0u, 0u};
-        const u32x4 vv = lok[u] ? vst[u] : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 kv = tr.lok[u] ? tr.k[u] : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 vv = tr.lok[u] ? tr.v[u] : u32x4{0u, 0u, 0u, 0u};
         *reinterpret_cast<u32x4*>(k_lds + p * KROW + 8 * dcol) = kv;
         *reinterpret_cast<u32x4*>(v_lds + p * VROW + 8 * dcol) = vv;
       }
     }
     __syncthreads();
-    if (it + 1 < ntiles) issue_tile(base + kTileP);  // in flight during this tile's arithmetic
+  };
+
+  // Transposing-read coordinates of this lane's 16-lane group: head-dim column offset and row half.
+  const int grp_col = 16 * ((lane >> 4) & 1), k16 = lane & 15;
+  const float c = a.scale_log2;
+  auto compute_tile = [&](int base) {
     if (wave_live) {
-
-    // ---- S^T = K Q^T: lane (n, r) holds S[row 16 nt + n][position base + 16 pt + 4 r + i]
-    f32x4 s[4][2];
+      // ---- S^T = K Q^T: element j of s[pb] holds S[token n][position base + 32 pb + 8 (j/4) + 4 hf + j%4]
+      f32x16 s[2];
 #pragma unroll
-    for (int pt = 0; pt < 4; ++pt) {
+      for (int pb = 0; pb < 2; ++pb) {
+        s[pb] = f32x16{};
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) s[pt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 ka = *reinterpret_cast<const bf16x8*>(k_lds + (16 * pt + n) * KROW + 32 * ks + 8 * r);
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-          s[pt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[nt][ks], s[pt][nt], 0, 0, 0);
+        for (int ks = 0; ks < KS; ++ks) {
+          const bf16x8 ka = *reinterpret_cast<const bf16x8*>(k_lds + (32 * pb + n) * KROW + 16 * ks + 8 * hf);
+          s[pb] = mfma32(ka, qb[ks], s[pb]);
+        }
       }
-    }
 
-    // ---- causal mask (only tiles that cross the diagonal of the wavefront's first row, or the end
-    // of the sequence; a wavefront-uniform branch) and online softmax per query row. Scores stay
-    // in raw units; the scale enters the exponent through one fma: p = 2^(s c - m c).
-    if (base + kTileP - 1 > shift + tok || base + kTileP > kv_len) {
+      // ---- causal mask (only tiles that cross the diagonal of the wavefront's first row, or the
+      // end of the sequence; a wavefront-uniform branch) and online softmax per query row. Scores
+      // stay in raw units; the scale enters the exponent through one fma: p = 2^(s c - m c).
+      if (base + kTileP - 1 > shift + tok || base + kTileP > kv_len) {
+        const int qpos = shift + tok + n;  // this lane's query row position
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const int qpos = shift + tok + 16 * nt + n;  // this lane's query row position
+        for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
-        for (int pt = 0; pt < 4; ++pt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int kp = base + 16 * pt + 4 * r + i;
-            if (kp > qpos || kp >= kv_len) s[pt][nt][i] = kNegInf;
+          for (int j = 0; j < 16; ++j) {
+            const int kp = base + 32 * pb + 8 * (j >> 2) + 4 * hf + (j & 3);
+            if (kp > qpos || kp >= kv_len) s[pb][j] = kNegInf;
           }
       }
-    }
-    const float c = a.scale_log2;
-    bf16x8 pb[2][2];  // B operands of P.V: [row tile][k-step of 32 positions]
-    float alpha[2];
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
       float mx = kNegInf;
 #pragma unroll
-      for (int pt = 0; pt < 4; ++pt)
+      for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[pt][nt][i]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
+        for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[pb][j]);
       mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run[nt], mx);
+      const float m_new = fmaxf(m_run, mx);
       const float m_use = m_new == kNegInf ? 0.f : m_new;
       const float mc = m_use * c;
-      alpha[nt] = __builtin_amdgcn_exp2f(__builtin_fmaf(m_run[nt], c, -mc));
+      const float alpha = __builtin_amdgcn_exp2f(__builtin_fmaf(m_run, c, -mc));
       float sum = 0.f;
 #pragma unroll
-      for (int pt = 0; pt < 4; ++pt)
+      for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          s[pt][nt][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[pt][nt][i], c, -mc));
-          sum += s[pt][nt][i];
+        for (int j = 0; j < 16; ++j) {
+          s[pb][j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[pb][j], c, -mc));
+          sum += s[pb][j];
         }
-      sum += __shfl_xor(sum, 16);
       sum += __shfl_xor(sum, 32);
-      l_run[nt] = l_run[nt] * alpha[nt] + sum;
-      m_run[nt] = m_new;
-      // k-step ks2 takes position tiles 2 ks2 (elements 0..3) and 2 ks2 + 1 (elements 4..7)
+      l_run = l_run * alpha + sum;
+      m_run = m_new;
+      // O rescale, skipped when no row's max moved
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
 #pragma unroll
-      for (int ks2 = 0; ks2 < 2; ++ks2) {
-        const f32x4 lo = s[2 * ks2][nt], hi = s[2 * ks2 + 1][nt];
-        const u32x4 packed = {pack_bf16x2(lo[0], lo[1]), pack_bf16x2(lo[2], lo[3]), pack_bf16x2(hi[0], hi[1]),
-                              pack_bf16x2(hi[2], hi[3])};
-        pb[nt][ks2] = __builtin_bit_cast(bf16x8, packed);
+        for (int db = 0; db < DB; ++db) acc[db] *= alpha;
       }
-    }
-    // O rescale, skipped when no row's max moved (common once the running max has settled)
-    if (__builtin_amdgcn_ballot_w64(alpha[0] != 1.f || alpha[1] != 1.f) != 0) {
+      // B operands of O^T += V^T P^T, k-step kk = positions 16 kk .. 16 kk + 15: lane half hf holds
+      // 16 kk + 4 hf + e (e < 4) and 16 kk + 8 + 4 hf + e - 4 (e >= 4), i.e. elements 8 (kk % 2) ..
+      // + 7 of s[kk / 2]
+      bf16x8 pbo[4];
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[nt][dt] *= alpha[nt];
-    }
+      for (int kk = 0; kk < 4; ++kk) {
+        const int o = 8 * (kk & 1);
+        const f32x16& sv = s[kk >> 1];
+        const u32x4 packed = {pack_bf16x2(sv[o], sv[o + 1]), pack_bf16x2(sv[o + 2], sv[o + 3]),
+                              pack_bf16x2(sv[o + 4], sv[o + 5]), pack_bf16x2(sv[o + 6], sv[o + 7])};
+        pbo[kk] = __builtin_bit_cast(bf16x8, packed);
+      }
 
-    // ---- O^T += V^T P^T: A = V^T[16 dims][32 positions] (element j < 4: position 32 ks2 + 4 r + j,
-    // j >= 4: position 32 ks2 + 16 + 4 r + j - 4, as packed into pb), B = P^T
+      // ---- O^T += V^T P^T: A = V^T[32 dims][16 positions], read transposed from the row-major
+      // value tile in the position order of pbo
 #pragma unroll
-    for (int ks2 = 0; ks2 < 2; ++ks2) {
+      for (int kk = 0; kk < 4; ++kk) {
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const i16x4 lo = read_column4(v_lds, VROW, 32 * ks2 + 4 * r, 16 * dt, n);
-        const i16x4 hi = read_column4(v_lds, VROW, 32 * ks2 + 16 + 4 * r, 16 * dt, n);
-        const bf16x8 va = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-          acc[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[nt][ks2], acc[nt][dt], 0, 0, 0);
+        for (int db = 0; db < DB; ++db) {
+          const i16x4 lo = read_column4(v_lds, VROW, 16 * kk + 4 * hf, 32 * db + grp_col, k16);
+          const i16x4 hi = read_column4(v_lds, VROW, 16 * kk + 8 + 4 * hf, 32 * db + grp_col, k16);
+          const bf16x8 va = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+          acc[db] = mfma32(va, pbo[kk], acc[db]);
+        }
       }
-    }
     }  // wave_live
+  };
+
+  // The next tile's loads are in flight during this tile's arithmetic. (A second register buffer,
+  // two tiles ahead, measured no faster and costs 32 VGPRs.)
+  TileRegs tr;
+  if (ntiles > 0) issue_tile(tr, 0);
+  for (int it = 0; it < ntiles; ++it) {
+    stage(tr);
+    if (it + 1 < ntiles) issue_tile(tr, (it + 1) * kTileP);
+    compute_tile(it * kTileP);
   }
+  if (__builtin_amdgcn_ballot_w64(page_bad) != 0 && lane == 0) report(a.err, MAS_ERRBIT_PAGE);
+  if (len_bad && tid == 0 && blockIdx.x == 0 && blockIdx.y == 0) report(a.err, MAS_ERRBIT_POSITION);
 
   if (!wave_live) return;
-  // ---- out[token][h][16 dt + 4 r + i] = O / l * bmm2_scale (bf16), or its fp8 quantize
+  const int t = tok + n;
+  if (t >= q_len) return;
+  // ---- out[token][h][32 db + 8 q + 4 hf + i] = O / l * bmm2_scale (bf16), or its fp8 quantize
   const float qs = a.out_fp8 ? (a.quant_scale_dev != nullptr ? *a.quant_scale_dev : a.quant_scale_host) : 1.f;
   const float rcp = 1.0f / qs;
+  const float sc = l_run > 0.f ? a.out_scale / l_run : 0.f;
+  const int64_t at = static_cast<int64_t>(q0 + t) * a.out_stride + h * a.out_head_stride + 4 * hf;
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    const int t = tok + 16 * nt + n;
-    if (t >= q_len) continue;
-    const float sc = l_run[nt] > 0.f ? a.out_scale / l_run[nt] : 0.f;
-    const int64_t at = static_cast<int64_t>(q0 + t) * a.out_stride + h * a.out_head_stride + 4 * r;
+  for (int db = 0; db < DB; ++db) {
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      const f32x4 o = acc[nt][dt];
-      const uint32_t y0 = pack_bf16x2(o[0] * sc, o[1] * sc), y1 = pack_bf16x2(o[2] * sc, o[3] * sc);
+    for (int q = 0; q < 4; ++q) {
+      const f32x16& o = acc[db];
+      const uint32_t y0 = pack_bf16x2(o[4 * q] * sc, o[4 * q + 1] * sc);
+      const uint32_t y1 = pack_bf16x2(o[4 * q + 2] * sc, o[4 * q + 3] * sc);
+      const int64_t e = at + 32 * db + 8 * q;
       if (a.out_fp8) {
         // the quantize the reference applies to the bf16 attention output (devstral2.py:93-95,110-111)
-        *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.out) + at + 16 * dt) =
+        *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.out) + e) =
             fp8x4_saturate_encode(div_by_scale(bf16_lo(y0), qs, rcp), div_by_scale(bf16_hi(y0), qs, rcp),
                                   div_by_scale(bf16_lo(y1), qs, rcp), div_by_scale(bf16_hi(y1), qs, rcp));
       } else {
-        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.out) + at + 16 * dt) = u32x2{y0, y1};
+        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.out) + e) = u32x2{y0, y1};
       }
     }
   }
@@ -390,10 +398,18 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   a.quant_scale_host = out_scale_host;
   a.err = err;
   const dim3 grid(static_cast<uint32_t>(gx), static_cast<uint32_t>(gy), static_cast<uint32_t>(num_rows));
+  // Pages of at least a tile: each tile lies in one page (one block-table read per tile).
+  const bool tile_pages = page_size >= kTileP;
   if (head_dim == 64) {
-    hipLaunchKernelGGL(context_attn<64>, grid, dim3(256), 0, stream, a);
+    if (tile_pages)
+      hipLaunchKernelGGL((context_attn<64, true>), grid, dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((context_attn<64, false>), grid, dim3(256), 0, stream, a);
   } else {
-    hipLaunchKernelGGL(context_attn<128>, grid, dim3(256), 0, stream, a);
+    if (tile_pages)
+      hipLaunchKernelGGL((context_attn<128, true>), grid, dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((context_attn<128, false>), grid, dim3(256), 0, stream, a);
   }
   return launch_status();
 }
