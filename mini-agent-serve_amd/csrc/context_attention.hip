@@ -55,6 +55,9 @@ struct ContextArgs {
 #ifndef MAS_CTX_MIN_WG
 #define MAS_CTX_MIN_WG 2
 #endif
+#ifndef MAS_CTX_PIPELINE
+#define MAS_CTX_PIPELINE 1
+#endif
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -72,8 +75,11 @@ __global__ __launch_bounds__(256, MAS_CTX_MIN_WG) void context_attn(ContextArgs 
   constexpr int VROW = D + 16;          // bf16 per LDS value row (+32 B: conflict-free column reads)
   constexpr int CPR = D / 8;            // 16-byte chunks per key / value row
   constexpr int LOADS = kTileP * CPR / 256;  // 16-byte chunks per thread per tile, each of K and V
-  __shared__ __align__(16) uint16_t k_lds[kTileP * KROW];
-  __shared__ __align__(16) uint16_t v_lds[kTileP * VROW];
+  // kBufs tile buffers: with the software pipeline, the next tile's keys are read while this
+  // tile's values are.
+  constexpr int kBufs = MAS_CTX_PIPELINE ? 2 : 1;
+  __shared__ __align__(16) uint16_t k_lds_all[kBufs][kTileP * KROW];
+  __shared__ __align__(16) uint16_t v_lds_all[kBufs][kTileP * VROW];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id_uniform();
   const int n = lane & 31, hf = lane >> 5;  // this lane's query row (token) and lane half
@@ -179,10 +185,10 @@ __global__ __launch_bounds__(256, MAS_CTX_MIN_WG) void context_attn(ContextArgs 
       }
     }
   };
-  // The tile in `tr` into LDS, between the barriers that order it after the previous tile's reads
-  // and before this tile's.
-  auto stage = [&](const TileRegs& tr) {
-    __syncthreads();
+  // The tile in `tr` into LDS buffer `buf` (rows past kv_len or on a bad page zeroed).
+  auto stage = [&](const TileRegs& tr, int buf) {
+    uint16_t* k_lds = k_lds_all[buf];
+    uint16_t* v_lds = v_lds_all[buf];
     if (tr.full) {
 #pragma unroll
       for (int u = 0; u < LOADS; ++u) {
@@ -200,102 +206,154 @@ __global__ __launch_bounds__(256, MAS_CTX_MIN_WG) void context_attn(ContextArgs 
         *reinterpret_cast<u32x4*>(v_lds + p * VROW + 8 * dcol) = vv;
       }
     }
-    __syncthreads();
   };
 
   // Transposing-read coordinates of this lane's 16-lane group: head-dim column offset and row half.
   const int grp_col = 16 * ((lane >> 4) & 1), k16 = lane & 15;
   const float c = a.scale_log2;
-  auto compute_tile = [&](int base) {
-    if (wave_live) {
-      // ---- S^T = K Q^T: element j of s[pb] holds S[token n][position base + 32 pb + 8 (j/4) + 4 hf + j%4]
-      f32x16 s[2];
+  // ---- S^T = K Q^T: element j of s[pb] holds S[token n][position base + 32 pb + 8 (j/4) + 4 hf + j%4]
+  auto scores = [&](int buf, f32x16 (&s)[2]) {
+    const uint16_t* k_lds = k_lds_all[buf];
 #pragma unroll
-      for (int pb = 0; pb < 2; ++pb) {
-        s[pb] = f32x16{};
+    for (int pb = 0; pb < 2; ++pb) {
+      s[pb] = f32x16{};
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const bf16x8 ka = *reinterpret_cast<const bf16x8*>(k_lds + (32 * pb + n) * KROW + 16 * ks + 8 * hf);
-          s[pb] = mfma32(ka, qb[ks], s[pb]);
-        }
+      for (int ks = 0; ks < KS; ++ks) {
+        const bf16x8 ka = *reinterpret_cast<const bf16x8*>(k_lds + (32 * pb + n) * KROW + 16 * ks + 8 * hf);
+        s[pb] = mfma32(ka, qb[ks], s[pb]);
       }
-
-      // ---- causal mask (only tiles that cross the diagonal of the wavefront's first row, or the
-      // end of the sequence; a wavefront-uniform branch) and online softmax per query row. Scores
-      // stay in raw units; the scale enters the exponent through one fma: p = 2^(s c - m c).
-      if (base + kTileP - 1 > shift + tok || base + kTileP > kv_len) {
-        const int qpos = shift + tok + n;  // this lane's query row position
-#pragma unroll
-        for (int pb = 0; pb < 2; ++pb)
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const int kp = base + 32 * pb + 8 * (j >> 2) + 4 * hf + (j & 3);
-            if (kp > qpos || kp >= kv_len) s[pb][j] = kNegInf;
-          }
-      }
-      float mx = kNegInf;
-#pragma unroll
-      for (int pb = 0; pb < 2; ++pb)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[pb][j]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = m_new == kNegInf ? 0.f : m_new;
-      const float mc = m_use * c;
-      const float alpha = __builtin_amdgcn_exp2f(__builtin_fmaf(m_run, c, -mc));
-      float sum = 0.f;
+    }
+  };
+  // ---- causal mask, only on tiles that cross the diagonal of the wavefront's first row or the end
+  // of the sequence (a wavefront-uniform branch)
+  auto mask = [&](f32x16 (&s)[2], int base) {
+    if (base + kTileP - 1 > shift + tok || base + kTileP > kv_len) {
+      const int qpos = shift + tok + n;  // this lane's query row position
 #pragma unroll
       for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-          s[pb][j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[pb][j], c, -mc));
-          sum += s[pb][j];
+          const int kp = base + 32 * pb + 8 * (j >> 2) + 4 * hf + (j & 3);
+          if (kp > qpos || kp >= kv_len) s[pb][j] = kNegInf;
         }
-      sum += __shfl_xor(sum, 32);
-      l_run = l_run * alpha + sum;
-      m_run = m_new;
-      // O rescale, skipped when no row's max moved
-      if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
+    }
+  };
+  // ---- online softmax per query row; scores stay in raw units, the scale enters the exponent
+  // through one fma: p = 2^(s c - m c). P^T is packed to bf16 as the B operands of O^T += V^T P^T:
+  // k-step kk = positions 16 kk .. 16 kk + 15, lane half hf holding 16 kk + 4 hf + e (e < 4) and
+  // 16 kk + 8 + 4 hf + e - 4 (e >= 4), i.e. elements 8 (kk % 2) .. + 7 of s[kk / 2]. Returns the
+  // factor O must be rescaled by.
+  auto softmax = [&](f32x16 (&s)[2], bf16x8 (&pbo)[4]) {
+    float mx = kNegInf;
 #pragma unroll
-        for (int db = 0; db < DB; ++db) acc[db] *= alpha;
+    for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[pb][j]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == kNegInf ? 0.f : m_new;
+    const float mc = m_use * c;
+    const float alpha = __builtin_amdgcn_exp2f(__builtin_fmaf(m_run, c, -mc));
+    float sum = 0.f;
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        s[pb][j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[pb][j], c, -mc));
+        sum += s[pb][j];
       }
-      // B operands of O^T += V^T P^T, k-step kk = positions 16 kk .. 16 kk + 15: lane half hf holds
-      // 16 kk + 4 hf + e (e < 4) and 16 kk + 8 + 4 hf + e - 4 (e >= 4), i.e. elements 8 (kk % 2) ..
-      // + 7 of s[kk / 2]
-      bf16x8 pbo[4];
+    sum += __shfl_xor(sum, 32);
+    l_run = l_run * alpha + sum;
+    m_run = m_new;
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const int o = 8 * (kk & 1);
-        const f32x16& sv = s[kk >> 1];
-        const u32x4 packed = {pack_bf16x2(sv[o], sv[o + 1]), pack_bf16x2(sv[o + 2], sv[o + 3]),
-                              pack_bf16x2(sv[o + 4], sv[o + 5]), pack_bf16x2(sv[o + 6], sv[o + 7])};
-        pbo[kk] = __builtin_bit_cast(bf16x8, packed);
+    for (int kk = 0; kk < 4; ++kk) {
+      const int o = 8 * (kk & 1);
+      const f32x16& sv = s[kk >> 1];
+      const u32x4 packed = {pack_bf16x2(sv[o], sv[o + 1]), pack_bf16x2(sv[o + 2], sv[o + 3]),
+                            pack_bf16x2(sv[o + 4], sv[o + 5]), pack_bf16x2(sv[o + 6], sv[o + 7])};
+      pbo[kk] = __builtin_bit_cast(bf16x8, packed);
+    }
+    return alpha;
+  };
+  // O rescale, skipped when no row's max moved
+  auto rescale = [&](float alpha) {
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db) acc[db] *= alpha;
+    }
+  };
+  // ---- O^T += V^T P^T: A = V^T[32 dims][16 positions], read transposed from the row-major value
+  // tile in the position order of pbo
+  auto pv = [&](int buf, const bf16x8 (&pbo)[4]) {
+    const uint16_t* v_lds = v_lds_all[buf];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const i16x4 lo = read_column4(v_lds, VROW, 16 * kk + 4 * hf, 32 * db + grp_col, k16);
+        const i16x4 hi = read_column4(v_lds, VROW, 16 * kk + 8 + 4 * hf, 32 * db + grp_col, k16);
+        const bf16x8 va = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        acc[db] = mfma32(va, pbo[kk], acc[db]);
       }
-
-      // ---- O^T += V^T P^T: A = V^T[32 dims][16 positions], read transposed from the row-major
-      // value tile in the position order of pbo
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          const i16x4 lo = read_column4(v_lds, VROW, 16 * kk + 4 * hf, 32 * db + grp_col, k16);
-          const i16x4 hi = read_column4(v_lds, VROW, 16 * kk + 8 + 4 * hf, 32 * db + grp_col, k16);
-          const bf16x8 va = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-          acc[db] = mfma32(va, pbo[kk], acc[db]);
-        }
-      }
-    }  // wave_live
+    }
   };
 
+  TileRegs tr;
+#if MAS_CTX_PIPELINE
+  // Software pipeline over tiles: tile it + 1's scores (MFMA, keys from the other LDS buffer) are
+  // computed in the same block as tile it's softmax (VALU), so the two overlap; then tile it's P.V.
+  // Buffer it & 1 holds tile it, buffer (it + 1) & 1 tile it + 1 (staged after the barrier that
+  // ends every read of tile it - 1, which used that buffer).
+  f32x16 s_a[2], s_b[2];
+  if (ntiles > 0) {
+    issue_tile(tr, 0);
+    stage(tr, 0);
+    __syncthreads();
+    if (ntiles > 1) issue_tile(tr, kTileP);
+    if (wave_live) scores(0, s_a);
+  }
+  // One tile; `cur` holds its scores, `nxt` receives the next tile's. Called with the two score
+  // arrays in turn (no copy between them).
+  auto step = [&](int it, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
+    const int buf = it & 1;
+    __syncthreads();  // tile it - 1's reads (of buffer buf ^ 1) are done
+    if (it + 1 < ntiles) stage(tr, buf ^ 1);
+    __syncthreads();
+    if (it + 2 < ntiles) issue_tile(tr, (it + 2) * kTileP);
+    if (wave_live) {
+      mask(cur, it * kTileP);
+      bf16x8 pbo[4];
+      scores(buf ^ 1, nxt);  // the next tile's (stale buffer contents after the last tile: unused)
+      const float alpha = softmax(cur, pbo);
+      rescale(alpha);
+      pv(buf, pbo);
+    }
+  };
+  int it = 0;
+  for (; it + 1 < ntiles; it += 2) {
+    step(it, s_a, s_b);
+    step(it + 1, s_b, s_a);
+  }
+  if (it < ntiles) step(it, s_a, s_b);
+#else
   // The next tile's loads are in flight during this tile's arithmetic. (A second register buffer,
   // two tiles ahead, measured no faster and costs 32 VGPRs.)
-  TileRegs tr;
   if (ntiles > 0) issue_tile(tr, 0);
   for (int it = 0; it < ntiles; ++it) {
-    stage(tr);
+    __syncthreads();  // the previous tile's LDS reads are done
+    stage(tr, 0);
+    __syncthreads();
     if (it + 1 < ntiles) issue_tile(tr, (it + 1) * kTileP);
-    compute_tile(it * kTileP);
+    if (wave_live) {
+      f32x16 s[2];
+      bf16x8 pbo[4];
+      scores(0, s);
+      mask(s, it * kTileP);
+      rescale(softmax(s, pbo));
+      pv(0, pbo);
+    }
   }
+#endif
   if (__builtin_amdgcn_ballot_w64(page_bad) != 0 && lane == 0) report(a.err, MAS_ERRBIT_PAGE);
   if (len_bad && tid == 0 && blockIdx.x == 0 && blockIdx.y == 0) report(a.err, MAS_ERRBIT_POSITION);
 
