@@ -20,7 +20,8 @@
 //   is read from the row-major value tile with gfx950's transposing LDS read (ds_read_b64_tr_b16:
 //   in each group of 16 lanes, lane 4a + b receives element b of the 4-element rows that lanes
 //   a, a + 4, a + 8, a + 12 point at), two per operand, in the position order the packing implies.
-// The next tile's key and value loads are issued before the current tile's arithmetic.
+// Tiles are software-pipelined over two LDS buffers: while tile i is in the softmax, tile i + 1's
+// score MFMAs run and tile i + 2's key and value loads are in flight.
 #include "device.h"
 
 namespace mas {
