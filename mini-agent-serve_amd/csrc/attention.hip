@@ -420,7 +420,23 @@ __global__ __launch_bounds__(64) void decode_attn_combine(DecodeArgs a) {
       }
       const int cnt = min(64, nsplit - s0);
       const float* po = a.part_o + (base + s0) * D + DPL * lane;
-      for (int j = 0; j < cnt; ++j) {
+      // eight splits' partials loaded before any is used, so their loads are in flight together
+      constexpr int kU = 8;
+      int j = 0;
+      for (; j + kU <= cnt; j += kU) {
+        float v[kU][DPL];
+#pragma unroll
+        for (int u = 0; u < kU; ++u)
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) v[u][e] = po[(j + u) * D + e];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+          const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wgt), j + u));
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) acc[e] = __builtin_fmaf(wj, v[u][e], acc[e]);
+        }
+      }
+      for (; j < cnt; ++j) {
         const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wgt), j));
 #pragma unroll
         for (int e = 0; e < DPL; ++e) acc[e] = __builtin_fmaf(wj, po[j * D + e], acc[e]);
