@@ -4,6 +4,11 @@
  * SiluAndMul, NeoX / GPT-J rotary embedding from a cos/sin table, the paged KV-cache append
  * (block-table and slot-mapping forms) and the token-embedding gather.
  *
+ * Also: SiluAndMul fused with the fp8 quantize of the down_proj input, RoPE + paged KV append
+ * (+ llama-4 query scale) in one kernel, the step's sample placeholders resolved with the
+ * embedding gather, and paged attention over the KV cache: split-KV decode and causal context
+ * (prefill), each optionally writing the o_proj input's fp8 quantize.
+ *
  * Conventions shared by every entry point:
  *   - Pointers are device pointers; tensors are bf16 unless stated (bf16 travels as raw 16-bit
  *     words, fp8 as raw bytes). Strides are in ELEMENTS of the pointed-to type, and the last
@@ -17,8 +22,10 @@
  *     MAS_ERRBIT_* bit into *err. No kernel reads or writes outside the buffers described.
  *
  * Reference interfaces replaced (paths relative to the mini-agent-serve repository):
- *   miniagentserve/models/devstral2/devstral2.py:18-23  flashinfer imports
+ *   miniagentserve/models/devstral2/devstral2.py:18-23  flashinfer imports (norm, activation, rope,
+ *                                                       page, decode and prefill attention)
  *   miniagentserve/models/devstral2/devstral2.py:260,282 nn.Embedding
+ *   miniagentserve/engine/model_runner.py:149-154        ModelRunner.fill_placeholders
  */
 #ifndef MAS_KERNELS_H
 #define MAS_KERNELS_H
@@ -37,7 +44,9 @@ extern "C" {
 #define MAS_ERR_DEVICE (-4)        /* hipGetDevice / device-attribute query failed        */
 
 #define MAS_ERRBIT_TOKEN_ID 1u  /* embedding: id < 0 or id >= vocab                       */
-#define MAS_ERRBIT_POSITION 2u  /* rope: position < 0 or >= table rows; kv: position < 0  */
+#define MAS_ERRBIT_POSITION 2u  /* rope: position < 0 or >= table rows; kv: position < 0;
+                                   attention: seq_len out of range, or (context) a row with
+                                   more query tokens than max_q_len                         */
 #define MAS_ERRBIT_BATCH 4u     /* kv: batch index outside [0, batch)                     */
 #define MAS_ERRBIT_PAGE 8u      /* kv: page slot past kv_indices or page id out of range  */
 #define MAS_ERRBIT_SLOT 16u     /* kv slot form: slot >= num_pages * page_size            */
@@ -243,8 +252,9 @@ int mas_paged_decode_attention_bf16(void* out, int64_t out_stride, int64_t out_h
  * own tokens: token i sits at position kv_len - q_len + i and attends to positions 0..that.
  * For query head h (kv head h / (num_q_heads / num_kv_heads)):
  *   out[t, h] = bmm2_scale * sum_p softmax_p(bmm1_scale * q[t, h] . k_p) * v_p
- * with fp32 accumulation and P rounded to bf16 for the P.V product. max_q_len bounds q_len (it
- * sizes the grid). head_dim 64 or 128; page_size a power of two. A seq_len outside
+ * with fp32 accumulation and P rounded to bf16 for the P.V product. max_q_len must bound q_len (it
+ * sizes the grid; a longer row's tokens past it are left unwritten, MAS_ERRBIT_POSITION).
+ * head_dim 64 or 128; page_size a power of two. A seq_len outside
  * [q_len, max_blocks * page_size] is clamped (MAS_ERRBIT_POSITION; tokens left before position 0
  * get zeros); a page id outside [0, num_pages) skips its position (MAS_ERRBIT_PAGE).
  * out_fp8 / out_scale_dev / out_scale_host: the fp8 output as for mas_paged_decode_attention_bf16.

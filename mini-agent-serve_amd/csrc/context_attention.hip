@@ -102,7 +102,9 @@ __global__ __launch_bounds__(256, MAS_CTX_MIN_WG) void context_attn(ContextArgs 
   const int64_t raw_len = a.seq_lens[row];
   // Error bits are reported at the end: a global atomic before the tile loop would keep the
   // compiler from reading the block table through the scalar cache.
-  const bool len_bad = raw_len < q_len || raw_len > cap;
+  // also flagged: a row with more query tokens than the grid covers (max_q_len too small); the
+  // tokens past the grid are left unwritten
+  const bool len_bad = raw_len < q_len || raw_len > cap || q_len > static_cast<int>(gridDim.y) * tokens_per_wg;
   const int kv_len = static_cast<int>(raw_len < 0 ? 0 : (raw_len > cap ? cap : raw_len));
   const int shift = kv_len - q_len;  // position of query token i = shift + i
 

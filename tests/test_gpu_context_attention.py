@@ -95,6 +95,24 @@ def test_context_attention_error_paths(mas, dev):
     assert int(flags.item()) == 8
 
 
+def test_context_attention_max_q_len_too_small_is_flagged(mas, dev):
+    """max_q_len sizes the grid: a row with more query tokens than it covers gets its covered tokens
+    right, leaves the rest unwritten and sets error bit 2."""
+    q_lens, kv_lens, hq, hk, dim, ps = [40, 10], [40, 10], 8, 2, 128, 16
+    q, kc, vc, tables, seq, cu = _case(13, q_lens, kv_lens, hq, hk, dim, ps)
+    out = torch.full(q.shape, 7.0, dtype=torch.bfloat16, device=dev)
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    ws = torch.zeros(16, dtype=torch.uint8, device=dev)
+    mas.attention.trtllm_batch_context_with_kv_cache(
+        q.to(dev), (kc.to(dev), vc.to(dev)), ws, tables.to(dev), seq.to(dev), 20, 0, 0.1, 1.0, 2, cu.to(dev), None,
+        out=out, kv_layout="NHD", error_flags=flags)
+    assert int(flags.item()) == 2
+    want = ops.paged_context_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), cu.numpy(), 0.1)
+    covered = [t for t in range(50) if not 32 <= t < 40]       # 32 tokens per grid tile (4 heads per kv head)
+    _check(bits(out)[covered], want[covered])
+    assert torch.all(out[32:40] == 7.0)
+
+
 def test_context_attention_in_graph_replays(mas, dev):
     q_lens, kv_lens, hq, hk, dim, ps = [128, 64], [256, 64], 32, 8, 128, 64
     q, kc, vc, tables, seq, cu = _case(12, q_lens, kv_lens, hq, hk, dim, ps)
