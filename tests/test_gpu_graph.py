@@ -106,3 +106,35 @@ def test_layer_pass_fused_and_separate_agree(mas, dev, fp8):
         y = mas.silu_and_mul(li.gate_up)
         ref = (y.float() / 0.05).clamp(-448, 448).to(torch.float8_e4m3fn)
         assert torch.equal(outs[0][6], ref.view(torch.uint8))
+
+
+def test_torch_compile_attention_matches_eager(mas, dev):
+    """Both attention ops, bf16 and fp8 outputs (device-tensor scale), through torch.compile's custom
+    ops: the same bytes as eager."""
+    g = torch.Generator(device=dev).manual_seed(8)
+    pages, ps, hq, hk, d = 12, 64, 8, 2, 128
+    kc = torch.randn(pages, ps, hk, d, generator=g, device=dev).bfloat16()
+    vc = torch.randn(pages, ps, hk, d, generator=g, device=dev).bfloat16()
+    tables = torch.randperm(pages, device=dev)[:8].reshape(2, 4).to(torch.int32)
+    seq = torch.tensor([200, 90], dtype=torch.int32, device=dev)
+    qd = torch.randn(2, hq, d, generator=g, device=dev).bfloat16()
+    cu = torch.tensor([0, 40, 70], dtype=torch.int32, device=dev)
+    qc = torch.randn(70, hq, d, generator=g, device=dev).bfloat16()
+    ws = torch.zeros(1 << 20, dtype=torch.uint8, device=dev)
+    scale = torch.tensor(0.02, device=dev)
+    att = mas.attention
+
+    def f(qd, qc):
+        o1 = att.trtllm_batch_decode_with_kv_cache(qd, (kc, vc), ws, tables, seq, 256, 0.09, 1.0)
+        o2 = att.trtllm_batch_decode_with_kv_cache(qd, (kc, vc), ws, tables, seq, 256, 0.09, 1.0,
+                                                   out_quant_scale=scale)
+        o3 = att.trtllm_batch_context_with_kv_cache(qc, (kc, vc), ws, tables, seq, 40, 200, 0.09, 1.0, 2, cu)
+        o4 = att.trtllm_batch_context_with_kv_cache(qc, (kc, vc), ws, tables, seq, 40, 200, 0.09, 1.0, 2, cu,
+                                                    out_quant_scale=0.02)
+        return o1 + 0, o2.view(torch.uint8) + 0, o3 + 0, o4.view(torch.uint8) + 0
+
+    want = f(qd, qc)
+    compiled = torch.compile(f, dynamic=True, fullgraph=True)
+    got = compiled(qd, qc)
+    for a, b in zip(got, want):
+        assert torch.equal(a, b)
