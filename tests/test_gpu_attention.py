@@ -47,6 +47,7 @@ CASES = [
     (2, 16, 2, 64, 32, [100, 1000]),               # head_dim 64, 8 per kv head
     (2, 16, 1, 256, 64, [513, 77]),                # head_dim 256, 16 per kv head
     (3, 6, 2, 128, 4, [9, 40, 2]),                 # 3 per kv head (padded), pages of 4
+    (2, 16, 4, 128, 512, [700, 1500]),             # pages of two chunks
 ]
 
 

@@ -49,6 +49,7 @@ CASES = [
     ([33, 90], [33, 95], 16, 8, 64, 32),           # 2 per kv head, head_dim 64
     ([17, 5], [50, 5], 6, 2, 64, 4),               # 3 per kv head, pages of 4
     ([200], [200], 8, 1, 128, 128),                # 8 per kv head, a longer row
+    ([130, 64], [600, 64], 16, 4, 128, 512),       # pages of eight tiles, chunked prefill
 ]
 
 
