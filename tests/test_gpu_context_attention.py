@@ -50,6 +50,7 @@ CASES = [
     ([17, 5], [50, 5], 6, 2, 64, 4),               # 3 per kv head, pages of 4
     ([200], [200], 8, 1, 128, 128),                # 8 per kv head, a longer row
     ([130, 64], [600, 64], 16, 4, 128, 512),       # pages of eight tiles, chunked prefill
+    ([20, 0, 7], [30, 10, 7], 8, 2, 128, 64),      # a row with no new tokens between two others
 ]
 
 
