@@ -232,6 +232,74 @@ def cpu_baseline_layer(shape, seconds: float, fp8: bool) -> dict:
                       f"{shape.tokens} tokens ({dt:.1f} s)"}
 
 
+def cpu_torch_layer(shape, seconds: float, fp8: bool) -> dict:
+    """The same sample as the oracle baseline, as torch CPU code on all of the host's torch threads:
+    the reference's math in torch (fp32 from bf16, rounded once), the kind of CPU path a user without
+    the GPU kernels would run. Reported beside the single-threaded oracle baseline."""
+    import torch.nn.functional as F
+
+    mas = __graft_entry__.load_package()
+    wl = mas.workloads
+    tokens = shape.tokens
+    if tokens * (shape.inter + shape.hidden) > 64 * (32768 + 5120):
+        tokens = 64
+    li = wl.make_layer_inputs(shape, "cpu", seed=1, with_cache=False)
+    hq, hk, d, eps = shape.q_heads, shape.kv_heads, shape.head_dim, shape.eps
+    x, r = li.hidden[:tokens].clone(), li.residual[:tokens].clone()
+    w, w2 = li.norm_weight.float(), li.post_norm_weight.float()
+    a, gu = li.attn_out[:tokens].clone(), li.gate_up[:tokens].clone()
+    qkv = li.qkv[:tokens].clone()
+    q = qkv[:, : hq * d].view(tokens, hq, d)
+    k = qkv[:, hq * d:(hq + hk) * d].view(tokens, hk, d)
+    v = qkv[:, (hq + hk) * d:].view(tokens, hk, d)
+    cs = li.table[li.positions[:tokens].long()]
+    half = d // 2
+    c, sn = cs[:, None, :half], cs[:, None, half:]
+    slots = li.slot_mapping[:tokens].numpy()
+    pages_used = np.unique(slots // shape.page_size)
+    remap = {p: j for j, p in enumerate(pages_used)}
+    local = torch.tensor([remap[s // shape.page_size] * shape.page_size + s % shape.page_size for s in slots])
+    kc = torch.zeros(len(pages_used) * shape.page_size, hk, d, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    inter = shape.inter
+
+    def norm(inp, res, weight):
+        s_ = inp.float() + res.float()
+        y = s_ * torch.rsqrt(s_.pow(2).mean(-1, keepdim=True) + eps) * weight
+        return (y / 0.05).clamp(-448, 448).to(torch.float8_e4m3fn) if fp8 else y.bfloat16(), s_.bfloat16()
+
+    def layer():
+        nonlocal r
+        _, r = norm(x, r, w)
+        if shape.norm_only:
+            return
+        for t in (q, k):
+            x1, x2 = t[..., :half].float(), t[..., half:].float()
+            t[..., :half] = (x1 * c - x2 * sn).bfloat16()
+            t[..., half:] = (x2 * c + x1 * sn).bfloat16()
+        kc[local] = k
+        vc[local] = v
+        _, r = norm(a, r, w2)
+        y = (F.silu(gu[:, :inter].float()) * gu[:, inter:].float()).bfloat16()
+        if fp8:
+            (y.float() / 0.05).clamp(-448, 448).to(torch.float8_e4m3fn)
+
+    sample_shape = type(shape)(**{**shape.__dict__, "tokens": tokens})
+    per_layer = wl.layer_credited_bytes(sample_shape, False, fp8)
+    layer()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        layer()
+        reps += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": round(per_layer * reps / dt / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "torch",
+            "sample": f"{reps} passes of the step's ops as torch CPU code on {tokens} of {shape.tokens} tokens "
+                      f"({dt:.1f} s, {torch.get_num_threads()} threads)"}
+
+
 def run_layer_workload(mas, args, shape, dev) -> dict:
     wl, lp = mas.workloads, mas.layer_pass
     n_sets = 1 if args.protocol == "hot" else max(2, math.ceil(COLD_BYTES / footprint_bytes(shape)))
@@ -569,6 +637,7 @@ def main() -> int:
     line["copy_ceiling_GBps"] = round(copy_ceiling_gbs(dev), 1)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_layer(shape, args.cpu_seconds, args.fp8)
+        line["cpu_torch"] = cpu_torch_layer(shape, args.cpu_seconds / 2, args.fp8)
     print(json.dumps(line), flush=True)
     return 0
 
