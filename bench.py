@@ -13,8 +13,9 @@ from a captured HIP graph, as the reference's model runner replays its decode gr
 Printed on one JSON line: the metric (credited HBM bytes per step / time per step), microseconds
 per layer, each kernel's average launch duration and bandwidth (HIP events around a graph of
 back-to-back launches of that kernel, on the stream it runs on), the roofline
-of the dominant kernel, and the CPU baseline (the numpy oracle timed on a bounded sample of the
-same workload on the host).
+of the dominant kernel, the CPU baseline (the numpy oracle timed on a bounded sample of the
+same workload on the host, one thread) and, for the layer workloads, the same sample as torch CPU
+code on all of torch's host threads (`cpu_torch`).
 
     python bench.py [--steps K] [--warmup W] [--workload NAME] [--protocol cold|hot] [--no-cpu]
 """
