@@ -12,16 +12,19 @@ from a captured HIP graph, as the reference's model runner replays its decode gr
 
 Printed on one JSON line: the metric (credited HBM bytes per step / time per step), microseconds
 per layer, each kernel's average launch duration and bandwidth (HIP events around a graph of
-back-to-back launches of that kernel, on the stream it runs on), the roofline
-of the dominant kernel, the CPU baseline (the numpy oracle timed on a bounded sample of the
-same workload on the host, one thread) and, for the layer workloads, the same sample as torch CPU
-code on all of torch's host threads (`cpu_torch`).
+back-to-back launches of that kernel, on the stream it runs on) beside the same for its memory
+skeleton (a kernel moving the same streams of the same buffers with no arithmetic: the practical
+ceiling at that size, launch ramp-up and drain included), the roofline of the dominant kernel, the
+CPU baseline (the numpy oracle timed on a bounded sample of the same workload on the host, one
+thread) and, for the layer workloads, the same sample as torch CPU code on all of torch's host
+threads (`cpu_torch`).
 
     python bench.py [--steps K] [--warmup W] [--workload NAME] [--protocol cold|hot] [--no-cpu]
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -86,8 +89,59 @@ def step_ops(shape, fp8: bool) -> tuple[str, ...]:
     return (norm, "rope", "append_paged_kv_cache", "silu_and_mul_quant" if fp8 else "silu_and_mul", "rope_append")
 
 
+SKELETON_OPS = ("fused_add_rmsnorm", "rope", "append_paged_kv_cache", "silu_and_mul")
+_skeleton_fn = None
+
+
+def load_skeletons(mas) -> bool:
+    """Loads the benchmark's memory skeletons (libmas_bench.so, built beside the kernel library)."""
+    global _skeleton_fn
+    path = Path(mas.__file__).resolve().parent / "libmas_bench.so"
+    if not path.exists():
+        return False
+    fn = ctypes.CDLL(str(path)).mas_bench_stream_skeleton
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64] * 4 + [ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p]
+    _skeleton_fn = fn
+    return True
+
+
+def skeleton_launcher(b, op):
+    """A closure launching the memory skeleton of ``op`` on the buffers of ``b``: the kernel's
+    streams (same rows, row strides and read / write mix) moved with no arithmetic. The KV store's
+    skeleton writes the cache's first rows instead of the mapped slots; index arrays and the norm
+    weight are not moved."""
+    li, s = b.inputs, b.inputs.shape
+    n = s.tokens
+    if op == "fused_add_rmsnorm":
+        h, r = li.hidden, li.residual
+        args = (h, h.stride(0), r, r.stride(0), h, h.stride(0), r, r.stride(0), n, s.hidden)
+    elif op == "silu_and_mul":
+        g = li.gate_up
+        up = g[:, s.inter:]
+        args = (g, g.stride(0), up, g.stride(0), b.silu_out, b.silu_out.stride(0), None, 0, n, s.inter)
+    elif op == "rope":
+        q = li.q
+        args = (q, q.stride(0), None, 0, q, q.stride(0), None, 0, n, (s.q_heads + s.kv_heads) * s.head_dim)
+    elif op == "append_paged_kv_cache":
+        k, v, row = li.k, li.v, s.kv_heads * s.head_dim
+        args = (k, k.stride(0), v, v.stride(0), li.k_cache, row, li.v_cache, row, n, row)
+    else:
+        raise ValueError(op)
+    ptrs = [a.data_ptr() if isinstance(a, torch.Tensor) else a for a in args]
+
+    def launch():
+        st = _skeleton_fn(*ptrs, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        if st != 0:
+            raise RuntimeError(f"memory skeleton of {op} failed with status {st}")
+    return launch
+
+
 def op_launcher(mas, b, op):
-    """A closure launching one kernel of the layer on the buffers of ``b``."""
+    """A closure launching one kernel of the layer on the buffers of ``b`` (``skeleton:<op>``: its
+    memory skeleton)."""
+    if op.startswith("skeleton:"):
+        return skeleton_launcher(b, op.split(":", 1)[1])
     li, s = b.inputs, b.inputs.shape
     if op == "fused_add_rmsnorm":
         return lambda: mas.norm.fused_add_rmsnorm(li.hidden, li.residual, li.norm_weight, s.eps)
@@ -359,10 +413,18 @@ def run_layer_workload(mas, args, shape, dev) -> dict:
     stream_us = (time.perf_counter() - s0) / stream_steps * 1e6
 
     launches = max(2 * n_sets, 100) if shape.decode else 4 * n_sets
-    op_us = time_ops(mas, sets, launches, step_ops(shape, args.fp8))
+    kernels = step_ops(shape, args.fp8)
+    skeletons = tuple(f"skeleton:{op}" for op in kernels if op in SKELETON_OPS and shape.tokens <= 65535) \
+        if _skeleton_fn is not None else ()
+    op_us = time_ops(mas, sets, launches, kernels + skeletons)
     cb = wl.credited_bytes(shape)
-    ops = {op: {"us": round(us, 3), "GB/s": round(cb[op] / us / 1e3, 1),
-                "frac": round(cb[op] / us / 1e3 / PEAK_HBM_GBS, 4)} for op, us in op_us.items()}
+    ops = {op: {"us": round(op_us[op], 3), "GB/s": round(cb[op] / op_us[op] / 1e3, 1),
+                "frac": round(cb[op] / op_us[op] / 1e3 / PEAK_HBM_GBS, 4)} for op in kernels}
+    for op in kernels:
+        if f"skeleton:{op}" in op_us:
+            sk = op_us[f"skeleton:{op}"]
+            ops[op]["skeleton_us"] = round(sk, 3)
+            ops[op]["of_skeleton"] = round(sk / op_us[op], 3)
     ms_per_step = elapsed / steps * 1e3
     dominant = step_ops(shape, args.fp8)[0 if shape.norm_only else 3]
     res = {"steps": steps, "warmup": warmup, "ms_per_step": ms_per_step, "per_step_bytes": per_step,
@@ -588,6 +650,7 @@ def main() -> int:
         return 1
     mas = __graft_entry__.load_package()
     mas.load_library()
+    load_skeletons(mas)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.workload in mas.workloads.CONTEXT_SHAPES:
@@ -632,6 +695,13 @@ def main() -> int:
                      "bytes_per_launch": res["dominant_bytes"],
                      "avg_launch_us": round(res["dominant_us"], 3)},
     }
+    dom = res["ops"].get(res["dominant"], {})
+    if "skeleton_us" in dom:
+        # the same bytes, buffers and launch shape moved by a kernel with no arithmetic, same run
+        sk_gbs = res["dominant_bytes"] / dom["skeleton_us"] / 1e3
+        line["roofline"]["skeleton"] = {"us": dom["skeleton_us"], "GB/s": round(sk_gbs, 1),
+                                        "frac": round(sk_gbs / PEAK_HBM_GBS, 4)}
+        line["roofline"]["frac_of_skeleton"] = dom["of_skeleton"]
     for key in ("separate_us_per_layer", "fused_us_per_layer", "stream_us_per_step"):
         if key in res:
             line[key] = round(res[key], 3)

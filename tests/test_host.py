@@ -35,6 +35,20 @@ def test_library_loads_and_exports_every_declared_symbol(mas):
         assert getattr(lib, name) is not None
 
 
+def test_benchmark_skeletons_live_in_their_own_library(mas):
+    kernels = ctypes.CDLL(str(mas._build.LIBRARY_PATH))
+    assert not hasattr(kernels, "mas_bench_stream_skeleton")
+    if not mas._build.BENCH_LIBRARY_PATH.exists():
+        pytest.skip("libmas_bench.so not built")
+    fn = ctypes.CDLL(str(mas._build.BENCH_LIBRARY_PATH)).mas_bench_stream_skeleton
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64] * 4 + [ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p]
+    assert fn(None, 0, None, 0, None, 0, None, 0, 0, 8, None) == 0          # empty: nothing launched
+    assert fn(16, 8, None, 0, 32, 8, None, 0, 70000, 8, None) == -1        # rows past one grid row each
+    assert fn(16, 8, None, 0, 32, 8, 48, 8, 4, 8, None) == -1              # two destinations, one source
+    assert fn(16, 8, None, 0, 40, 8, None, 0, 4, 8, None) == -1            # misaligned destination
+
+
 def test_library_links_against_one_hip_runtime(mas):
     mas.load_library()
     maps = Path("/proc/self/maps").read_text()
