@@ -230,7 +230,7 @@ def cpu_baseline_layer(shape, seconds: float, fp8: bool) -> dict:
     wl = mas.workloads
     tokens = shape.tokens
     # A sample of whole tokens: the full batch when it fits the time budget, else a row slice.
-    if tokens * (shape.inter + shape.hidden) > 64 * (32768 + 5120):
+    if tokens * ((0 if shape.norm_only else shape.inter) + shape.hidden) > 64 * (32768 + 5120):
         tokens = 64
     li = wl.make_layer_inputs(shape, "cpu", seed=1, with_cache=False)
 
@@ -296,7 +296,7 @@ def cpu_torch_layer(shape, seconds: float, fp8: bool) -> dict:
     mas = __graft_entry__.load_package()
     wl = mas.workloads
     tokens = shape.tokens
-    if tokens * (shape.inter + shape.hidden) > 64 * (32768 + 5120):
+    if tokens * ((0 if shape.norm_only else shape.inter) + shape.hidden) > 64 * (32768 + 5120):
         tokens = 64
     li = wl.make_layer_inputs(shape, "cpu", seed=1, with_cache=False)
     hq, hk, d, eps = shape.q_heads, shape.kv_heads, shape.head_dim, shape.eps
@@ -323,25 +323,41 @@ def cpu_torch_layer(shape, seconds: float, fp8: bool) -> dict:
         y = s_ * torch.rsqrt(s_.pow(2).mean(-1, keepdim=True) + eps) * weight
         return (y / 0.05).clamp(-448, 448).to(torch.float8_e4m3fn) if fp8 else y.bfloat16(), s_.bfloat16()
 
+    op_s = {"fused_add_rmsnorm": 0.0, "rope": 0.0, "append_paged_kv_cache": 0.0, "silu_and_mul": 0.0}
+    clock = time.perf_counter
+
     def layer():
         nonlocal r
+        t = clock()
         _, r = norm(x, r, w)
+        op_s["fused_add_rmsnorm"] += clock() - t
         if shape.norm_only:
             return
-        for t in (q, k):
-            x1, x2 = t[..., :half].float(), t[..., half:].float()
-            t[..., :half] = (x1 * c - x2 * sn).bfloat16()
-            t[..., half:] = (x2 * c + x1 * sn).bfloat16()
+        t = clock()
+        for u in (q, k):
+            x1, x2 = u[..., :half].float(), u[..., half:].float()
+            u[..., :half] = (x1 * c - x2 * sn).bfloat16()
+            u[..., half:] = (x2 * c + x1 * sn).bfloat16()
+        t2 = clock()
         kc[local] = k
         vc[local] = v
+        t3 = clock()
         _, r = norm(a, r, w2)
+        t4 = clock()
         y = (F.silu(gu[:, :inter].float()) * gu[:, inter:].float()).bfloat16()
         if fp8:
             (y.float() / 0.05).clamp(-448, 448).to(torch.float8_e4m3fn)
+        t5 = clock()
+        op_s["rope"] += t2 - t
+        op_s["append_paged_kv_cache"] += t3 - t2
+        op_s["fused_add_rmsnorm"] += t4 - t3
+        op_s["silu_and_mul"] += t5 - t4
 
     sample_shape = type(shape)(**{**shape.__dict__, "tokens": tokens})
     per_layer = wl.layer_credited_bytes(sample_shape, False, fp8)
     layer()
+    for key in op_s:
+        op_s[key] = 0.0
     reps, t0 = 0, time.perf_counter()
     while True:
         layer()
@@ -349,10 +365,13 @@ def cpu_torch_layer(shape, seconds: float, fp8: bool) -> dict:
         if time.perf_counter() - t0 >= seconds:
             break
     dt = time.perf_counter() - t0
+    calls = {"fused_add_rmsnorm": 1 if shape.norm_only else 2}
     return {"value": round(per_layer * reps / dt / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
             "kind": "torch",
             "sample": f"{reps} passes of the step's ops as torch CPU code on {tokens} of {shape.tokens} tokens "
-                      f"({dt:.1f} s, {torch.get_num_threads()} threads)"}
+                      f"({dt:.1f} s, {torch.get_num_threads()} threads)",
+            # average µs per call of each op on the sample's tokens
+            "op_us": {key: round(1e6 * v / (reps * calls.get(key, 1)), 1) for key, v in op_s.items() if v > 0}}
 
 
 def run_layer_workload(mas, args, shape, dev) -> dict:
