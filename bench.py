@@ -660,7 +660,7 @@ def main() -> int:
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}, "
+        print(f"bench.py runs on one GPU: these kernels have no multi-GPU path (asked for --gpus {args.gpus}, "
               f"WORLD_SIZE {world}); the layer kernels are token-parallel and would shard without exchange",
               file=sys.stderr)
         return 2
