@@ -26,14 +26,15 @@ How each function is pinned (the tests under tests/test_oracle_*.py):
 - KV store / embedding: against brute-force loops and torch indexing; the block-table and slot
   forms agree.
 - Tables: against transformers' default and YaRN inverse frequencies and attention factor.
-- Activation quantize and SiluAndMul + quantize: bit for bit against the reference's own torch
-  expression (y / scale, clamp to +-448, cast to e4m3fn) on every finite bf16 value.
+- Activation quantize: bit for bit against the reference's own torch expression (y / scale, clamp
+  to +-448, cast to e4m3fn) on every finite bf16 value; SiluAndMul + quantize: against SiluAndMul
+  followed by that expression.
 - llama-4 query scale: bit for bit against transformers' get_llama_4_attn_scale after the bf16 cast.
 - Placeholder fill: the closed-form cases of the runner's rule (-1 - r -> last token of row r).
 - Decode and context attention: against torch's scaled_dot_product_attention in fp32 on the
   gathered rows (grouped heads; for context rows an explicit causal mask aligned to the end of
-  each row), plus closed forms (one position returns its value row, scale 0 the mean of the value
-  rows, an empty row zeros).
+  each row); decode also against closed forms (one position returns its value row, scale 0 the
+  mean of the value rows, an empty row zeros).
 flashinfer's own rounding choices (which the reference inherits) cannot be observed here: the
 library is absent and the reference has no tests or fixtures, so agreement with flashinfer
 bit for bit is "parity unpinned"; the oracle fixes one documented rounding order per op and the
