@@ -52,9 +52,17 @@ struct ContextArgs {
   uint32_t* err;
 };
 
-// Workgroups per CU the register allocation must allow (2: at most 256 VGPRs per lane).
+// Wavefronts per workgroup: each stages its share of every key / value tile, and all of them
+// read it.
+#ifndef MAS_CTX_WAVES
+#define MAS_CTX_WAVES 4
+#endif
+constexpr int kCtxWaves = MAS_CTX_WAVES;
+constexpr int kCtxThreads = 64 * kCtxWaves;
+// Workgroups per CU the register allocation must allow (two wavefronts per SIMD: at most 256
+// VGPRs per lane).
 #ifndef MAS_CTX_MIN_WG
-#define MAS_CTX_MIN_WG 2
+#define MAS_CTX_MIN_WG (8 / MAS_CTX_WAVES)
 #endif
 #ifndef MAS_CTX_PIPELINE
 #define MAS_CTX_PIPELINE 1
@@ -69,13 +77,13 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
 }
 
 template <int D, bool kTilePages>
-__global__ __launch_bounds__(256, MAS_CTX_MIN_WG) void context_attn(ContextArgs a) {
+__global__ __launch_bounds__(kCtxThreads, MAS_CTX_MIN_WG) void context_attn(ContextArgs a) {
   constexpr int KS = D / 16;            // MFMA k-steps over the head dim (S^T)
   constexpr int DB = D / 32;            // 32-dim blocks of O^T
   constexpr int KROW = D + 8;           // bf16 per LDS key row (+16 B: conflict-free A reads)
   constexpr int VROW = D + 16;          // bf16 per LDS value row (+32 B: conflict-free column reads)
   constexpr int CPR = D / 8;            // 16-byte chunks per key / value row
-  constexpr int LOADS = kTileP * CPR / 256;  // 16-byte chunks per thread per tile, each of K and V
+  constexpr int LOADS = kTileP * CPR / kCtxThreads;  // 16-byte chunks per thread per tile, each of K and V
   // kBufs tile buffers: with the software pipeline, the next tile's keys are read while this
   // tile's values are.
   constexpr int kBufs = MAS_CTX_PIPELINE ? 2 : 1;
@@ -88,7 +96,7 @@ __global__ __launch_bounds__(256, MAS_CTX_MIN_WG) void context_attn(ContextArgs 
   const int kvh = blockIdx.x / hgroups, hg = blockIdx.x - kvh * hgroups;
   const int row = blockIdx.z;
   const int q0 = a.cu_seqlens_q[row], q_len = a.cu_seqlens_q[row + 1] - q0;
-  const int tokens_per_wg = kRowsPerWave * (4 / a.heads_per_wg);
+  const int tokens_per_wg = kRowsPerWave * (kCtxWaves / a.heads_per_wg);
   // Token tiles in reverse launch order: the last tiles reach the most positions, so they start first.
 #ifndef MAS_CTX_REVERSE
 #define MAS_CTX_REVERSE 1
@@ -142,12 +150,12 @@ __global__ __launch_bounds__(256, MAS_CTX_MIN_WG) void context_attn(ContextArgs 
 
   const int32_t* bt = a.block_tables + row * a.bt_stride;
   const int pmask = (1 << a.log2_page) - 1;
-  // Thread's chunks of a tile: chunk c = tid + 256 u -> position tid / CPR + (256 / CPR) u, head-dim
+  // Thread's chunks of a tile: chunk c = tid + T u (T threads) -> position tid / CPR + (T / CPR) u, head-dim
   // chunk tid % CPR (the same for every u). Rows past kv_len or on a page id outside the cache load
   // row 0 of page 0 and are zeroed when stored; the flags are kept so that the loads themselves are
   // not waited on here. With pages of at least a tile, a tile lies in one page: one (wave-uniform)
   // block-table read per tile and precomputed per-thread offsets.
-  constexpr int kPosStep = 256 / CPR;
+  constexpr int kPosStep = kCtxThreads / CPR;
   const int dcol = tid % CPR, prow = tid / CPR;
   const int64_t lane_off = static_cast<int64_t>(prow) * a.entry_stride + kvh * a.head_stride + 8 * dcol;
   struct TileRegs {
@@ -424,7 +432,7 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   const int64_t group = num_q_heads / num_kv_heads;
   const int heads_per_wg = group >= 4 ? 4 : (group == 2 ? 2 : 1);
   const int64_t hgroups = cdiv(group, heads_per_wg);
-  const int64_t tokens_per_wg = kRowsPerWave * (4 / heads_per_wg);
+  const int64_t tokens_per_wg = kRowsPerWave * (kCtxWaves / heads_per_wg);
   const int64_t gx = num_kv_heads * hgroups, gy = cdiv(max_q_len, tokens_per_wg);
   if (gx > INT32_MAX || gy > 65535) return MAS_ERR_UNSUPPORTED;
   int log2_page = 0;
@@ -463,14 +471,14 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   const bool tile_pages = page_size >= kTileP;
   if (head_dim == 64) {
     if (tile_pages)
-      hipLaunchKernelGGL((context_attn<64, true>), grid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((context_attn<64, true>), grid, dim3(kCtxThreads), 0, stream, a);
     else
-      hipLaunchKernelGGL((context_attn<64, false>), grid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((context_attn<64, false>), grid, dim3(kCtxThreads), 0, stream, a);
   } else {
     if (tile_pages)
-      hipLaunchKernelGGL((context_attn<128, true>), grid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((context_attn<128, true>), grid, dim3(kCtxThreads), 0, stream, a);
     else
-      hipLaunchKernelGGL((context_attn<128, false>), grid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((context_attn<128, false>), grid, dim3(kCtxThreads), 0, stream, a);
   }
   return launch_status();
 }
