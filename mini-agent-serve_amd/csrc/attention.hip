@@ -403,43 +403,74 @@ __global__ __launch_bounds__(64) void decode_attn_combine(DecodeArgs a) {
   const int split_len = a.chunks_per_split * kChunk;
   const int nsplit = (L + split_len - 1) / split_len;
   const int64_t base = (static_cast<int64_t>(b) * a.hq + h) * a.max_splits;
-  float mx = kNegInf;
-  for (int s = lane; s < nsplit; s += 64) mx = fmaxf(mx, a.part_ml[(base + s) * 2]);
-  mx = wave_max(mx);
   float acc[DPL];
 #pragma unroll
   for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
   float lsum = 0.f;
-  if (mx != kNegInf) {
-    for (int s0 = 0; s0 < nsplit; s0 += 64) {
-      float wgt = 0.f;
-      if (s0 + lane < nsplit) {
-        const f32x2 ml = *reinterpret_cast<const f32x2*>(a.part_ml + (base + s0 + lane) * 2);
-        wgt = __builtin_amdgcn_exp2f(ml[0] - mx);
-        lsum = __builtin_fmaf(wgt, ml[1], lsum);
-      }
-      const int cnt = min(64, nsplit - s0);
-      const float* po = a.part_o + (base + s0) * D + DPL * lane;
-      // eight splits' partials loaded before any is used, so their loads are in flight together
-      constexpr int kU = 8;
-      int j = 0;
-      for (; j + kU <= cnt; j += kU) {
-        float v[kU][DPL];
+  constexpr int kOneRound = 32;
+  if (nsplit <= kOneRound) {
+    // Every load in one round trip: lane s reads split s's (max, sum), and all splits' partial O
+    // rows are loaded (indices past the last split clamped to it, weighted 0) before the max is
+    // known. Same weights and summation order as the general path below.
+    const int sl = lane < nsplit ? lane : (nsplit > 0 ? nsplit - 1 : 0);
+    const f32x2 ml = *reinterpret_cast<const f32x2*>(a.part_ml + (base + sl) * 2);
+    const float* po = a.part_o + base * D + DPL * lane;
+    float v[kOneRound][DPL];
 #pragma unroll
-        for (int u = 0; u < kU; ++u)
+    for (int u = 0; u < kOneRound; ++u) {
+      const int su = u < nsplit ? u : sl;
 #pragma unroll
-          for (int e = 0; e < DPL; ++e) v[u][e] = po[(j + u) * D + e];
+      for (int e = 0; e < DPL; ++e) v[u][e] = po[su * D + e];
+    }
+    const float m_lane = lane < nsplit ? ml[0] : kNegInf;
+    const float mx = wave_max(m_lane);
+    if (mx != kNegInf) {
+      const float wgt = lane < nsplit ? __builtin_amdgcn_exp2f(m_lane - mx) : 0.f;
+      lsum = wgt * ml[1];
 #pragma unroll
-        for (int u = 0; u < kU; ++u) {
-          const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wgt), j + u));
+      for (int u = 0; u < kOneRound; ++u) {
+        if (u < nsplit) {
+          const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wgt), u));
 #pragma unroll
           for (int e = 0; e < DPL; ++e) acc[e] = __builtin_fmaf(wj, v[u][e], acc[e]);
         }
       }
-      for (; j < cnt; ++j) {
-        const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wgt), j));
+    }
+  } else {
+    float mx = kNegInf;
+    for (int s = lane; s < nsplit; s += 64) mx = fmaxf(mx, a.part_ml[(base + s) * 2]);
+    mx = wave_max(mx);
+    if (mx != kNegInf) {
+      for (int s0 = 0; s0 < nsplit; s0 += 64) {
+        float wgt = 0.f;
+        if (s0 + lane < nsplit) {
+          const f32x2 ml = *reinterpret_cast<const f32x2*>(a.part_ml + (base + s0 + lane) * 2);
+          wgt = __builtin_amdgcn_exp2f(ml[0] - mx);
+          lsum = __builtin_fmaf(wgt, ml[1], lsum);
+        }
+        const int cnt = min(64, nsplit - s0);
+        const float* po = a.part_o + (base + s0) * D + DPL * lane;
+        // eight splits' partials loaded before any is used, so their loads are in flight together
+        constexpr int kU = 8;
+        int j = 0;
+        for (; j + kU <= cnt; j += kU) {
+          float v[kU][DPL];
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) acc[e] = __builtin_fmaf(wj, po[j * D + e], acc[e]);
+          for (int u = 0; u < kU; ++u)
+#pragma unroll
+            for (int e = 0; e < DPL; ++e) v[u][e] = po[(j + u) * D + e];
+#pragma unroll
+          for (int u = 0; u < kU; ++u) {
+            const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wgt), j + u));
+#pragma unroll
+            for (int e = 0; e < DPL; ++e) acc[e] = __builtin_fmaf(wj, v[u][e], acc[e]);
+          }
+        }
+        for (; j < cnt; ++j) {
+          const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wgt), j));
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) acc[e] = __builtin_fmaf(wj, po[j * D + e], acc[e]);
+        }
       }
     }
   }
