@@ -125,17 +125,23 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
-// Sum over the block; `slots` is an LDS array with one float per wavefront. The caller alternates
-// between two slot arrays on consecutive calls, so one barrier per call is enough.
+// Sum over the block (at most 16 wavefronts); `slots` is a 16-float, 16-byte aligned LDS array.
+// Each wavefront's sum goes to its slot and the unused slots are zeroed, then every lane reads all
+// 16 back with four 16-byte reads and adds them as a fixed tree: no loop over the wavefront count
+// after the barrier. The caller alternates between two slot arrays on consecutive calls, so one
+// barrier per call is enough.
 __device__ __forceinline__ float block_sum(float v, float* slots) {
   v = wave_sum(v);
   const int nwaves = blockDim.x / kWave;
   if (nwaves == 1) return v;
-  if ((threadIdx.x & (kWave - 1)) == 0) slots[threadIdx.x / kWave] = v;
+  const int tid = threadIdx.x;
+  if ((tid & (kWave - 1)) == 0) slots[tid / kWave] = v;
+  if (tid >= nwaves && tid < 16) slots[tid] = 0.f;
   __syncthreads();
-  float t = 0.f;
-  for (int i = 0; i < nwaves; ++i) t += slots[i];
-  return t;
+  const f32x4 a0 = *reinterpret_cast<const f32x4*>(slots), a1 = *reinterpret_cast<const f32x4*>(slots + 4);
+  const f32x4 a2 = *reinterpret_cast<const f32x4*>(slots + 8), a3 = *reinterpret_cast<const f32x4*>(slots + 12);
+  return (((a0[0] + a0[1]) + (a0[2] + a0[3])) + ((a1[0] + a1[1]) + (a1[2] + a1[3]))) +
+         (((a2[0] + a2[1]) + (a2[2] + a2[3])) + ((a3[0] + a3[1]) + (a3[2] + a3[3])));
 }
 
 // Four values of one column of a row-major bf16 tile in LDS (rows vrow elements apart) from four
