@@ -10,10 +10,11 @@
 // fp32 accumulation, P rounded to bf16 for the P.V product (as flash-attention kernels do), the
 // output rounded once to bf16.
 //
-// One workgroup of four wavefronts per (kv head, head group, token tile, prompt row). Each wavefront
-// owns 32 query rows: 32 consecutive tokens of one query head; the four wavefronts cover up to four
-// heads of the kv head's group (or, for groups of 1 or 2, more tokens of fewer heads), so every
-// 64-position key / value tile they stage in LDS serves 128 query rows. Per tile:
+// One workgroup of four (or, for groups of 8+ query heads, eight) wavefronts per (kv head, head
+// group, token tile, prompt row). Each wavefront owns 32 query rows: 32 consecutive tokens of one
+// query head; the wavefronts cover up to four heads of the kv head's group and one or more
+// 32-token tiles of them (more tokens of fewer heads for groups of 1 or 2), so every 64-position
+// key / value tile they stage in LDS serves 128 (256) query rows. Per tile:
 //   S^T = K Q^T on MFMA (v_mfma_f32_32x32x16_bf16; A = 32 key rows read from LDS, B = the
 //   wavefront's 32 query rows, held in registers), causal mask, online softmax per query row, then
 //   O^T += V^T P^T on MFMA, where P^T is packed to bf16 straight from the S^T accumulators and V^T
@@ -52,18 +53,12 @@ struct ContextArgs {
   uint32_t* err;
 };
 
-// Wavefronts per workgroup: each stages its share of every key / value tile, and all of them
-// read it.
-#ifndef MAS_CTX_WAVES
-#define MAS_CTX_WAVES 4
-#endif
-constexpr int kCtxWaves = MAS_CTX_WAVES;
-constexpr int kCtxThreads = 64 * kCtxWaves;
-// Workgroups per CU the register allocation must allow (two wavefronts per SIMD: at most 256
-// VGPRs per lane).
-#ifndef MAS_CTX_MIN_WG
-#define MAS_CTX_MIN_WG (8 / MAS_CTX_WAVES)
-#endif
+// Wavefronts per workgroup (kWaves, 4 or 8): each stages its share of every key / value tile, and
+// all of them read it. The register allocation is capped for two wavefronts per SIMD (8 / kWaves
+// workgroups per CU, at most 256 VGPRs per lane). Eight wavefronts (two 32-token tiles of the same
+// heads per workgroup: half the staging per flop) measured ~2% faster with 12 query heads per kv
+// head (123B, 4 x 4096 tokens) and ~4% slower with 4 (24B, 4 x 2048: the grid halves), in
+// alternating runs on one box; the launch picks 8 when a kv head has at least 8 query heads.
 #ifndef MAS_CTX_PIPELINE
 #define MAS_CTX_PIPELINE 1
 #endif
@@ -76,8 +71,10 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-template <int D, bool kTilePages>
-__global__ __launch_bounds__(kCtxThreads, MAS_CTX_MIN_WG) void context_attn(ContextArgs a) {
+template <int D, bool kTilePages, int kWaves>
+__global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextArgs a) {
+  constexpr int kCtxWaves = kWaves;
+  constexpr int kCtxThreads = 64 * kWaves;
   constexpr int KS = D / 16;            // MFMA k-steps over the head dim (S^T)
   constexpr int DB = D / 32;            // 32-dim blocks of O^T
   constexpr int KROW = D + 8;           // bf16 per LDS key row (+16 B: conflict-free A reads)
@@ -432,7 +429,8 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   const int64_t group = num_q_heads / num_kv_heads;
   const int heads_per_wg = group >= 4 ? 4 : (group == 2 ? 2 : 1);
   const int64_t hgroups = cdiv(group, heads_per_wg);
-  const int64_t tokens_per_wg = kRowsPerWave * (kCtxWaves / heads_per_wg);
+  const int waves = group >= 8 ? 8 : 4;
+  const int64_t tokens_per_wg = kRowsPerWave * (waves / heads_per_wg);
   const int64_t gx = num_kv_heads * hgroups, gy = cdiv(max_q_len, tokens_per_wg);
   if (gx > INT32_MAX || gy > 65535) return MAS_ERR_UNSUPPORTED;
   int log2_page = 0;
@@ -469,16 +467,31 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   const dim3 grid(static_cast<uint32_t>(gx), static_cast<uint32_t>(gy), static_cast<uint32_t>(num_rows));
   // Pages of at least a tile: each tile lies in one page (one block-table read per tile).
   const bool tile_pages = page_size >= kTileP;
+  const dim3 block(static_cast<uint32_t>(64 * waves));
   if (head_dim == 64) {
-    if (tile_pages)
-      hipLaunchKernelGGL((context_attn<64, true>), grid, dim3(kCtxThreads), 0, stream, a);
-    else
-      hipLaunchKernelGGL((context_attn<64, false>), grid, dim3(kCtxThreads), 0, stream, a);
+    if (waves == 8) {
+      if (tile_pages)
+        hipLaunchKernelGGL((context_attn<64, true, 8>), grid, block, 0, stream, a);
+      else
+        hipLaunchKernelGGL((context_attn<64, false, 8>), grid, block, 0, stream, a);
+    } else {
+      if (tile_pages)
+        hipLaunchKernelGGL((context_attn<64, true, 4>), grid, block, 0, stream, a);
+      else
+        hipLaunchKernelGGL((context_attn<64, false, 4>), grid, block, 0, stream, a);
+    }
   } else {
-    if (tile_pages)
-      hipLaunchKernelGGL((context_attn<128, true>), grid, dim3(kCtxThreads), 0, stream, a);
-    else
-      hipLaunchKernelGGL((context_attn<128, false>), grid, dim3(kCtxThreads), 0, stream, a);
+    if (waves == 8) {
+      if (tile_pages)
+        hipLaunchKernelGGL((context_attn<128, true, 8>), grid, block, 0, stream, a);
+      else
+        hipLaunchKernelGGL((context_attn<128, false, 8>), grid, block, 0, stream, a);
+    } else {
+      if (tile_pages)
+        hipLaunchKernelGGL((context_attn<128, true, 4>), grid, block, 0, stream, a);
+      else
+        hipLaunchKernelGGL((context_attn<128, false, 4>), grid, block, 0, stream, a);
+    }
   }
   return launch_status();
 }
