@@ -51,6 +51,8 @@ CASES = [
     ([200], [200], 8, 1, 128, 128),                # 8 per kv head, a longer row
     ([130, 64], [600, 64], 16, 4, 128, 512),       # pages of eight tiles, chunked prefill
     ([20, 0, 7], [30, 10, 7], 8, 2, 128, 64),      # a row with no new tokens between two others
+    ([45, 19], [80, 19], 16, 2, 64, 16),           # 8 per kv head (eight-wavefront groups), head_dim 64, small pages
+    ([70, 33], [90, 33], 24, 2, 128, 32),          # 12 per kv head, pages smaller than a tile
 ]
 
 
