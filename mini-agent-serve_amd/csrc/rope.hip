@@ -78,6 +78,9 @@ __global__ __launch_bounds__(kBlock) void rope_inplace(RopeArgs a) {
   const float* trow = a.table + pos * a.table_stride + chunk * 8;
   const f32x4 c0 = load_cached_f4(trow), c1 = load_cached_f4(trow + 4);
   const f32x4 s0 = load_cached_f4(trow + kHalf), s1 = load_cached_f4(trow + kHalf + 4);
+  // Keeps the head rows' unpacking below the table loads: hoisted above them, it would make the
+  // table loads wait for the head rows to arrive.
+  load_fence();
   const float cs[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
   const float sn[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
 

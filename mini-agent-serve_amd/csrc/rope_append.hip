@@ -60,22 +60,26 @@ struct FusedArgs {
   uint32_t* err;
 };
 
-__device__ __forceinline__ bool resolve_page(const FusedArgs& a, int64_t t, int64_t pos, int64_t* dst_row) {
+// Errors set bits in *errbits, reported once at the end of the kernel: a global atomic on a path
+// before the index loads would keep the compiler from reading them through the scalar cache (it
+// would load them as vectors and wait for every load in flight, the head rows included).
+__device__ __forceinline__ bool resolve_page(const FusedArgs& a, int64_t t, int64_t pos, int64_t* dst_row,
+                                             uint32_t* errbits) {
   const int64_t b = a.batch_indices[t];
   const bool b_ok = b >= 0 && b < a.batch;
   if (!b_ok || pos < 0) {
-    report(a.err, b_ok ? MAS_ERRBIT_POSITION : MAS_ERRBIT_BATCH);
+    *errbits |= b_ok ? MAS_ERRBIT_POSITION : MAS_ERRBIT_BATCH;
     return false;
   }
   const int64_t end = a.kv_indptr[b + 1];
   const int64_t idx = static_cast<int64_t>(a.kv_indptr[b]) + pos / a.page_size;
   if (idx < 0 || idx >= a.num_indices || idx >= end) {
-    report(a.err, MAS_ERRBIT_PAGE);
+    *errbits |= MAS_ERRBIT_PAGE;
     return false;
   }
   const int64_t page = a.kv_indices[idx];
   if (page < 0 || page >= a.num_pages) {
-    report(a.err, MAS_ERRBIT_PAGE);
+    *errbits |= MAS_ERRBIT_PAGE;
     return false;
   }
   *dst_row = page * a.page_stride + (pos % a.page_size) * a.entry_stride;
@@ -120,33 +124,37 @@ __global__ __launch_bounds__(kBlock) void rope_append(FusedArgs a) {
   const bool appends = last >= hq;
   const int64_t pos = a.positions[t];
   bool rope_ok = rotates;
+  uint32_t errbits = 0;  // reported at the end (see resolve_page)
   if (rotates && (pos < 0 || pos >= a.table_rows)) {
-    if (lane == 0 && group == 0) report(a.err, MAS_ERRBIT_POSITION);
+    if (group == 0) errbits |= MAS_ERRBIT_POSITION;
     rope_ok = false;
   }
   int64_t dst_row = 0;
-  const bool cache_ok = appends && resolve_page(a, t, pos, &dst_row);
-  float q_scale = 1.0f;
-  if (a.q_scale != nullptr && rope_ok && first < hq) {
-    const int64_t row = pos / a.q_scale_interval;
-    if (row < a.q_scale_rows) {
-      q_scale = bf16_lo(a.q_scale[row]);
-    } else if (lane == 0) {
-      report(a.err, MAS_ERRBIT_POSITION);
-    }
-  }
+  const bool cache_ok = appends && resolve_page(a, t, pos, &dst_row, &errbits);
 
   float cs[8], sn[8];
   if (rope_ok) {
     const float* trow = a.table + pos * a.table_stride + chunk * 8;
     const f32x4 c0 = load_cached_f4(trow), c1 = load_cached_f4(trow + 4);
     const f32x4 s0 = load_cached_f4(trow + kHalf), s1 = load_cached_f4(trow + kHalf + 4);
+    load_fence();  // the head rows' unpacking stays below the table loads (see rope.hip)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       cs[i] = c0[i];
       cs[4 + i] = c1[i];
       sn[i] = s0[i];
       sn[4 + i] = s1[i];
+    }
+  }
+  // After the table loads: the 2-byte scale entry is a vector load, and waiting for it waits for
+  // every load issued before it, all of which the rotation needs anyway.
+  float q_scale = 1.0f;
+  if (a.q_scale != nullptr && rope_ok && first < hq) {
+    const int64_t row = pos / a.q_scale_interval;
+    if (row < a.q_scale_rows) {
+      q_scale = bf16_lo(a.q_scale[row]);
+    } else {
+      errbits |= MAS_ERRBIT_POSITION;
     }
   }
 
@@ -210,6 +218,7 @@ __global__ __launch_bounds__(kBlock) void rope_append(FusedArgs a) {
       store_stream(dst + off_b, ob);
     }
   }
+  if (errbits != 0 && lane == 0) report(a.err, errbits);
 }
 
 template <int LPH, bool kNeox, int PASSES>
