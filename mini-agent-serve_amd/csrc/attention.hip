@@ -398,8 +398,10 @@ __global__ __launch_bounds__(64) void decode_attn_combine(DecodeArgs a) {
   const int lane = threadIdx.x;
   const int h = blockIdx.x, b = blockIdx.y;
   const int64_t raw = a.seq_lens[b];
-  if (h == 0 && lane == 0 && (raw < 0 || raw > (a.max_blocks << a.log2_page))) report(a.err, MAS_ERRBIT_POSITION);
-  const int L = kv_len(a, b);
+  const int64_t cap = a.max_blocks << a.log2_page;
+  // reported at the end: a global atomic here would turn the loads below into waits on every load
+  const bool len_bad = raw < 0 || raw > cap;
+  const int L = static_cast<int>(raw < 0 ? 0 : (raw > cap ? cap : raw));
   const int split_len = a.chunks_per_split * kChunk;
   const int nsplit = (L + split_len - 1) / split_len;
   const int64_t base = (static_cast<int64_t>(b) * a.hq + h) * a.max_splits;
@@ -474,6 +476,7 @@ __global__ __launch_bounds__(64) void decode_attn_combine(DecodeArgs a) {
       }
     }
   }
+  if (len_bad && h == 0 && lane == 0) report(a.err, MAS_ERRBIT_POSITION);
   const float denom = wave_sum(lsum);
   const float scale = denom > 0.f ? a.out_scale / denom : 0.f;
   const int64_t at = b * a.out_stride + h * a.out_head_stride + DPL * lane;
