@@ -47,7 +47,7 @@ COLD_BYTES = 768 << 20         # working set cycled by the cold protocol (3x the
 # HBM bytes per launch of a workload's dominant kernel, from two rocprofv3 counter passes
 # (FETCH_SIZE, then WRITE_SIZE) over `bench.py --pmc-probe`, each calibrated by the same counter on
 # a 256 MiB device copy (fetch factor 1.9997, write factor 1.0000). Re-measure when the kernel changes.
-MEASURED_TRAFFIC = {("decode64_24b", "silu_and_mul"): 12_612_709,
+MEASURED_TRAFFIC = {("decode64_24b", "silu_and_mul"): 12_611_644,
                     ("prefill8192_24b", "silu_and_mul"): 1_610_374_077,
                     ("prefill16384_123b", "silu_and_mul"): 2_818_327_781,
                     ("decode_attn_64x8192_24b", "paged_decode_attention"): 1_114_384_294}
