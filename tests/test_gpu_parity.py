@@ -31,7 +31,9 @@ def _close_bf16(got_bits, want_bits, min_exact=0.99):
 # ---- fused_add_rmsnorm ------------------------------------------------------------------------------
 
 NORM_SHAPES = [(1, 8), (3, 100), (7, 5120), (64, 5120), (256, 5120), (33, 12288), (2, 4096), (5, 65544),
-               (300, 1000)]
+               (300, 1000),
+               (9, 8192),   # 1024 lanes: sixteen wavefront sums, no slot left zero
+               (4, 7680)]   # 960 lanes: fifteen
 
 
 @pytest.mark.parametrize("rows,hidden", NORM_SHAPES)
@@ -70,7 +72,7 @@ def test_fused_add_rmsnorm_strided_rows_and_3d(mas, dev):
     _close_bf16(bits(x3d), want_x)
 
 
-@pytest.mark.parametrize("rows,hidden", [(1, 8), (3, 100), (64, 5120), (128, 12288), (17, 4104)])
+@pytest.mark.parametrize("rows,hidden", [(1, 8), (3, 100), (64, 5120), (128, 12288), (17, 4104), (5, 8192)])
 @pytest.mark.parametrize("scale_kind", ["tensor", "float"])
 def test_fused_add_rmsnorm_quant_fp8(mas, dev, rows, hidden, scale_kind):
     g = torch.Generator().manual_seed(rows * 3 + hidden)
