@@ -170,7 +170,8 @@ int mas_store_kv_slots_bf16(void* k_cache, void* v_cache, int64_t page_stride, i
  * the same positions. Each k row is read once and one kernel is launched instead of two. A
  * position outside the table skips the rotation of that token (its unrotated k is stored); a
  * destination out of range skips its cache write; both are reported through `err` as above.
- * head_dim must be one of 32, 64, 128, 256, 512.
+ * head_dim must be one of 32, 64, 128, 256, 512; table_rows must be at least 1 when there are
+ * rows and heads (each token's table row is loaded before its position is judged).
  * Optional llama-4 query scaling: when q_scale_table (bf16, q_scale_rows entries, row k =
  * bf16(1 + beta * log1p(k))) is given, q ends as bf16(f32(bf16(rope(q))) *
  * f32(q_scale_table[pos / q_scale_interval])), the reference's query_states after its two-rounding

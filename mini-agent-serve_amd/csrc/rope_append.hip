@@ -129,22 +129,26 @@ __global__ __launch_bounds__(kBlock) void rope_append(FusedArgs a) {
     if (group == 0) errbits |= MAS_ERRBIT_POSITION;
     rope_ok = false;
   }
+  // The table row loads first (they need only the position), then the page lookup, whose scalar
+  // loads are waited on one by one while the table rows are in flight; nothing reads the table
+  // rows or the head rows until both are issued. The loads are unconditional (row 0 stands in for
+  // a bad position and is never used; the host rejects an empty table), so no branch joins on them.
+  const float* trow = a.table + (rope_ok ? pos : 0) * a.table_stride + chunk * 8;
+  const f32x4 c0 = load_cached_f4(trow);
+  const f32x4 c1 = load_cached_f4(trow + 4);
+  const f32x4 s0 = load_cached_f4(trow + kHalf);
+  const f32x4 s1 = load_cached_f4(trow + kHalf + 4);
+  load_fence();
   int64_t dst_row = 0;
   const bool cache_ok = appends && resolve_page(a, t, pos, &dst_row, &errbits);
-
+  load_fence();
   float cs[8], sn[8];
-  if (rope_ok) {
-    const float* trow = a.table + pos * a.table_stride + chunk * 8;
-    const f32x4 c0 = load_cached_f4(trow), c1 = load_cached_f4(trow + 4);
-    const f32x4 s0 = load_cached_f4(trow + kHalf), s1 = load_cached_f4(trow + kHalf + 4);
-    load_fence();  // the head rows' unpacking stays below the table loads (see rope.hip)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      cs[i] = c0[i];
-      cs[4 + i] = c1[i];
-      sn[i] = s0[i];
-      sn[4 + i] = s1[i];
-    }
+  for (int i = 0; i < 4; ++i) {
+    cs[i] = c0[i];
+    cs[4 + i] = c1[i];
+    sn[i] = s0[i];
+    sn[4 + i] = s1[i];
   }
   // After the table loads: the 2-byte scale entry is a vector load, and waiting for it waits for
   // every load issued before it, all of which the rotation needs anyway.
@@ -265,6 +269,7 @@ extern "C" int mas_rope_append_paged_kv_cache_bf16(
     return MAS_ERR_UNSUPPORTED;
   if (num_q_heads + 2 * num_kv_heads > INT32_MAX) return MAS_ERR_UNSUPPORTED;
   if (rows == 0 || num_q_heads + num_kv_heads == 0) return MAS_OK;
+  if (table_rows == 0) return MAS_ERR_INVALID_VALUE;  // every token's row is loaded, even a bad position's
   if (positions == nullptr || table == nullptr || batch_indices == nullptr || kv_indptr == nullptr)
     return MAS_ERR_INVALID_VALUE;
   if ((num_q_heads > 0 && q == nullptr) || (num_kv_heads > 0 && (k == nullptr || v == nullptr || k_cache == nullptr ||

@@ -49,6 +49,19 @@ def test_benchmark_skeletons_live_in_their_own_library(mas):
     assert fn(16, 8, None, 0, 40, 8, None, 0, 4, 8, None) == -1            # misaligned destination
 
 
+def test_fused_rope_append_rejects_an_empty_table(mas):
+    """Every token's table row is loaded before its position is judged, so an empty table is an
+    argument error (returned before anything is enqueued) rather than a per-token error bit."""
+    fn = mas.load_library().mas_rope_append_paged_kv_cache_bf16
+    p = 256                                     # any non-null address: nothing is dereferenced
+
+    def call(table_rows, rows):
+        return fn(p, 128, 128, 1, p, 128, 128, p, 128, 128, 1, p, p, 128, table_rows, rows, 128, 1,
+                  p, p, 16 * 128, 128, 128, 4, 16, p, p, 4, p, 1, None, 0, 0, p, None)
+    assert call(0, 3) == -1
+    assert call(0, 0) == 0                      # nothing to do: not an error
+
+
 def test_library_links_against_one_hip_runtime(mas):
     mas.load_library()
     maps = Path("/proc/self/maps").read_text()
