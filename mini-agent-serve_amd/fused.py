@@ -78,6 +78,8 @@ def _fused(positions, query, key, value, head_size, cos_sin_cache, is_neox, batc
         raise ValueError("query, key, value, positions and batch_indices must have the same number of rows")
     if kv_indptr.shape[0] < 1:
         raise ValueError("kv_indptr needs batch + 1 entries")
+    if cos_sin_cache.shape[0] == 0 and q_rows > 0 and hq + heads > 0:
+        raise ValueError("cos_sin_cache has no rows (the fused op loads each token's row before judging its position)")
     q_scale_ptr, q_scale_rows, interval = None, 0, 0
     if llama_4_scaling_beta:
         interval = int(original_max_position_embeddings)

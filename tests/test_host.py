@@ -60,6 +60,17 @@ def test_fused_rope_append_rejects_an_empty_table(mas):
                   p, p, 16 * 128, 128, 128, 4, 16, p, p, 4, p, 1, None, 0, 0, p, None)
     assert call(0, 3) == -1
     assert call(0, 0) == 0                      # nothing to do: not an error
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    with FakeTensorMode():                      # the wrapper says so before the library is called
+        cuda = dict(device="cuda")
+        qkv = torch.empty(3, 6 * 128, dtype=torch.bfloat16, **cuda)
+        cache = torch.empty(4, 16, 2, 128, dtype=torch.bfloat16, **cuda)
+        i32 = torch.zeros(3, dtype=torch.int32, **cuda)
+        with pytest.raises(ValueError, match="cos_sin_cache has no rows"):
+            mas.fused.apply_rope_and_append_paged_kv_cache(
+                i32, qkv[:, :256], qkv[:, 256:512], qkv[:, 512:], 128, torch.empty(0, 128, **cuda), True, i32,
+                (cache, cache.clone()), torch.zeros(4, dtype=torch.int32, **cuda), torch.zeros(2, dtype=torch.int32,
+                                                                                               **cuda))
 
 
 def test_library_links_against_one_hip_runtime(mas):
