@@ -79,6 +79,29 @@ def test_decode_attention_long_splits_and_bmm2_scale(mas, dev):
         _run(mas, dev, q, kc, vc, tables, seq, 0.09, workspace_bytes=16)
 
 
+@pytest.mark.parametrize("batch,hq,hk,width,max_len", [
+    (32, 16, 8, 2048, 1500),    # 32 x 8 x 128 splits of one chunk > 16384: two chunks per split
+    (4500, 2, 2, 64, 400),      # 4500 x 2 x 2 splits of two chunks > 16384: one split of 4 chunks per row
+])
+def test_decode_attention_large_grids_take_longer_splits(mas, dev, batch, hq, hk, width, max_len):
+    """Past 16384 (row, kv head, split) work items the kernel walks several chunks per split even
+    with a full workspace; results as the oracle's. The block tables are wide (16-slot pages) and
+    the rows short, so the oracle stays cheap while the grid is large."""
+    dim, ps = 128, 16
+    g = torch.Generator().manual_seed(batch)
+    lens = torch.randint(1, max_len + 1, (batch,), generator=g).to(torch.int32)
+    pages = int(((lens + ps - 1) // ps).sum()) + 1
+    tables = torch.randint(0, pages, (batch, width), generator=g, dtype=torch.int32)
+    q = torch.randn(batch, hq, dim, generator=g).bfloat16()
+    kc = torch.randn(pages, ps, hk, dim, generator=g).bfloat16()
+    vc = torch.randn(pages, ps, hk, dim, generator=g).bfloat16()
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = _run(mas, dev, q, kc, vc, tables, lens, 0.09, flags=flags)
+    want = ops.paged_decode_attention(bits(q), bits(kc), bits(vc), tables.numpy(), lens.numpy(), 0.09)
+    _check(bits(out), want)
+    assert int(flags.item()) == 0
+
+
 def test_decode_attention_strided_query_and_out(mas, dev):
     """q as the column view of the qkv rows (row stride (Hq + 2 Hk) * D), out as a strided view."""
     batch, hq, hk, dim, ps, lens = 4, 32, 8, 128, 16, [33, 70, 5, 16]
