@@ -69,8 +69,8 @@ def _custom_op_scale(quant_scale) -> tuple[torch.Tensor | None, float]:
 def decode_workspace_bytes(batch: int, num_q_heads: int, head_dim: int, max_blocks: int, page_size: int,
                            chunks_per_split: int = 1) -> int:
     """Workspace bytes the kernel needs for splits of ``chunks_per_split`` chunks of 256 positions
-    (1: the most parallel split; a smaller workspace, or more than 16384 (row, kv head, split)
-    work items, makes the kernel pick longer splits)."""
+    (1: the most parallel split; a smaller workspace, more than 64 splits per row or more than
+    16384 (row, kv head, split) work items make the kernel pick longer splits)."""
     n = _lib.load().mas_paged_decode_attention_workspace_bytes(batch, num_q_heads, head_dim, max_blocks, page_size,
                                                                 chunks_per_split)
     if n < 0:

@@ -593,19 +593,20 @@ extern "C" int mas_paged_decode_attention_bf16(void* out, int64_t out_stride, in
   if (!aligned) return MAS_ERR_MISALIGNED;
 
   // The smallest split (most parallelism) whose partials fit the workspace, with at most
-  // kMaxSplitItems (row, kv head, split) work items: past that, eight rounds of two wavefronts per
-  // SIMD, more splits only add per-split overhead and partials (64 rows x 8 kv heads x 128 splits
-  // of 256 positions: 804 us per call; with 4 chunks per split, 16384 items: 738 us).
+  // kMaxSplitItems (row, kv head, split) work items and kMaxRowSplits splits per row: past those,
+  // more splits only add per-split overhead, partials and combine passes (64 rows x 8 kv heads x
+  // 128 splits of 256 positions: 804 us per call, with 4 chunks per split 738 us; 8 rows x 8 kv
+  // heads x 128 splits: 124 us, with 2 chunks per split 117 us).
   const int64_t chunks = cdiv(cap, kChunk);
 #ifndef MAS_ATTN_MIN_CHUNKS
 #define MAS_ATTN_MIN_CHUNKS 1
 #endif
-  constexpr int64_t kMaxSplitItems = 16384;
+  constexpr int64_t kMaxSplitItems = 16384, kMaxRowSplits = 64;
   int64_t per_split = MAS_ATTN_MIN_CHUNKS;
   while (per_split < chunks &&
          (mas_paged_decode_attention_workspace_bytes(batch, num_q_heads, head_dim, max_blocks, page_size, per_split) >
               workspace_bytes ||
-          cdiv(chunks, per_split) > 65535 || batch * num_kv_heads * cdiv(chunks, per_split) > kMaxSplitItems))
+          cdiv(chunks, per_split) > kMaxRowSplits || batch * num_kv_heads * cdiv(chunks, per_split) > kMaxSplitItems))
     per_split *= 2;
   if (per_split > chunks) per_split = chunks > 0 ? chunks : 1;
   if (mas_paged_decode_attention_workspace_bytes(batch, num_q_heads, head_dim, max_blocks, page_size, per_split) >

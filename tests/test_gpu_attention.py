@@ -48,6 +48,7 @@ CASES = [
     (2, 16, 1, 256, 64, [513, 77]),                # head_dim 256, 16 per kv head
     (3, 6, 2, 128, 4, [9, 40, 2]),                 # 3 per kv head (padded), pages of 4
     (2, 16, 4, 128, 512, [700, 1500]),             # pages of two chunks
+    (2, 8, 2, 128, 256, [9000, 100]),              # 36 splits: the combine's path past 32 splits
 ]
 
 
@@ -82,10 +83,11 @@ def test_decode_attention_long_splits_and_bmm2_scale(mas, dev):
 @pytest.mark.parametrize("batch,hq,hk,width,max_len", [
     (32, 16, 8, 2048, 1500),    # 32 x 8 x 128 splits of one chunk > 16384: two chunks per split
     (4500, 2, 2, 64, 400),      # 4500 x 2 x 2 splits of two chunks > 16384: one split of 4 chunks per row
+    (2, 4, 2, 2048, 1500),      # a small grid, but 128 chunks per row > 64 splits: two chunks per split
 ])
 def test_decode_attention_large_grids_take_longer_splits(mas, dev, batch, hq, hk, width, max_len):
-    """Past 16384 (row, kv head, split) work items the kernel walks several chunks per split even
-    with a full workspace; results as the oracle's. The block tables are wide (16-slot pages) and
+    """Past 16384 (row, kv head, split) work items or 64 splits per row the kernel walks several
+    chunks per split even with a full workspace; results as the oracle's. The block tables are wide (16-slot pages) and
     the rows short, so the oracle stays cheap while the grid is large."""
     dim, ps = 128, 16
     g = torch.Generator().manual_seed(batch)
