@@ -25,9 +25,11 @@ imports it as ``mini_agent_serve_amd``.
 """
 from __future__ import annotations
 
-from . import _lib, activation, attention, embedding, fused, norm, page, rope, workloads
+from . import _compile_fix, _lib, activation, attention, embedding, fused, norm, page, rope, workloads
 from . import layer_pass
 from . import _ops  # noqa: F401  (registers the torch.library ops)
+
+_compile_fix.arm()  # Inductor's missing sym_storage_offset lowering, installed when Inductor loads
 from .activation import silu_and_mul, silu_and_mul_quant
 from .embedding import Embedding
 from .fused import apply_rope_and_append_paged_kv_cache

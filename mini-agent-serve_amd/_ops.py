@@ -4,6 +4,11 @@ The public wrappers call the kernels directly in eager mode (one ctypes call, no
 and route through these ops only while ``torch.compile`` traces, so a compiled model, like the
 reference's ``torch.compile(model, dynamic=True)`` at miniagentserve/engine/model_runner.py:98,
 keeps each kernel as one opaque node instead of breaking its graph at a ctypes call.
+
+Every op whose kernel reports out-of-range indices takes the caller's ``error_flags`` word as a
+mutated optional argument, so a compiled model reports them as an eager one does. Optional
+arguments are passed explicitly by the wrappers (no defaults: the dispatcher's in-place bookkeeping
+indexes mutated arguments by position).
 """
 from __future__ import annotations
 
@@ -15,6 +20,12 @@ from torch.library import custom_op
 from . import activation, attention, embedding, fused, norm, page, rope
 
 Tensor = torch.Tensor
+
+
+def _cache(k_cache: Tensor, v_cache: Optional[Tensor]):
+    """The ops' cache arguments: separate k / v caches, or (v_cache None) one combined
+    ``[pages, 2, ...]`` tensor, passed whole so that the compiled graph holds no sub-view of it."""
+    return (k_cache, v_cache) if v_cache is not None else k_cache
 
 
 def _quant_scale(tensor: Optional[Tensor], host: float):
@@ -78,116 +89,146 @@ def _(input, out):
     return None
 
 
-@custom_op("mas::apply_rope_with_cos_sin_cache_inplace", mutates_args=("query", "key"))
+@custom_op("mas::apply_rope_with_cos_sin_cache_inplace", mutates_args=("query", "key", "error_flags"))
 def _apply_rope(positions: Tensor, query: Tensor, key: Tensor, head_size: int, cos_sin_cache: Tensor,
-                is_neox: bool) -> None:
-    rope._apply_rope(positions, query, key, head_size, cos_sin_cache, is_neox)
+                is_neox: bool, error_flags: Optional[Tensor]) -> None:
+    rope._apply_rope(positions, query, key, head_size, cos_sin_cache, is_neox, error_flags)
 
 
 @_apply_rope.register_fake
-def _(positions, query, key, head_size, cos_sin_cache, is_neox):
+def _(positions, query, key, head_size, cos_sin_cache, is_neox, error_flags):
     return None
 
 
-@custom_op("mas::append_paged_kv_cache", mutates_args=("k_cache", "v_cache"))
+@custom_op("mas::append_paged_kv_cache", mutates_args=("k_cache", "v_cache", "error_flags"))
 def _append_paged_kv_cache(append_key: Tensor, append_value: Tensor, batch_indices: Tensor, positions: Tensor,
-                           k_cache: Tensor, v_cache: Tensor, kv_indices: Tensor, kv_indptr: Tensor,
-                           kv_layout: str) -> None:
-    page._append(append_key, append_value, batch_indices, positions, (k_cache, v_cache), kv_indices, kv_indptr,
-                 kv_layout, None)
+                           k_cache: Tensor, v_cache: Optional[Tensor], kv_indices: Tensor, kv_indptr: Tensor,
+                           kv_layout: str, error_flags: Optional[Tensor]) -> None:
+    page._append(append_key, append_value, batch_indices, positions, _cache(k_cache, v_cache), kv_indices, kv_indptr,
+                 kv_layout, error_flags)
 
 
 @_append_paged_kv_cache.register_fake
-def _(append_key, append_value, batch_indices, positions, k_cache, v_cache, kv_indices, kv_indptr, kv_layout):
+def _(append_key, append_value, batch_indices, positions, k_cache, v_cache, kv_indices, kv_indptr, kv_layout,
+      error_flags):
     return None
 
 
-@custom_op("mas::store_kv_slots", mutates_args=("k_cache", "v_cache"))
+@custom_op("mas::store_kv_slots", mutates_args=("k_cache", "v_cache", "error_flags"))
 def _store_kv_slots(key: Tensor, value: Tensor, k_cache: Tensor, v_cache: Tensor, slot_mapping: Tensor,
-                    kv_layout: str) -> None:
-    page._store_slots(key, value, k_cache, v_cache, slot_mapping, kv_layout, None)
+                    kv_layout: str, error_flags: Optional[Tensor]) -> None:
+    page._store_slots(key, value, k_cache, v_cache, slot_mapping, kv_layout, error_flags)
 
 
 @_store_kv_slots.register_fake
-def _(key, value, k_cache, v_cache, slot_mapping, kv_layout):
+def _(key, value, k_cache, v_cache, slot_mapping, kv_layout, error_flags):
     return None
 
 
-@custom_op("mas::embedding", mutates_args=())
-def _embedding(input_ids: Tensor, weight: Tensor) -> Tensor:
-    out = torch.empty(tuple(input_ids.shape) + (weight.shape[1],), dtype=weight.dtype, device=weight.device)
-    embedding._embedding(input_ids, weight, out)
+def _embedding_shape(input_ids: Tensor, weight: Tensor) -> tuple:
+    return tuple(input_ids.shape) + (weight.shape[1],)
+
+
+@custom_op("mas::embedding", mutates_args=("error_flags",))
+def _embedding(input_ids: Tensor, weight: Tensor, error_flags: Optional[Tensor]) -> Tensor:
+    out = torch.empty(_embedding_shape(input_ids, weight), dtype=weight.dtype, device=weight.device)
+    embedding._embedding(input_ids, weight, out, error_flags)
     return out
 
 
 @_embedding.register_fake
-def _(input_ids, weight):
-    return weight.new_empty(tuple(input_ids.shape) + (weight.shape[1],))
+def _(input_ids, weight, error_flags):
+    return weight.new_empty(_embedding_shape(input_ids, weight))
 
 
-@custom_op("mas::embedding_fill_placeholders", mutates_args=("input_ids",))
-def _embedding_fill(input_ids: Tensor, weight: Tensor, last_tokens: Tensor) -> Tensor:
-    out = torch.empty(tuple(input_ids.shape) + (weight.shape[1],), dtype=weight.dtype, device=weight.device)
-    embedding._embedding(input_ids, weight, out, None, last_tokens)
+@custom_op("mas::embedding_out", mutates_args=("out", "error_flags"))
+def _embedding_out(input_ids: Tensor, weight: Tensor, out: Tensor, error_flags: Optional[Tensor]) -> None:
+    embedding._embedding(input_ids, weight, out, error_flags)
+
+
+@_embedding_out.register_fake
+def _(input_ids, weight, out, error_flags):
+    return None
+
+
+@custom_op("mas::embedding_fill_placeholders", mutates_args=("input_ids", "error_flags"))
+def _embedding_fill(input_ids: Tensor, weight: Tensor, last_tokens: Tensor, error_flags: Optional[Tensor]) -> Tensor:
+    out = torch.empty(_embedding_shape(input_ids, weight), dtype=weight.dtype, device=weight.device)
+    embedding._embedding(input_ids, weight, out, error_flags, last_tokens)
     return out
 
 
 @_embedding_fill.register_fake
-def _(input_ids, weight, last_tokens):
-    return weight.new_empty(tuple(input_ids.shape) + (weight.shape[1],))
+def _(input_ids, weight, last_tokens, error_flags):
+    return weight.new_empty(_embedding_shape(input_ids, weight))
 
 
-@custom_op("mas::fill_placeholders", mutates_args=("input_ids",))
-def _fill(input_ids: Tensor, last_tokens: Tensor) -> None:
-    embedding._fill_placeholders(input_ids, last_tokens)
+@custom_op("mas::embedding_fill_placeholders_out", mutates_args=("input_ids", "out", "error_flags"))
+def _embedding_fill_out(input_ids: Tensor, weight: Tensor, last_tokens: Tensor, out: Tensor,
+                        error_flags: Optional[Tensor]) -> None:
+    embedding._embedding(input_ids, weight, out, error_flags, last_tokens)
 
 
-@_fill.register_fake
-def _(input_ids, last_tokens):
+@_embedding_fill_out.register_fake
+def _(input_ids, weight, last_tokens, out, error_flags):
     return None
 
 
-@custom_op("mas::paged_decode_attention", mutates_args=("workspace", "out"))
-def _paged_decode_attention(query: Tensor, k_cache: Tensor, v_cache: Tensor, workspace: Tensor, block_tables: Tensor,
+@custom_op("mas::fill_placeholders", mutates_args=("input_ids", "error_flags"))
+def _fill(input_ids: Tensor, last_tokens: Tensor, error_flags: Optional[Tensor]) -> None:
+    embedding._fill_placeholders(input_ids, last_tokens, error_flags)
+
+
+@_fill.register_fake
+def _(input_ids, last_tokens, error_flags):
+    return None
+
+
+@custom_op("mas::paged_decode_attention", mutates_args=("workspace", "out", "error_flags"))
+def _paged_decode_attention(query: Tensor, k_cache: Tensor, v_cache: Optional[Tensor], workspace: Tensor,
+                            block_tables: Tensor,
                             seq_lens: Tensor, bmm1_scale: float, bmm2_scale: float, out: Tensor, kv_layout: str,
-                            quant_scale: Optional[Tensor] = None, quant_scale_host: float = 0.0) -> None:
-    attention._decode(query, (k_cache, v_cache), workspace, block_tables, seq_lens, bmm1_scale, bmm2_scale, out,
-                      kv_layout, None, _quant_scale(quant_scale, quant_scale_host))
+                            quant_scale: Optional[Tensor], quant_scale_host: float,
+                            error_flags: Optional[Tensor]) -> None:
+    attention._decode(query, _cache(k_cache, v_cache), workspace, block_tables, seq_lens, bmm1_scale, bmm2_scale, out,
+                      kv_layout, error_flags, _quant_scale(quant_scale, quant_scale_host))
 
 
 @_paged_decode_attention.register_fake
 def _(query, k_cache, v_cache, workspace, block_tables, seq_lens, bmm1_scale, bmm2_scale, out, kv_layout,
-      quant_scale=None, quant_scale_host=0.0):
+      quant_scale, quant_scale_host, error_flags):
     return None
 
 
-@custom_op("mas::paged_context_attention", mutates_args=("out",))
-def _paged_context_attention(query: Tensor, k_cache: Tensor, v_cache: Tensor, block_tables: Tensor, seq_lens: Tensor,
+@custom_op("mas::paged_context_attention", mutates_args=("out", "error_flags"))
+def _paged_context_attention(query: Tensor, k_cache: Tensor, v_cache: Optional[Tensor], block_tables: Tensor,
+                             seq_lens: Tensor,
                              cu_seqlens_q: Tensor, max_q_len: int, bmm1_scale: float, bmm2_scale: float, out: Tensor,
-                             kv_layout: str, quant_scale: Optional[Tensor] = None,
-                             quant_scale_host: float = 0.0) -> None:
-    attention._context(query, (k_cache, v_cache), block_tables, seq_lens, cu_seqlens_q, max_q_len, bmm1_scale,
-                       bmm2_scale, out, kv_layout, None, _quant_scale(quant_scale, quant_scale_host))
+                             kv_layout: str, quant_scale: Optional[Tensor], quant_scale_host: float,
+                             error_flags: Optional[Tensor]) -> None:
+    attention._context(query, _cache(k_cache, v_cache), block_tables, seq_lens, cu_seqlens_q, max_q_len, bmm1_scale,
+                       bmm2_scale, out, kv_layout, error_flags, _quant_scale(quant_scale, quant_scale_host))
 
 
 @_paged_context_attention.register_fake
 def _(query, k_cache, v_cache, block_tables, seq_lens, cu_seqlens_q, max_q_len, bmm1_scale, bmm2_scale, out,
-      kv_layout, quant_scale=None, quant_scale_host=0.0):
+      kv_layout, quant_scale, quant_scale_host, error_flags):
     return None
 
 
-@custom_op("mas::apply_rope_and_append_paged_kv_cache", mutates_args=("query", "key", "k_cache", "v_cache"))
+@custom_op("mas::apply_rope_and_append_paged_kv_cache",
+           mutates_args=("query", "key", "k_cache", "v_cache", "error_flags"))
 def _rope_append(positions: Tensor, query: Tensor, key: Tensor, value: Tensor, head_size: int, cos_sin_cache: Tensor,
-                 is_neox: bool, batch_indices: Tensor, k_cache: Tensor, v_cache: Tensor, kv_indices: Tensor,
-                 kv_indptr: Tensor, kv_layout: str, llama_4_scaling_beta: float = 0.0,
-                 original_max_position_embeddings: int = 0) -> None:
-    fused._fused(positions, query, key, value, head_size, cos_sin_cache, is_neox, batch_indices, (k_cache, v_cache),
-                 kv_indices, kv_indptr, kv_layout, None, llama_4_scaling_beta, original_max_position_embeddings)
+                 is_neox: bool, batch_indices: Tensor, k_cache: Tensor, v_cache: Optional[Tensor], kv_indices: Tensor,
+                 kv_indptr: Tensor, kv_layout: str, llama_4_scaling_beta: float, original_max_position_embeddings: int,
+                 error_flags: Optional[Tensor]) -> None:
+    fused._fused(positions, query, key, value, head_size, cos_sin_cache, is_neox, batch_indices, _cache(k_cache, v_cache),
+                 kv_indices, kv_indptr, kv_layout, error_flags, llama_4_scaling_beta, original_max_position_embeddings)
 
 
 @_rope_append.register_fake
 def _(positions, query, key, value, head_size, cos_sin_cache, is_neox, batch_indices, k_cache, v_cache, kv_indices,
-      kv_indptr, kv_layout, llama_4_scaling_beta=0.0, original_max_position_embeddings=0):
+      kv_indptr, kv_layout, llama_4_scaling_beta, original_max_position_embeddings, error_flags):
     return None
 
 

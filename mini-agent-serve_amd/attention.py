@@ -109,13 +109,13 @@ def _decode(query, kv_cache, workspace_buffer, block_tables, seq_lens, bmm1_scal
         raise ValueError("block_tables must be [batch, max_blocks] int32 with a contiguous last dimension")
     if seq_lens.dim() != 1 or seq_lens.shape[0] < batch or not seq_lens.is_contiguous():
         raise ValueError("seq_lens must be a contiguous int32 [batch] tensor")
+    args = (out.data_ptr(), out.stride(0), out.stride(1), query.data_ptr(), query.stride(0), query.stride(1),
+            k_cache.data_ptr(), v_cache.data_ptr(), pstride, estride, hstride, pages, page_size, block_tables.data_ptr(),
+            block_tables.stride(0), block_tables.shape[1], seq_lens.data_ptr(), batch, hq, hk, dim, float(bmm1_scale),
+            float(bmm2_scale), out_fp8, scale_ptr, scale_host)
     nbytes = workspace_buffer.numel() * workspace_buffer.element_size()
-    st = _lib.load().mas_paged_decode_attention_bf16(
-        out.data_ptr(), out.stride(0), out.stride(1), query.data_ptr(), query.stride(0), query.stride(1),
-        k_cache.data_ptr(), v_cache.data_ptr(), pstride, estride, hstride, pages, page_size, block_tables.data_ptr(),
-        block_tables.stride(0), block_tables.shape[1], seq_lens.data_ptr(), batch, hq, hk, dim, float(bmm1_scale),
-        float(bmm2_scale), out_fp8, scale_ptr, scale_host, workspace_buffer.data_ptr(), nbytes,
-        error_word(error_flags, device), _lib.stream_handle(device))
+    st = _lib.load().mas_paged_decode_attention_bf16(*args, workspace_buffer.data_ptr(), nbytes,
+                                                     error_word(error_flags, device), _lib.stream_handle(device))
     _lib.check(st, "trtllm_batch_decode_with_kv_cache")
 
 
@@ -146,10 +146,11 @@ def trtllm_batch_decode_with_kv_cache(query: torch.Tensor, kv_cache, workspace_b
     if out is None:
         out = torch.empty(query.shape, dtype=dtype, device=query.device)
     if torch.compiler.is_compiling():
-        k_cache, v_cache = (kv_cache if isinstance(kv_cache, (tuple, list)) else (kv_cache[:, 0], kv_cache[:, 1]))
+        k_cache, v_cache = (kv_cache if isinstance(kv_cache, (tuple, list)) else (kv_cache, None))
         qs, qs_host = _custom_op_scale(out_quant_scale)
         torch.ops.mas.paged_decode_attention(query, k_cache, v_cache, workspace_buffer, block_tables, seq_lens,
-                                             float(bmm1_scale), float(bmm2_scale), out, kv_layout, qs, qs_host)
+                                             float(bmm1_scale), float(bmm2_scale), out, kv_layout, qs, qs_host,
+                                             error_flags)
         return out
     _decode(query, kv_cache, workspace_buffer, block_tables, seq_lens, bmm1_scale, bmm2_scale, out, kv_layout,
             error_flags, out_quant_scale)
@@ -231,11 +232,11 @@ def trtllm_batch_context_with_kv_cache(query: torch.Tensor, kv_cache, workspace_
     if out is None:
         out = torch.empty(query.shape, dtype=dtype, device=query.device)
     if torch.compiler.is_compiling():
-        k_cache, v_cache = (kv_cache if isinstance(kv_cache, (tuple, list)) else (kv_cache[:, 0], kv_cache[:, 1]))
+        k_cache, v_cache = (kv_cache if isinstance(kv_cache, (tuple, list)) else (kv_cache, None))
         qs, qs_host = _custom_op_scale(out_quant_scale)
         torch.ops.mas.paged_context_attention(query, k_cache, v_cache, block_tables, seq_lens, cum_seq_lens_q,
                                               int(max_q_len), float(bmm1_scale), float(bmm2_scale), out, kv_layout,
-                                              qs, qs_host)
+                                              qs, qs_host, error_flags)
         return out
     _context(query, kv_cache, block_tables, seq_lens, cum_seq_lens_q, max_q_len, bmm1_scale, bmm2_scale, out,
              kv_layout, error_flags, out_quant_scale)

@@ -48,7 +48,7 @@ def fill_placeholders(input_ids: torch.Tensor, last_tokens: torch.Tensor, *,
     in int64 ``input_ids`` becomes ``last_tokens[r]`` (int32 samples), in place. A placeholder with
     ``r >= len(last_tokens)`` is left as is and sets bit 32 of ``error_flags``."""
     if torch.compiler.is_compiling():
-        torch.ops.mas.fill_placeholders(input_ids, last_tokens)
+        torch.ops.mas.fill_placeholders(input_ids, last_tokens, error_flags)
         return
     _fill_placeholders(input_ids, last_tokens, error_flags)
 
@@ -92,9 +92,15 @@ def embedding(input_ids: torch.Tensor, weight: torch.Tensor, out: torch.Tensor |
     resolved to ``last_tokens[r]`` and written back into ``input_ids``, as ``fill_placeholders``.
     """
     if torch.compiler.is_compiling():
+        if out is None:
+            if last_tokens is not None:
+                return torch.ops.mas.embedding_fill_placeholders(input_ids, weight, last_tokens, error_flags)
+            return torch.ops.mas.embedding(input_ids, weight, error_flags)
         if last_tokens is not None:
-            return torch.ops.mas.embedding_fill_placeholders(input_ids, weight, last_tokens)
-        return torch.ops.mas.embedding(input_ids, weight)
+            torch.ops.mas.embedding_fill_placeholders_out(input_ids, weight, last_tokens, out, error_flags)
+        else:
+            torch.ops.mas.embedding_out(input_ids, weight, out, error_flags)
+        return out
     if out is None:
         out = torch.empty(tuple(input_ids.shape) + (weight.shape[1],), dtype=weight.dtype, device=weight.device)
     _embedding(input_ids, weight, out, error_flags, last_tokens)

@@ -115,13 +115,12 @@ def apply_rope_and_append_paged_kv_cache(positions: torch.Tensor, query: torch.T
     scale (devstral2.py:175-179) to q in place: afterwards ``query`` holds what the reference's
     ``query_states`` holds after line 179, bit for bit."""
     if torch.compiler.is_compiling():
-        k_cache, v_cache = (paged_kv_cache if isinstance(paged_kv_cache, (tuple, list))
-                            else (paged_kv_cache[:, 0], paged_kv_cache[:, 1]))
+        k_cache, v_cache = (paged_kv_cache if isinstance(paged_kv_cache, (tuple, list)) else (paged_kv_cache, None))
         torch.ops.mas.apply_rope_and_append_paged_kv_cache(positions, query, key, value, int(head_size),
                                                            cos_sin_cache, bool(is_neox), batch_indices, k_cache,
                                                            v_cache, kv_indices, kv_indptr, kv_layout,
                                                            float(llama_4_scaling_beta),
-                                                           int(original_max_position_embeddings))
+                                                           int(original_max_position_embeddings), error_flags)
         return
     _fused(positions, query, key, value, head_size, cos_sin_cache, is_neox, batch_indices, paged_kv_cache,
            kv_indices, kv_indptr, kv_layout, error_flags, llama_4_scaling_beta, original_max_position_embeddings)

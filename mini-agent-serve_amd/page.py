@@ -111,10 +111,9 @@ def append_paged_kv_cache(append_key: torch.Tensor, append_value: torch.Tensor, 
     ``error_flags`` (a 1-element int32 device tensor) the kernel records why (bits 2/4/8).
     """
     if torch.compiler.is_compiling():
-        k_cache, v_cache = (paged_kv_cache if isinstance(paged_kv_cache, (tuple, list))
-                            else (paged_kv_cache[:, 0], paged_kv_cache[:, 1]))
+        k_cache, v_cache = (paged_kv_cache if isinstance(paged_kv_cache, (tuple, list)) else (paged_kv_cache, None))
         torch.ops.mas.append_paged_kv_cache(append_key, append_value, batch_indices, positions, k_cache, v_cache,
-                                            kv_indices, kv_indptr, kv_layout)
+                                            kv_indices, kv_indptr, kv_layout, error_flags)
         return
     _append(append_key, append_value, batch_indices, positions, paged_kv_cache, kv_indices, kv_indptr, kv_layout,
             error_flags)
@@ -142,7 +141,7 @@ def store_kv_slots(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor
     """Slot-mapping form of the store: token t goes to page ``slot // page_size``, entry
     ``slot % page_size`` with ``slot = slot_mapping[t]`` (int64); a negative slot is skipped."""
     if torch.compiler.is_compiling():
-        torch.ops.mas.store_kv_slots(key, value, k_cache, v_cache, slot_mapping, kv_layout)
+        torch.ops.mas.store_kv_slots(key, value, k_cache, v_cache, slot_mapping, kv_layout, error_flags)
         return
     _store_slots(key, value, k_cache, v_cache, slot_mapping, kv_layout, error_flags)
 

@@ -84,7 +84,7 @@ def apply_rope_with_cos_sin_cache_inplace(positions: torch.Tensor, query: torch.
     """
     if torch.compiler.is_compiling():
         torch.ops.mas.apply_rope_with_cos_sin_cache_inplace(positions, query, key, int(head_size), cos_sin_cache,
-                                                            bool(is_neox))
+                                                            bool(is_neox), error_flags)
         return
     _apply_rope(positions, query, key, head_size, cos_sin_cache, is_neox, error_flags)
 

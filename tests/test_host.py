@@ -146,13 +146,14 @@ def test_fake_kernels_under_fake_tensor_mode(mas):
         assert torch.ops.mas.silu_and_mul(x).shape == (7, 96)
         ids = torch.empty(2, 5, dtype=torch.int64, device="cuda")
         table = torch.empty(10, 32, dtype=torch.bfloat16, device="cuda")
-        assert torch.ops.mas.embedding(ids, table).shape == (2, 5, 32)
+        assert torch.ops.mas.embedding(ids, table, None).shape == (2, 5, 32)
         h = torch.empty(3, 64, dtype=torch.bfloat16, device="cuda")
         torch.ops.mas.fused_add_rmsnorm(h, h.clone(), torch.empty(64, dtype=torch.bfloat16, device="cuda"), 1e-6)
     expected = {"fused_add_rmsnorm", "fused_add_rmsnorm_quant", "fused_add_rmsnorm_quant_hs", "silu_and_mul",
                 "silu_and_mul_out", "apply_rope_with_cos_sin_cache_inplace", "append_paged_kv_cache",
-                "store_kv_slots", "embedding", "silu_and_mul_quant", "silu_and_mul_quant_hs",
-                "apply_rope_and_append_paged_kv_cache"}
+                "store_kv_slots", "embedding", "embedding_out", "embedding_fill_placeholders",
+                "embedding_fill_placeholders_out", "fill_placeholders", "silu_and_mul_quant", "silu_and_mul_quant_hs",
+                "apply_rope_and_append_paged_kv_cache", "paged_decode_attention", "paged_context_attention"}
     assert expected <= {name for name in dir(torch.ops.mas) if not name.startswith("_")}
 
 
