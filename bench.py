@@ -10,14 +10,20 @@ cycles through enough distinct layer buffer sets (each with its own KV cache) th
 finds its data in the 256 MB Infinity Cache - what a 40-layer forward pass sees; steps are replayed
 from a captured HIP graph, as the reference's model runner replays its decode graphs.
 
+Timing: after the warm-up steps, the --steps timed steps run in chunks of at most 50; each chunk's
+HIP graph runs untimed lead-in steps, a kernel that stores the GPU wall clock, the chunk's steps, a
+second clock store and one more step. Each graph is replayed once untimed (a graph's first replay
+also uploads it), then the chunks' stamped intervals are summed: exactly --steps steps, with no
+graph launch or host gap inside (ROCm does not allow timing events inside graphs). Beside it: HIP events around replays of graphs of the timed steps
+alone (graph launch included, ``graph_us_per_step``) and the host clock (``host_us_per_step``).
+
 Printed on one JSON line: the metric (credited HBM bytes per step / time per step), microseconds
 per layer, each kernel's average launch duration and bandwidth (HIP events around a graph of
 back-to-back launches of that kernel, on the stream it runs on) beside the same for its memory
 skeleton (a kernel moving the same streams of the same buffers with no arithmetic: the practical
 ceiling at that size, launch ramp-up and drain included), the roofline of the dominant kernel, the
-CPU baseline (the numpy oracle timed on a bounded sample of the same workload on the host, one
-thread) and, for the layer workloads, the same sample as torch CPU code on all of torch's host
-threads (`cpu_torch`).
+CPU baseline (the same ops as torch CPU code on all of torch's host threads, on a bounded sample of
+the workload, thread count stated) and, beside it, the numpy oracle on one thread (`cpu_oracle`).
 
     python bench.py [--steps K] [--warmup W] [--workload NAME] [--protocol cold|hot] [--no-cpu]
 """
@@ -91,19 +97,81 @@ def step_ops(shape, fp8: bool) -> tuple[str, ...]:
 
 SKELETON_OPS = ("fused_add_rmsnorm", "rope", "append_paged_kv_cache", "silu_and_mul")
 _skeleton_fn = None
+_stamp_fn = None
+_clock_khz = 0
 
 
-def load_skeletons(mas) -> bool:
-    """Loads the benchmark's memory skeletons (libmas_bench.so, built beside the kernel library)."""
-    global _skeleton_fn
+def load_skeletons(mas) -> None:
+    """Loads the benchmark's library (libmas_bench.so, built beside the kernel library): the memory
+    skeletons and the wall-clock stamp kernel that brackets timed steps inside a graph."""
+    global _skeleton_fn, _stamp_fn, _clock_khz
     path = Path(mas.__file__).resolve().parent / "libmas_bench.so"
     if not path.exists():
-        return False
-    fn = ctypes.CDLL(str(path)).mas_bench_stream_skeleton
+        raise RuntimeError(f"{path.name} is not built; run __graft_entry__.build()")
+    lib = ctypes.CDLL(str(path))
+    fn = lib.mas_bench_stream_skeleton
     fn.restype = ctypes.c_int
     fn.argtypes = [ctypes.c_void_p, ctypes.c_int64] * 4 + [ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p]
     _skeleton_fn = fn
-    return True
+    _stamp_fn = lib.mas_bench_timestamp
+    _stamp_fn.restype = ctypes.c_int
+    _stamp_fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    khz = ctypes.c_int(0)
+    lib.mas_bench_wall_clock_khz.restype = ctypes.c_int
+    if lib.mas_bench_wall_clock_khz(ctypes.byref(khz)) != 0 or khz.value <= 0:
+        raise RuntimeError("could not read the GPU wall-clock rate")
+    _clock_khz = khz.value
+
+
+def _stamp(ptr: int) -> None:
+    if _stamp_fn(ptr, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)) != 0:
+        raise RuntimeError("timestamp kernel launch failed")
+
+
+def time_steps(run_steps, k: int, w: int, lead: int, per_graph: int) -> dict:
+    """Times exactly ``k`` steps. ``run_steps(lo, hi)`` enqueues steps lo..hi-1 (step i uses input
+    set i modulo the sets, so consecutive ranges continue the cycle).
+
+    The k steps run in chunks of at most ``per_graph``. Each chunk's HIP graph holds ``lead``
+    untimed steps, a wall-clock stamp, the chunk's steps, a second stamp and one more step, so the
+    stamps bracket exactly those steps inside one graph replay: no graph launch, host gap or
+    synchronisation falls between them (one kernel boundary does: the second stamp's dispatch).
+    After ``w`` warm-up steps (their own graph) and one untimed replay of each chunk graph (a
+    graph's first replay on ROCm also uploads it, ~9% slower), the chunk graphs are replayed in
+    turn and their intervals summed. Chunks keep graphs small: a single graph of a few thousand
+    kernels ran ~7% slower per kernel than graphs of a few hundred. Also reported: HIP events
+    around replays of graphs of the k steps alone (graph launch included) and the host clock
+    around replay + synchronize."""
+    stamps = torch.zeros(2, dtype=torch.int64, device="cuda")
+    at = stamps.data_ptr()
+    chunk = max(1, min(k, per_graph))
+    sizes = [chunk] * (k // chunk) + ([k % chunk] if k % chunk else [])
+
+    def stamped(count):
+        def body():
+            run_steps(0, lead)
+            _stamp(at)
+            run_steps(lead, lead + count)
+            _stamp(at + 8)
+            run_steps(lead + count, lead + count + 1)
+        return capture(body)
+
+    graphs = {count: stamped(count) for count in set(sizes)}
+    warm = capture(lambda: run_steps(0, w)) if w > 0 else None
+    torch.cuda.synchronize()
+    if warm is not None:
+        warm.replay()
+    for g in graphs.values():
+        g.replay()
+    ticks = 0
+    for count in sizes:
+        graphs[count].replay()
+        torch.cuda.synchronize()
+        t0, t1 = stamps.tolist()
+        ticks += t1 - t0
+    del graphs, warm
+    graph_s, host_s = timed_replays(lambda count: capture(lambda: run_steps(0, count)), per_graph, k, w)
+    return {"device_s": ticks / (_clock_khz * 1e3), "graph_s": graph_s, "host_s": host_s, "chunks": len(sizes)}
 
 
 def skeleton_launcher(b, op):
@@ -194,6 +262,43 @@ def time_ops(mas, layer_sets, launches: int, ops: tuple[str, ...], replays: int 
     return out
 
 
+def timed_replays(make_graph, per_graph: int, k: int, w: int) -> tuple[float, float]:
+    """(device seconds, host seconds) for exactly ``k`` steps replayed from captured HIP graphs.
+
+    ``make_graph(count)`` captures a graph of ``count`` consecutive steps starting from the first
+    input set (``per_graph`` steps make whole passes over the sets). Device timing: ``w`` warm-up
+    steps, then one untimed lead-in replay of ``per_graph`` steps, then the ``k`` timed steps (whole
+    ``per_graph`` graphs and one remainder graph) between two HIP events on the stream. The timed
+    graphs are enqueued while the lead-in still runs, so no graph launch or host gap falls inside
+    the timed region, whatever ``k``. Host timing: the same ``k`` steps from an idle stream,
+    ``time.perf_counter`` around replay and synchronize (graph launch and sync included)."""
+    graphs = {per_graph: make_graph(per_graph)}
+    for count in (w, k):                              # every graph is captured before the timed region
+        rem = count % per_graph
+        if rem and rem not in graphs:
+            graphs[rem] = make_graph(rem)
+
+    def replay(count):
+        for _ in range(count // per_graph):
+            graphs[per_graph].replay()
+        if count % per_graph:
+            graphs[count % per_graph].replay()
+
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    replay(w)
+    graphs[per_graph].replay()                        # lead-in, untimed
+    start.record()
+    replay(k)
+    stop.record()
+    torch.cuda.synchronize()
+    device_s = start.elapsed_time(stop) * 1e-3
+    t0 = time.perf_counter()
+    replay(k)
+    torch.cuda.synchronize()
+    return device_s, time.perf_counter() - t0
+
+
 def copy_ceiling_gbs(dev, nbytes: int = 1 << 30) -> float:
     """Device-to-device copy rate (read + write bytes per second), a practical streaming ceiling."""
     a = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev)
@@ -222,8 +327,9 @@ def capture(fn) -> torch.cuda.CUDAGraph:
     return g
 
 
-def cpu_baseline_layer(shape, seconds: float, fp8: bool) -> dict:
-    """The oracle's five layer ops on a bounded sample of the workload, timed on the host."""
+def cpu_oracle_layer(shape, seconds: float, fp8: bool) -> dict:
+    """The oracle's five layer ops (numpy, one thread) on a bounded sample of the workload, timed on
+    the host; reported beside the torch CPU baseline."""
     from oracle import ops as oops
 
     mas = __graft_entry__.load_package()
@@ -288,9 +394,9 @@ def cpu_baseline_layer(shape, seconds: float, fp8: bool) -> dict:
 
 
 def cpu_torch_layer(shape, seconds: float, fp8: bool) -> dict:
-    """The same sample as the oracle baseline, as torch CPU code on all of the host's torch threads:
-    the reference's math in torch (fp32 from bf16, rounded once), the kind of CPU path a user without
-    the GPU kernels would run. Reported beside the single-threaded oracle baseline."""
+    """The CPU baseline: the step's ops as torch CPU code on all of torch's host threads (the thread
+    count is reported), on a bounded sample of the workload - the reference's math in torch (fp32
+    from bf16, rounded once), the CPU path a user without the GPU kernels would run."""
     import torch.nn.functional as F
 
     mas = __graft_entry__.load_package()
@@ -367,11 +473,120 @@ def cpu_torch_layer(shape, seconds: float, fp8: bool) -> dict:
     dt = time.perf_counter() - t0
     calls = {"fused_add_rmsnorm": 1 if shape.norm_only else 2}
     return {"value": round(per_layer * reps / dt / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
-            "kind": "torch",
+            "kind": "port",
             "sample": f"{reps} passes of the step's ops as torch CPU code on {tokens} of {shape.tokens} tokens "
                       f"({dt:.1f} s, {torch.get_num_threads()} threads)",
             # average µs per call of each op on the sample's tokens
             "op_us": {key: round(1e6 * v / (reps * calls.get(key, 1)), 1) for key, v in op_s.items() if v > 0}}
+
+
+class EmbeddingBench:
+    """The token-embedding gather (devstral2.py:282) on the shape's tokens, cold: ``launches`` launches
+    each gather ``tokens`` distinct rows of a ``[vocab, hidden]`` bf16 table (no row repeats within a
+    replay, which touches more than the 256 MB Infinity Cache), writing the sets' output rows in turn.
+
+    Also the step-input path (model_runner.py:135,149-154 + devstral2.py:282): each step's ids are
+    refreshed from a pristine copy (standing in for the runner's one host-to-device transfer, which
+    rewrites the placeholders every step), then either the reference's torch sequence
+    (``fill_placeholders`` as written, then ``F.embedding``) or this library's one launch resolving the
+    placeholders inside the gather."""
+
+    def __init__(self, mas, shape, dev, launches: int = 512, seed: int = 0):
+        self.mas = mas
+        n, h, v = shape.tokens, shape.hidden, shape.vocab
+        self.tokens, self.hidden, self.vocab = n, h, v
+        self.launches = min(launches, v // n)
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.table = torch.randn(v, h, generator=g, device=dev).to(torch.bfloat16)
+        cpu = torch.Generator().manual_seed(seed)
+        rows = torch.randperm(v, generator=cpu)[: self.launches * n].view(self.launches, n)
+        self.ids = rows.to(dev)
+        self.outs = [torch.empty(n, h, dtype=torch.bfloat16, device=dev) for _ in range(min(self.launches, 50))]
+        # decode steps: every id is a placeholder -1 - r for the previous step's sample r
+        self.placeholders = (-1 - torch.arange(n, dtype=torch.int64)).to(dev)
+        self.step_ids = [torch.empty(n, dtype=torch.int64, device=dev) for _ in range(self.launches)]
+        self.last = [r.to(torch.int32) for r in self.ids]
+
+    def credited(self) -> int:
+        return 4 * self.tokens * self.hidden + 8 * self.tokens
+
+    def launcher(self, op: str, i: int):
+        mas, out = self.mas, self.outs[i % len(self.outs)]
+        ids, step_ids, last, ph = self.ids[i], self.step_ids[i], self.last[i], self.placeholders
+        if op == "embedding":
+            return lambda: mas.embedding.embedding(ids, self.table, out=out)
+        if op == "skeleton:embedding":
+            # the same bytes and launch shape with no id lookup: rows i, i + stride, ... of the table
+            stride = (self.vocab // self.tokens) * self.table.stride(0)
+            src = self.table[i % (self.vocab // self.tokens)]
+            ptrs = (src.data_ptr(), stride, None, 0, out.data_ptr(), out.stride(0), None, 0, self.tokens, self.hidden)
+
+            def launch():
+                st = _skeleton_fn(*ptrs, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+                if st != 0:
+                    raise RuntimeError(f"embedding skeleton failed with status {st}")
+            return launch
+        if op == "step_input_reset":
+            return lambda: step_ids.copy_(ph)
+        if op == "step_input_reference":
+            def reference():
+                step_ids.copy_(ph)
+                # ModelRunner.fill_placeholders (model_runner.py:149-154), then embed_tokens (devstral2.py:282)
+                is_placeholder = step_ids < 0
+                rows = (-1 - step_ids).clamp(min=0)
+                sampled = last[rows]
+                step_ids.copy_(torch.where(is_placeholder, sampled, step_ids))
+                torch.nn.functional.embedding(step_ids, self.table)
+            return reference
+        if op == "step_input_fused":
+            def fused():
+                step_ids.copy_(ph)
+                mas.embedding.embedding(step_ids, self.table, out=out, last_tokens=last)
+            return fused
+        raise ValueError(op)
+
+    def time(self, ops, replays: int = 5) -> dict[str, float]:
+        """Average µs per launch (per step for the step-input sequences), as ``time_ops``."""
+        res = {}
+        for op in ops:
+            fns = [self.launcher(op, i) for i in range(self.launches)]
+
+            def body():
+                for f in fns:
+                    f()
+
+            g = capture(body)
+            g.replay()
+            events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                      for _ in range(replays)]
+            for start, stop in events:
+                start.record()
+                g.replay()
+                stop.record()
+            torch.cuda.synchronize()
+            times = sorted(a.elapsed_time(b) for a, b in events)
+            res[op] = 1000.0 * times[len(times) // 2] / self.launches
+            del g
+        return res
+
+    def report(self) -> tuple[dict, dict]:
+        """(the embedding's ``ops`` entry, the step-input comparison)."""
+        ops = ("embedding", "step_input_reset", "step_input_reference", "step_input_fused")
+        if _skeleton_fn is not None:
+            ops = ops + ("skeleton:embedding",)
+        t = self.time(ops)
+        cb = self.credited()
+        entry = {"us": round(t["embedding"], 3), "GB/s": round(cb / t["embedding"] / 1e3, 1),
+                 "frac": round(cb / t["embedding"] / 1e3 / PEAK_HBM_GBS, 4), "launches_per_replay": self.launches}
+        if "skeleton:embedding" in t:
+            entry["skeleton_us"] = round(t["skeleton:embedding"], 3)
+            entry["of_skeleton"] = round(t["skeleton:embedding"] / t["embedding"], 3)
+        steps = {"ids_refresh_us": round(t["step_input_reset"], 3),
+                 "reference_us": round(t["step_input_reference"], 3),
+                 "fused_us": round(t["step_input_fused"], 3),
+                 "what": "per step: ids refreshed (device copy), then the reference's fill_placeholders + "
+                         "F.embedding (6 launches) or one placeholder-resolving gather; graph-replayed, cold rows"}
+        return entry, steps
 
 
 def run_layer_workload(mas, args, shape, dev) -> dict:
@@ -390,36 +605,18 @@ def run_layer_workload(mas, args, shape, dev) -> dict:
         for i in range(lo, hi):
             lp.run_layer(sets[i % n_sets])
 
-    def timed_steps(k: int, w: int) -> float:
-        """Seconds for k steps replayed from HIP graphs after w warm-up steps. One replay runs a
-        whole number of passes over the layer sets and at least 50 steps, amortising the launch."""
+    def timed_steps(k: int, w: int) -> dict:
         per_graph = n_sets * max(1, math.ceil(50 / n_sets))
-        graphs = {per_graph: capture(lambda: run_range(0, per_graph))}
-        for count in (w, k):                          # every graph is captured before the timed region
-            rem = count % per_graph
-            if rem and rem not in graphs:
-                graphs[rem] = capture(lambda: run_range(0, rem))
+        return time_steps(run_range, k, w, lead=per_graph, per_graph=per_graph)
 
-        def replay(count):
-            for _ in range(count // per_graph):
-                graphs[per_graph].replay()
-            if count % per_graph:
-                graphs[count % per_graph].replay()
-
-        replay(w)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        replay(k)
-        torch.cuda.synchronize()
-        return time.perf_counter() - t0
-
-    elapsed = timed_steps(steps, warmup)
+    timing = timed_steps(steps, warmup)
+    elapsed = timing["device_s"]
     other_us = None
     if not shape.norm_only:
         # the other RoPE / KV form, for comparison (same buffers, same step count)
         for b in sets:
             b.fuse_rope_kv = not fused
-        other_us = timed_steps(steps, warmup) / steps * 1e6
+        other_us = timed_steps(steps, warmup)["device_s"] / steps * 1e6
         for b in sets:
             b.fuse_rope_kv = fused
 
@@ -444,11 +641,16 @@ def run_layer_workload(mas, args, shape, dev) -> dict:
             sk = op_us[f"skeleton:{op}"]
             ops[op]["skeleton_us"] = round(sk, 3)
             ops[op]["of_skeleton"] = round(sk / op_us[op], 3)
+    step_inputs = None
+    if shape.decode and not shape.norm_only:
+        ops["embedding"], step_inputs = EmbeddingBench(mas, shape, dev).report()
     ms_per_step = elapsed / steps * 1e3
     dominant = step_ops(shape, args.fp8)[0 if shape.norm_only else 3]
     res = {"steps": steps, "warmup": warmup, "ms_per_step": ms_per_step, "per_step_bytes": per_step,
            "value": per_step / (ms_per_step * 1e-3) / 1e9, "stream_us_per_step": stream_us, "ops": ops,
-           "sets": n_sets, "dominant": dominant, "dominant_bytes": cb[dominant], "dominant_us": op_us[dominant]}
+           "sets": n_sets, "dominant": dominant, "dominant_bytes": cb[dominant], "dominant_us": op_us[dominant],
+           "graph_us_per_step": timing["graph_s"] / steps * 1e6, "host_us_per_step": timing["host_s"] / steps * 1e6,
+           "step_inputs": step_inputs}
     if other_us is not None:
         res["separate_us_per_layer" if fused else "fused_us_per_layer"] = other_us
     return res
@@ -460,26 +662,21 @@ def run_pass_workload(mas, args, shape, dev) -> dict:
     per_step = passes[0].credited_bytes()
     steps = args.steps if args.steps is not None else 20
     warmup = args.warmup if args.warmup is not None else 3
-    g = capture(passes[0].run)
-    for _ in range(warmup):
-        g.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        g.replay()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+    timing = time_steps(lambda lo, hi: [passes[0].run() for _ in range(lo, hi)], steps, warmup, lead=1, per_graph=10)
+    elapsed = timing["device_s"]
     ops_timed = step_ops(shape, args.fp8)
     op_us = time_ops(mas, passes[0].layers, shape.layers, ops_timed)
     cb = wl.credited_bytes(shape)
     ops = {op: {"us": round(us, 3), "GB/s": round(cb[op] / us / 1e3, 1),
                 "frac": round(cb[op] / us / 1e3 / PEAK_HBM_GBS, 4)} for op, us in op_us.items()}
+    ops["embedding"], step_inputs = EmbeddingBench(mas, shape, dev).report()
     ms_per_step = elapsed / steps * 1e3
     dominant = ops_timed[3]
     return {"steps": steps, "warmup": warmup, "ms_per_step": ms_per_step, "per_step_bytes": per_step,
             "value": per_step / (ms_per_step * 1e-3) / 1e9, "ops": ops, "sets": 1, "dominant": dominant,
             "dominant_bytes": cb[dominant], "dominant_us": op_us[dominant],
-            "us_per_layer": ms_per_step * 1e3 / shape.layers}
+            "us_per_layer": ms_per_step * 1e3 / shape.layers, "graph_us_per_step": timing["graph_s"] / steps * 1e6,
+            "host_us_per_step": timing["host_s"] / steps * 1e6, "step_inputs": step_inputs}
 
 
 def run_attention_workload(mas, args, shape, dev) -> dict:
@@ -497,15 +694,8 @@ def run_attention_workload(mas, args, shape, dev) -> dict:
     steps = args.steps if args.steps is not None else 50
     warmup = args.warmup if args.warmup is not None else 5
     call()
-    g = capture(call)
-    for _ in range(warmup):
-        g.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        g.replay()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+    timing = time_steps(lambda lo, hi: [call() for _ in range(lo, hi)], steps, warmup, lead=4, per_graph=10)
+    elapsed = timing["device_s"]
     # per-call duration: HIP events around graphs of back-to-back calls, median of five replays
     graph_calls = 10
     gb = capture(lambda: [call() for _ in range(graph_calls)])
@@ -526,7 +716,8 @@ def run_attention_workload(mas, args, shape, dev) -> dict:
                                                "frac": round(per_step / call_us / 1e3 / PEAK_HBM_GBS, 4)}},
             "attention": {"mean_len": round(float(lens.float().mean()), 1), "longest": int(lens.max()),
                           "positions": int(lens.sum()), "kv_pages": inp.k_cache.shape[0]},
-            "inputs": inp}
+            "inputs": inp, "graph_us_per_step": timing["graph_s"] / steps * 1e6,
+            "host_us_per_step": timing["host_s"] / steps * 1e6}
 
 
 def context_main(mas, args, shape, dev) -> int:
@@ -546,15 +737,8 @@ def context_main(mas, args, shape, dev) -> int:
     steps = args.steps if args.steps is not None else 20
     warmup = args.warmup if args.warmup is not None else 3
     call()
-    g = capture(call)
-    for _ in range(warmup):
-        g.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        g.replay()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+    timing = time_steps(lambda lo, hi: [call() for _ in range(lo, hi)], steps, warmup, lead=1, per_graph=4)
+    elapsed = timing["device_s"]
     gb = capture(lambda: [call() for _ in range(4)])
     gb.replay()
     events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(5)]
@@ -574,7 +758,8 @@ def context_main(mas, args, shape, dev) -> int:
         "config": {"workload": shape.name, "rows": shape.rows, "q_len": shape.q_len, "cached": shape.cached,
                    "q_heads": shape.q_heads, "kv_heads": shape.kv_heads, "head_dim": shape.head_dim,
                    "page_size": shape.page_size, "flops": flops, "launch": "hip-graph"},
-        "us_per_call": round(ms_per_step * 1e3, 3),
+        "us_per_call": round(ms_per_step * 1e3, 3), "graph_us_per_call": round(timing["graph_s"] / steps * 1e6, 3),
+        "host_us_per_call": round(timing["host_s"] / steps * 1e6, 3),
         "ops": {"paged_context_attention": {"us": round(call_us, 3), "TFLOP/s": round(kernel_tflops, 1),
                                             "frac": round(kernel_tflops / PEAK_BF16_TFLOPS, 4)}},
         "roofline": {"bound": "mfma", "kernel": "paged_context_attention", "achieved": round(kernel_tflops, 1),
@@ -582,12 +767,85 @@ def context_main(mas, args, shape, dev) -> int:
                      "traffic": None, "flops_per_launch": flops, "avg_launch_us": round(call_us, 3)},
     }
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline_context(inp, args.cpu_seconds)
+        line["cpu_baseline"] = cpu_torch_context(inp, args.cpu_seconds)
+        line["cpu_oracle"] = cpu_oracle_context(inp, args.cpu_seconds / 2)
     print(json.dumps(line), flush=True)
     return 0
 
 
-def cpu_baseline_context(inp, seconds: float) -> dict:
+def _cpu_kv(inp):
+    """The workload's caches on the host, as fp32 [pages * page_size, kv_heads, head_dim]."""
+    s = inp.shape
+    return (inp.k_cache.cpu().float().view(-1, s.kv_heads, s.head_dim),
+            inp.v_cache.cpu().float().view(-1, s.kv_heads, s.head_dim))
+
+
+def _cpu_rows(tables_row, n: int, page_size: int) -> torch.Tensor:
+    """Cache rows of positions 0..n-1 through one block-table row."""
+    p = torch.arange(n)
+    return tables_row[p // page_size].long() * page_size + p % page_size
+
+
+def cpu_torch_attention(inp, seconds: float) -> dict:
+    """The CPU baseline for decode attention: each row's attention as torch CPU code in fp32 (keys and
+    values gathered through its block table, grouped query heads batched per kv head) on all of
+    torch's host threads, cycling over the workload's rows for about ``seconds``; credited bytes of
+    the rows done per second."""
+    s = inp.shape
+    q = inp.q.cpu().float()
+    kc, vc = _cpu_kv(inp)
+    tables, lens = inp.block_tables.cpu(), inp.seq_lens.cpu()
+    g = s.q_heads // s.kv_heads
+    scale = s.head_dim ** -0.5
+    done_bytes, rows, t0 = 0, 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        b = rows % s.batch
+        n = int(lens[b])
+        idx = _cpu_rows(tables[b], n, s.page_size)
+        k = kc[idx].permute(1, 2, 0)                                   # [Hk, D, n]
+        v = vc[idx].permute(1, 0, 2)                                   # [Hk, n, D]
+        p = torch.softmax((q[b].view(s.kv_heads, g, s.head_dim) @ k) * scale, dim=-1)
+        (p @ v).to(torch.bfloat16)
+        done_bytes += n * s.kv_heads * s.head_dim * 4 + 2 * s.q_heads * s.head_dim * 2 + 4 * (-(-n // s.page_size)) + 4
+        rows += 1
+    elapsed = time.perf_counter() - t0
+    return {"value": round(done_bytes / elapsed / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port", "sample": f"{rows} rows of the workload's decode attention as torch CPU code, fp32 "
+                                      f"({elapsed:.1f} s, {torch.get_num_threads()} threads)"}
+
+
+def cpu_torch_context(inp, seconds: float) -> dict:
+    """The CPU baseline for context attention: causal attention of the first row's query tokens in
+    blocks of 64 from its end (the longest reach first) as torch CPU code in fp32 on all of torch's
+    host threads, for about ``seconds``; algorithmic flops done per second."""
+    s = inp.shape
+    kv_len = s.cached + s.q_len
+    q = inp.q.cpu()[: s.q_len].float()                                  # row 0's tokens
+    kc, vc = _cpu_kv(inp)
+    idx = _cpu_rows(inp.block_tables.cpu()[0], kv_len, s.page_size)
+    k = kc[idx].permute(1, 2, 0)                                        # [Hk, D, kv_len]
+    v = vc[idx].permute(1, 0, 2)                                        # [Hk, kv_len, D]
+    g = s.q_heads // s.kv_heads
+    scale = s.head_dim ** -0.5
+    done, tokens, t0 = 0, 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds and tokens < s.q_len:
+        hi = s.q_len - tokens
+        lo = max(0, hi - 64)
+        reach = s.cached + hi                                           # positions the block's last token sees
+        qb = q[lo:hi].view(hi - lo, s.kv_heads, g, s.head_dim).permute(1, 2, 0, 3).reshape(s.kv_heads, -1, s.head_dim)
+        sc = (qb @ k[:, :, :reach]) * scale                             # [Hk, g * tokens, reach]
+        pos = s.cached + torch.arange(lo, hi).repeat(g)
+        sc.masked_fill_(torch.arange(reach)[None, None, :] > pos[None, :, None], float("-inf"))
+        (torch.softmax(sc, dim=-1) @ v[:, :reach]).to(torch.bfloat16)
+        done += sum(s.cached + i + 1 for i in range(lo, hi)) * s.q_heads * s.head_dim * 4
+        tokens += hi - lo
+    elapsed = time.perf_counter() - t0
+    return {"value": round(done / elapsed / 1e12, 6), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port", "sample": f"{tokens} query tokens of one row (longest reach first) as torch CPU code, "
+                                      f"fp32 ({elapsed:.1f} s, {torch.get_num_threads()} threads)"}
+
+
+def cpu_oracle_context(inp, seconds: float) -> dict:
     """The oracle's causal attention on the host, on query tokens of the first row taken from its
     end (the longest reach), for about ``seconds``; algorithmic flops done per second."""
     from oracle import ops as oops
@@ -612,7 +870,7 @@ def cpu_baseline_context(inp, seconds: float) -> dict:
             "sample": f"{tokens} query tokens of one row (longest reach first), single-threaded numpy ({elapsed:.1f} s)"}
 
 
-def cpu_baseline_attention(inp, seconds: float) -> dict:
+def cpu_oracle_attention(inp, seconds: float) -> dict:
     """The oracle's decode attention on the host, one row at a time over the workload's rows (cycling),
     for about ``seconds``; credited bytes of the rows done per second."""
     from oracle import ops as oops
@@ -721,13 +979,16 @@ def main() -> int:
         line["roofline"]["skeleton"] = {"us": dom["skeleton_us"], "GB/s": round(sk_gbs, 1),
                                         "frac": round(sk_gbs / PEAK_HBM_GBS, 4)}
         line["roofline"]["frac_of_skeleton"] = dom["of_skeleton"]
-    for key in ("separate_us_per_layer", "fused_us_per_layer", "stream_us_per_step"):
+    for key in ("separate_us_per_layer", "fused_us_per_layer", "stream_us_per_step", "graph_us_per_step",
+                "host_us_per_step"):
         if key in res:
             line[key] = round(res[key], 3)
+    if res.get("step_inputs"):
+        line["step_inputs"] = res["step_inputs"]
     line["copy_ceiling_GBps"] = round(copy_ceiling_gbs(dev), 1)
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline_layer(shape, args.cpu_seconds, args.fp8)
-        line["cpu_torch"] = cpu_torch_layer(shape, args.cpu_seconds / 2, args.fp8)
+        line["cpu_baseline"] = cpu_torch_layer(shape, args.cpu_seconds, args.fp8)
+        line["cpu_oracle"] = cpu_oracle_layer(shape, args.cpu_seconds / 2, args.fp8)
     print(json.dumps(line), flush=True)
     return 0
 
@@ -762,6 +1023,7 @@ def attention_main(mas, args, shape, dev) -> int:
                    "kv_heads": shape.kv_heads, "head_dim": shape.head_dim, "page_size": shape.page_size,
                    "max_len": shape.max_len, **res["attention"], "launch": "hip-graph"},
         "us_per_call": round(res["ms_per_step"] * 1e3, 3),
+        "graph_us_per_call": round(res["graph_us_per_step"], 3), "host_us_per_call": round(res["host_us_per_step"], 3),
         "frac_of_peak": round(res["value"] / PEAK_HBM_GBS, 4),
         "ops": res["ops"],
         "roofline": {"bound": "hbm", "kernel": res["dominant"], "achieved": round(dom_gbs, 1), "peak": PEAK_HBM_GBS,
@@ -771,7 +1033,8 @@ def attention_main(mas, args, shape, dev) -> int:
         "copy_ceiling_GBps": round(copy_ceiling_gbs(dev), 1),
     }
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline_attention(res["inputs"], args.cpu_seconds)
+        line["cpu_baseline"] = cpu_torch_attention(res["inputs"], args.cpu_seconds)
+        line["cpu_oracle"] = cpu_oracle_attention(res["inputs"], args.cpu_seconds / 2)
     print(json.dumps(line), flush=True)
     return 0
 

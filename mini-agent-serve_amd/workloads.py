@@ -59,6 +59,10 @@ SHAPES: dict[str, Shape] = {s.name: s for s in [
     # 40-layer decode pass over 256 sequences (GEMM and attention outputs replaced by N(0,1));
     # 512 pages x 256 slots per layer, each sequence's current page distinct
     Shape("decode_pass_256x40", 256, 5120, 32768, 32, 8, 128, 512, 256, 256, True, layers=40),
+    # the same decode and prefill layers on the reference engine's default 16-slot pages
+    # (miniagentserve/engine/serving_engine.py:24), pools of the same capacity
+    Shape("decode64_24b_p16", 64, 5120, 32768, 32, 8, 128, 32768, 16, 64, True),
+    Shape("prefill8192_24b_p16", 8192, 5120, 32768, 32, 8, 128, 65536, 16, 4, False),
 ]}
 
 
@@ -214,6 +218,8 @@ ATTENTION_SHAPES: dict[str, AttentionShape] = {s.name: s for s in [
     AttentionShape("decode_attn_64x8192_24b", 64, 32, 8, 128, 256, 8192),
     # Devstral-2 123B: 12 query heads per kv head
     AttentionShape("decode_attn_64x8192_123b", 64, 96, 8, 128, 256, 8192),
+    # the reference engine's default 16-slot pages (serving_engine.py:24)
+    AttentionShape("decode_attn_64x8192_24b_p16", 64, 32, 8, 128, 16, 8192),
 ]}
 
 
@@ -286,6 +292,8 @@ CONTEXT_SHAPES: dict[str, ContextShape] = {s.name: s for s in [
     ContextShape("context_attn_4x2048_24b", 4, 2048, 0, 32, 8, 128, 256),
     # the prefill-16384 step's attention: 4 prompts of 4096 tokens, Devstral-2 123B heads
     ContextShape("context_attn_4x4096_123b", 4, 4096, 0, 96, 8, 128, 256),
+    # the reference engine's default 16-slot pages (serving_engine.py:24)
+    ContextShape("context_attn_4x2048_24b_p16", 4, 2048, 0, 32, 8, 128, 16),
 ]}
 
 
