@@ -71,34 +71,17 @@ __device__ __forceinline__ int kv_len(const DecodeArgs& a, int b) {
   return static_cast<int>(L < 0 ? 0 : (L > cap ? cap : L));
 }
 
-// Key loads: a wavefront's load instruction reads 64 bytes of each of 16 key rows, so the other
-// half of each 128-byte line comes with the next instruction; value loads read whole rows.
-#ifndef MAS_ATTN_K_NT
-#define MAS_ATTN_K_NT 0
-#endif
-#ifndef MAS_ATTN_V_NT
-#define MAS_ATTN_V_NT 1
-#endif
-__device__ __forceinline__ u32x4 attn_load_k(const uint16_t* p) {
-  if constexpr (MAS_ATTN_K_NT) return load_stream(p);
-  return load_cached(p);
-}
-__device__ __forceinline__ u32x4 attn_load_v(const uint16_t* p) {
-  if constexpr (MAS_ATTN_V_NT) return load_stream(p);
-  return load_cached(p);
-}
+// Key loads go through the cache hierarchy: a wavefront's load instruction reads 64 bytes of each
+// of 16 key rows, so the other half of each 128-byte line comes with the next instruction. Value
+// loads read whole rows and bypass it (non-temporal).
+__device__ __forceinline__ u32x4 attn_load_k(const uint16_t* p) { return load_cached(p); }
+__device__ __forceinline__ u32x4 attn_load_v(const uint16_t* p) { return load_stream(p); }
 
-// Wavefronts per workgroup of the split kernel: consecutive kv heads of one split, so one CU reads
-// whole 2 KB position blocks ([kv head][head dim]) together. Each wavefront works on its own; LDS
-// traffic is ordered within the wavefront only.
-#ifndef MAS_ATTN_WG_WAVES
-#define MAS_ATTN_WG_WAVES 1
-#endif
-constexpr int kAttnWaves = MAS_ATTN_WG_WAVES;
+// One wavefront per workgroup of the split kernel (kv heads of one position block in consecutive
+// workgroups); LDS traffic is ordered within the wavefront only.
+constexpr int kAttnWaves = 1;
 // Wavefronts per SIMD the split kernel's registers are capped for (two load buffers of a step each).
-#ifndef MAS_ATTN_MIN_WAVES
-#define MAS_ATTN_MIN_WAVES 2
-#endif
+constexpr int kAttnMinWaves = 2;
 
 // Orders this wavefront's LDS writes before its later reads (and reads before later writes).
 __device__ __forceinline__ void wave_lds_sync() {
@@ -182,7 +165,7 @@ __device__ __forceinline__ void issue_step(const DecodeArgs& a, StepLoads<D>& st
 // tile, so it keeps ~16 significant bits (one bf16 term alone rounds it to 8). O stays in
 // 4 * D / 16 accumulator registers whatever the group size.
 template <int GP, int D, bool kBig>
-__global__ __launch_bounds__(64 * kAttnWaves, D <= 128 ? MAS_ATTN_MIN_WAVES : 1) void decode_attn_split(DecodeArgs a) {
+__global__ __launch_bounds__(64 * kAttnWaves, D <= 128 ? kAttnMinWaves : 1) void decode_attn_split(DecodeArgs a) {
   constexpr int KS = D / 32;
   constexpr int DT = D / 16;               // MFMA tiles over the head dim for P.V
   constexpr int LPP = D / 8;               // value-row layout: lanes per row
@@ -598,11 +581,8 @@ extern "C" int mas_paged_decode_attention_bf16(void* out, int64_t out_stride, in
   // 128 splits of 256 positions: 804 us per call, with 4 chunks per split 738 us; 8 rows x 8 kv
   // heads x 128 splits: 124 us, with 2 chunks per split 117 us).
   const int64_t chunks = cdiv(cap, kChunk);
-#ifndef MAS_ATTN_MIN_CHUNKS
-#define MAS_ATTN_MIN_CHUNKS 1
-#endif
   constexpr int64_t kMaxSplitItems = 16384, kMaxRowSplits = 64;
-  int64_t per_split = MAS_ATTN_MIN_CHUNKS;
+  int64_t per_split = 1;
   while (per_split < chunks &&
          (mas_paged_decode_attention_workspace_bytes(batch, num_q_heads, head_dim, max_blocks, page_size, per_split) >
               workspace_bytes ||

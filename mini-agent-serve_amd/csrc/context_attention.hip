@@ -59,9 +59,6 @@ struct ContextArgs {
 // heads per workgroup: half the staging per flop) measured ~2% faster with 12 query heads per kv
 // head (123B, 4 x 4096 tokens) and ~4% slower with 4 (24B, 4 x 2048: the grid halves), in
 // alternating runs on one box; the launch picks 8 when a kv head has at least 8 query heads.
-#ifndef MAS_CTX_PIPELINE
-#define MAS_CTX_PIPELINE 1
-#endif
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -81,9 +78,9 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   constexpr int VROW = D + 16;          // bf16 per LDS value row (+32 B: conflict-free column reads)
   constexpr int CPR = D / 8;            // 16-byte chunks per key / value row
   constexpr int LOADS = kTileP * CPR / kCtxThreads;  // 16-byte chunks per thread per tile, each of K and V
-  // kBufs tile buffers: with the software pipeline, the next tile's keys are read while this
-  // tile's values are.
-  constexpr int kBufs = MAS_CTX_PIPELINE ? 2 : 1;
+  // Two tile buffers: with the software pipeline, the next tile's keys are read while this tile's
+  // values are.
+  constexpr int kBufs = 2;
   __shared__ __align__(16) uint16_t k_lds_all[kBufs][kTileP * KROW];
   __shared__ __align__(16) uint16_t v_lds_all[kBufs][kTileP * VROW];
 
@@ -95,10 +92,7 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   const int q0 = a.cu_seqlens_q[row], q_len = a.cu_seqlens_q[row + 1] - q0;
   const int tokens_per_wg = kRowsPerWave * (kCtxWaves / a.heads_per_wg);
   // Token tiles in reverse launch order: the last tiles reach the most positions, so they start first.
-#ifndef MAS_CTX_REVERSE
-#define MAS_CTX_REVERSE 1
-#endif
-  const int tile_idx = MAS_CTX_REVERSE ? static_cast<int>(gridDim.y - 1 - blockIdx.y) : static_cast<int>(blockIdx.y);
+  const int tile_idx = static_cast<int>(gridDim.y - 1 - blockIdx.y);
   const int tile_tok = tile_idx * tokens_per_wg;
   if (tile_tok >= q_len) return;  // uniform over the workgroup
   // kv_len clamped to the block table's reach; a kv_len below q_len leaves the first tokens with
@@ -307,7 +301,6 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   };
 
   TileRegs tr;
-#if MAS_CTX_PIPELINE
   // Software pipeline over tiles: tile it + 1's scores (MFMA, keys from the other LDS buffer) are
   // computed in the same block as tile it's softmax (VALU), so the two overlap; then tile it's P.V.
   // Buffer it & 1 holds tile it, buffer (it + 1) & 1 tile it + 1 (staged after the barrier that
@@ -343,25 +336,6 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
     step(it + 1, s_b, s_a);
   }
   if (it < ntiles) step(it, s_a, s_b);
-#else
-  // The next tile's loads are in flight during this tile's arithmetic. (A second register buffer,
-  // two tiles ahead, measured no faster and costs 32 VGPRs.)
-  if (ntiles > 0) issue_tile(tr, 0);
-  for (int it = 0; it < ntiles; ++it) {
-    __syncthreads();  // the previous tile's LDS reads are done
-    stage(tr, 0);
-    __syncthreads();
-    if (it + 1 < ntiles) issue_tile(tr, (it + 1) * kTileP);
-    if (wave_live) {
-      f32x16 s[2];
-      bf16x8 pbo[4];
-      scores(0, s);
-      mask(s, it * kTileP);
-      rescale(softmax(s, pbo));
-      pv(0, pbo);
-    }
-  }
-#endif
   if (__builtin_amdgcn_ballot_w64(page_bad) != 0 && lane == 0) report(a.err, MAS_ERRBIT_PAGE);
   if (len_bad && tid == 0 && blockIdx.x == 0 && blockIdx.y == 0) report(a.err, MAS_ERRBIT_POSITION);
 

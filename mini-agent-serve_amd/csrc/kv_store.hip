@@ -20,14 +20,9 @@ namespace {
 
 // One wavefront per workgroup and per (token, tensor): measured best on MI355X at every size, from
 // the 64-token decode (2.17 us) to 16384 prefill tokens (ahead of 128/256/512-thread workgroups and
-// of one wavefront moving both of a token's rows). Both are overridable for experiments.
-#ifndef MAS_KV_BLOCK
-#define MAS_KV_BLOCK 64
-#endif
-#ifndef MAS_KV_SPLIT
-#define MAS_KV_SPLIT 2
-#endif
-constexpr int kBlock = MAS_KV_BLOCK;
+// of one wavefront moving both of a token's rows).
+constexpr int kBlock = 64;
+constexpr int kSplit = 2;  // wavefronts per token: one for k, one for v
 constexpr int kWavesPerBlock = kBlock / kWave;
 constexpr int kUnroll = 2;
 
@@ -174,7 +169,6 @@ int check_common(const KvArgs& a, int64_t num_heads, int64_t head_dim, bool* emp
 // q/k/v column views) are one contiguous run at both ends: no per-vector head arithmetic.
 template <bool kSlotForm>
 int launch(const KvArgs& a, hipStream_t s) {
-  constexpr int kSplit = MAS_KV_SPLIT;
   const int64_t head_dim = 8 * static_cast<int64_t>(a.vec_per_head);
   const bool contiguous = a.key_head_stride == head_dim && a.value_head_stride == head_dim && a.head_stride == head_dim;
   const int64_t blocks = cdiv(a.rows * kSplit, kWavesPerBlock);

@@ -160,25 +160,14 @@ __global__ __launch_bounds__(256) void fused_add_rmsnorm_generic(NormArgs a) {
 
 constexpr int kVpts[] = {1, 2, 3, 4, 5, 6, 8};
 
-// Tuning overrides for experiments (0 = use the heuristic below).
-#ifndef MAS_NORM_FORCE_VPT
-#define MAS_NORM_FORCE_VPT 0
-#endif
-#ifndef MAS_NORM_BLOCKS_PER_CU
-#define MAS_NORM_BLOCKS_PER_CU 0
-#endif
-
 // Picks the register tile: VPT vectors per lane and a multiple of 64 lanes covering the row, with
 // at most 12.5% padding. The most lanes per row wins, at every row count: measured on MI355X,
 // 640 lanes beat 320 and 128 for hidden 5120, and 768 beat 512, 384 and 256 for hidden 12288
 // (more waves in flight per CU, fewer registers per lane).
-bool choose_tile(int64_t nvec, int64_t rows, int cus, int* vpt, int* threads) {
-  (void)rows;
-  (void)cus;
+bool choose_tile(int64_t nvec, int* vpt, int* threads) {
   int best_v = 0, best_t = 0;
   int64_t best_score = INT64_MAX;
   for (int v : kVpts) {
-    if (MAS_NORM_FORCE_VPT != 0 && v != MAS_NORM_FORCE_VPT) continue;
     const int64_t t = cdiv(cdiv(nvec, v), kWave) * kWave;
     if (t > max_threads_for(v)) continue;
     const int64_t waste = t * v - nvec;
@@ -226,8 +215,6 @@ int run_norm(const NormArgs& a, int out_elem_bytes, hipStream_t stream) {
   if (a.rows > 1 && (a.in_stride < a.hidden || a.res_stride < a.hidden || a.out_stride < a.hidden))
     return MAS_ERR_INVALID_VALUE;
   if (!(a.eps >= 0.f)) return MAS_ERR_INVALID_VALUE;
-  int cus = 0;
-  if (const int st = device_cu_count(&cus); st != MAS_OK) return st;
 
   const int64_t nvec = a.hidden / 8;
   // 16-byte rows: hidden % 8 == 0, every base pointer and row stride keeps 16-byte alignment
@@ -236,10 +223,8 @@ int run_norm(const NormArgs& a, int out_elem_bytes, hipStream_t stream) {
                       (reinterpret_cast<uintptr_t>(a.out) % (8 * out_elem_bytes) == 0) && (a.in_stride % 8 == 0) &&
                       (a.res_stride % 8 == 0) && (a.out_stride % 8 == 0);
   int vpt = 0, threads = 0;
-  int64_t grid = a.rows < INT32_MAX ? a.rows : INT32_MAX;
-  if (MAS_NORM_BLOCKS_PER_CU > 0 && grid > static_cast<int64_t>(MAS_NORM_BLOCKS_PER_CU) * cus)
-    grid = static_cast<int64_t>(MAS_NORM_BLOCKS_PER_CU) * cus;
-  if (vec_ok && choose_tile(nvec, a.rows, cus, &vpt, &threads)) {
+  const int64_t grid = a.rows < INT32_MAX ? a.rows : INT32_MAX;
+  if (vec_ok && choose_tile(nvec, &vpt, &threads)) {
     return launch_tile<kFp8>(vpt, dim3(static_cast<uint32_t>(grid)), dim3(threads), stream, a);
   }
   hipLaunchKernelGGL((fused_add_rmsnorm_generic<kFp8>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0, stream,

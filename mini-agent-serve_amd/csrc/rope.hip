@@ -18,10 +18,7 @@
 namespace mas {
 namespace {
 
-#ifndef MAS_ROPE_BLOCK
-#define MAS_ROPE_BLOCK 256
-#endif
-constexpr int kBlock = MAS_ROPE_BLOCK;  // threads per workgroup (64..512 measured equal on MI355X)
+constexpr int kBlock = 256;  // threads per workgroup (64..512 measured equal on MI355X)
 constexpr int kWavesPerBlock = kBlock / kWave;
 
 struct RopeArgs {
@@ -139,15 +136,6 @@ template <int LPH, bool kNeox, bool kPos64>
 int pick_passes(RopeArgs a, int cus, hipStream_t s) {
   constexpr int kHeadsPerPass = kWave / LPH;
   const int64_t passes = cdiv(a.num_heads, kHeadsPerPass);
-#if defined(MAS_ROPE_FORCE_PASSES) && MAS_ROPE_FORCE_PASSES > 0
-  switch (MAS_ROPE_FORCE_PASSES) {
-    case 1: return launch_rope<LPH, kNeox, kPos64, 1>(a, s);
-    case 2: return launch_rope<LPH, kNeox, kPos64, 2>(a, s);
-    case 3: return launch_rope<LPH, kNeox, kPos64, 3>(a, s);
-    case 4: return launch_rope<LPH, kNeox, kPos64, 4>(a, s);
-    default: return launch_rope<LPH, kNeox, kPos64, 5>(a, s);
-  }
-#endif
   if (a.rows * passes < static_cast<int64_t>(cus) * 16) return launch_rope<LPH, kNeox, kPos64, 1>(a, s);
   return launch_rope<LPH, kNeox, kPos64, 2>(a, s);
 }

@@ -28,11 +28,8 @@ namespace mas {
 namespace {
 
 // One wavefront per workgroup and one pass (64 / LPH heads) per wavefront: measured best on MI355X
-// at decode (3.09 us for 64 tokens) and on par or better at prefill. Overridable for experiments.
-#ifndef MAS_FUSED_BLOCK
-#define MAS_FUSED_BLOCK 64
-#endif
-constexpr int kBlock = MAS_FUSED_BLOCK;
+// at decode (3.09 us for 64 tokens) and on par or better at prefill (2 and 3 passes, 128-512 threads).
+constexpr int kBlock = 64;
 constexpr int kWavesPerBlock = kBlock / kWave;
 
 struct FusedArgs {
@@ -235,19 +232,9 @@ int launch(FusedArgs a, hipStream_t s) {
   return launch_status();
 }
 
-template <int LPH, bool kNeox>
-int pick(const FusedArgs& a, int cus, hipStream_t s) {
-  (void)cus;
-#if defined(MAS_FUSED_FORCE_PASSES) && MAS_FUSED_FORCE_PASSES > 1
-  if (MAS_FUSED_FORCE_PASSES == 3) return launch<LPH, kNeox, 3>(a, s);
-  return launch<LPH, kNeox, 2>(a, s);
-#endif
-  return launch<LPH, kNeox, 1>(a, s);
-}
-
 template <int LPH>
-int dispatch(const FusedArgs& a, bool neox, int cus, hipStream_t s) {
-  return neox ? pick<LPH, true>(a, cus, s) : pick<LPH, false>(a, cus, s);
+int dispatch(const FusedArgs& a, bool neox, hipStream_t s) {
+  return neox ? launch<LPH, true, 1>(a, s) : launch<LPH, false, 1>(a, s);
 }
 
 }  // namespace
@@ -286,8 +273,6 @@ extern "C" int mas_rope_append_paged_kv_cache_bf16(
   if (!q_ok || !kv_ok || !aligned16(table) || table_stride % 4 != 0 ||
       (reinterpret_cast<uintptr_t>(q_scale_table) & 1u) != 0)
     return MAS_ERR_MISALIGNED;
-  int cus = 0;
-  if (const int st = device_cu_count(&cus); st != MAS_OK) return st;
   FusedArgs a{static_cast<uint16_t*>(q), q_stride, q_head_stride, static_cast<uint16_t*>(k), k_stride, k_head_stride,
               static_cast<const uint16_t*>(v), v_stride, v_head_stride, positions, batch_indices, table, table_stride,
               table_rows, static_cast<const uint16_t*>(q_scale_table), q_scale_rows, q_scale_interval, static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), page_stride, entry_stride,
@@ -295,11 +280,11 @@ extern "C" int mas_rope_append_paged_kv_cache_bf16(
               static_cast<int>(num_q_heads), static_cast<int>(num_kv_heads), 0, err};
   const bool neox = is_neox != 0;
   switch (head_dim) {
-    case 32: return dispatch<2>(a, neox, cus, stream);
-    case 64: return dispatch<4>(a, neox, cus, stream);
-    case 128: return dispatch<8>(a, neox, cus, stream);
-    case 256: return dispatch<16>(a, neox, cus, stream);
-    case 512: return dispatch<32>(a, neox, cus, stream);
+    case 32: return dispatch<2>(a, neox, stream);
+    case 64: return dispatch<4>(a, neox, stream);
+    case 128: return dispatch<8>(a, neox, stream);
+    case 256: return dispatch<16>(a, neox, stream);
+    case 512: return dispatch<32>(a, neox, stream);
     default: return MAS_ERR_UNSUPPORTED;
   }
 }

@@ -134,12 +134,12 @@ dim3 row_tile_grid(int64_t tiles_per_row, int64_t rows) {
   return dim3(static_cast<uint32_t>(tiles_per_row), static_cast<uint32_t>(rows < 65535 ? rows : 65535));
 }
 
-template <int UNROLL>
+// One vector per lane and a grid covering every vector once: measured best on MI355X at every size
+// from the 64-token decode to 16384 x 28672 (more waves in flight beat 2 and 4 vectors per lane).
 int launch_vec(void* out, int64_t out_stride, const void* in, int64_t in_stride, int64_t rows, int64_t inter,
-               int cus, hipStream_t s) {
-  (void)cus;
-  hipLaunchKernelGGL((silu_and_mul_vec<UNROLL>), row_tile_grid(cdiv(inter / 8, kBlock * UNROLL), rows), dim3(kBlock),
-                     0, s, out, out_stride, in, in_stride, rows, inter);
+               hipStream_t s) {
+  hipLaunchKernelGGL((silu_and_mul_vec<1>), row_tile_grid(cdiv(inter / 8, kBlock), rows), dim3(kBlock), 0, s, out,
+                     out_stride, in, in_stride, rows, inter);
   return launch_status();
 }
 
@@ -165,18 +165,7 @@ extern "C" int mas_silu_and_mul_bf16(void* out, int64_t out_stride, const void* 
                        out_stride, input, input_stride, rows, inter);
     return launch_status();
   }
-  // Enough tiles to keep every CU busy with several workgroups: 4 vectors per lane; otherwise
-  // spread the work over more, smaller tiles.
-  const int64_t vectors = rows * (inter / 8);
-#if defined(MAS_SILU_FORCE_UNROLL) && MAS_SILU_FORCE_UNROLL > 0
-  if (MAS_SILU_FORCE_UNROLL == 1) return launch_vec<1>(out, out_stride, input, input_stride, rows, inter, cus, stream);
-  if (MAS_SILU_FORCE_UNROLL == 2) return launch_vec<2>(out, out_stride, input, input_stride, rows, inter, cus, stream);
-  return launch_vec<4>(out, out_stride, input, input_stride, rows, inter, cus, stream);
-#endif
-  // One vector per lane and a grid covering every vector once: measured best on MI355X at every
-  // size from the 64-token decode to 16384 x 28672 (more waves in flight beat deeper unrolling).
-  (void)vectors;
-  return launch_vec<1>(out, out_stride, input, input_stride, rows, inter, cus, stream);
+  return launch_vec(out, out_stride, input, input_stride, rows, inter, stream);
 }
 
 extern "C" int mas_silu_and_mul_quant_fp8(void* out, int64_t out_stride, const void* input, int64_t input_stride,
