@@ -42,6 +42,8 @@ extern "C" {
 #define MAS_ERR_UNSUPPORTED (-2)   /* a shape this library does not implement             */
 #define MAS_ERR_MISALIGNED (-3)    /* a pointer or stride breaks the kernel's alignment   */
 #define MAS_ERR_DEVICE (-4)        /* hipGetDevice / device-attribute query failed        */
+#define MAS_ERR_SCRATCH (-5)       /* the call needs more scratch than the no-allocation
+                                      entry point's static buffer holds                    */
 
 #define MAS_ERRBIT_TOKEN_ID 1u  /* embedding: id < 0 or id >= vocab                       */
 #define MAS_ERRBIT_POSITION 2u  /* rope: position < 0 or >= table rows; kv: position < 0;
@@ -273,6 +275,33 @@ int mas_paged_context_attention_bf16(void* out, int64_t out_stride, int64_t out_
                                      int64_t head_dim, float bmm1_scale, float bmm2_scale, int out_fp8,
                                      const float* out_scale_dev, float out_scale_host, uint32_t* err,
                                      hipStream_t stream);
+
+/*
+ * mas_paged_decode_attention_bf16 without a workspace argument: the same kernels and results, with
+ * the split partials in a scratch array the library keeps in device memory, one per GPU it runs on,
+ * MAS_DECODE_ATTENTION_SCRATCH_BYTES long, held until the process ends. No allocation happens in the
+ * call: the array's address is looked up once per device, on the first call there (the caller's
+ * current device is left as it was). Splits are made as long as needed for the partials to fit the
+ * array; a call that does not fit even with one split per row (batch * num_q_heads * (head_dim + 2)
+ * * 4 bytes over the limit) returns MAS_ERR_SCRATCH and enqueues nothing. Every call on one GPU
+ * uses that GPU's one array: calls that overlap in time on one GPU (on different streams) race and
+ * must be ordered by the caller; consecutive calls on one stream are safe. Nothing in the array
+ * needs clearing between calls.
+ * No counterpart in the reference (it always passes a workspace, devstral2.py:36-42,187): this is
+ * for callers that cannot allocate a workspace - code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation.
+ */
+#define MAS_DECODE_ATTENTION_SCRATCH_BYTES (64ll << 20)
+int mas_paged_decode_attention_bf16_noalloc(void* out, int64_t out_stride, int64_t out_head_stride, const void* q,
+                                            int64_t q_stride, int64_t q_head_stride, const void* k_cache,
+                                            const void* v_cache, int64_t page_stride, int64_t entry_stride,
+                                            int64_t head_stride, int64_t num_pages, int64_t page_size,
+                                            const int32_t* block_tables, int64_t block_table_stride,
+                                            int64_t max_blocks, const int32_t* seq_lens, int64_t batch,
+                                            int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                                            float bmm1_scale, float bmm2_scale, int out_fp8,
+                                            const float* out_scale_dev, float out_scale_host, uint32_t* err,
+                                            hipStream_t stream);
 
 /*
  * Workspace bytes mas_paged_decode_attention_bf16 needs when each split covers chunks_per_split

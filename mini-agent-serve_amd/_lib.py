@@ -48,6 +48,10 @@ _SIGNATURES: dict[str, list] = {
                                         _i64, _i64, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _i64,
                                         _i64, ctypes.c_float, ctypes.c_float, _i32, _c_void_p, ctypes.c_float,
                                         _c_void_p, _i64, _c_void_p, _c_void_p],
+    "mas_paged_decode_attention_bf16_noalloc": [_c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _c_void_p,
+                                                _i64, _i64, _i64, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64,
+                                                _i64, _i64, _i64, ctypes.c_float, ctypes.c_float, _i32, _c_void_p,
+                                                ctypes.c_float, _c_void_p, _c_void_p],
     "mas_paged_decode_attention_workspace_bytes": [_i64, _i64, _i64, _i64, _i64, _i64],
     "mas_paged_context_attention_bf16": [_c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64,
                                          _i64, _i64, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64,

@@ -185,7 +185,7 @@ def _(input_ids, last_tokens, error_flags):
 
 
 @custom_op("mas::paged_decode_attention", mutates_args=("workspace", "out", "error_flags"))
-def _paged_decode_attention(query: Tensor, k_cache: Tensor, v_cache: Optional[Tensor], workspace: Tensor,
+def _paged_decode_attention(query: Tensor, k_cache: Tensor, v_cache: Optional[Tensor], workspace: Optional[Tensor],
                             block_tables: Tensor,
                             seq_lens: Tensor, bmm1_scale: float, bmm2_scale: float, out: Tensor, kv_layout: str,
                             quant_scale: Optional[Tensor], quant_scale_host: float,

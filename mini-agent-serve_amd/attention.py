@@ -81,16 +81,17 @@ def decode_workspace_bytes(batch: int, num_q_heads: int, head_dim: int, max_bloc
 def _decode(query, kv_cache, workspace_buffer, block_tables, seq_lens, bmm1_scale, bmm2_scale, out, kv_layout,
             error_flags, quant_scale=None) -> None:
     k_cache, v_cache, pstride, estride, hstride, pages, page_size, hk, dim = _cache_geometry(kv_cache, kv_layout)
-    for name, t in (("query", query), ("out", out), ("block_tables", block_tables), ("seq_lens", seq_lens),
-                    ("workspace_buffer", workspace_buffer)):
+    for name, t in (("query", query), ("out", out), ("block_tables", block_tables), ("seq_lens", seq_lens)):
         require_gpu(t, name)
     require_dtype(query, "query", torch.bfloat16)
     require_dtype(out, "out", torch.bfloat16 if quant_scale is None else FP8)
     require_dtype(block_tables, "block_tables", torch.int32)
     require_dtype(seq_lens, "seq_lens", torch.int32)
     device = require_same_device(("query", query), ("k_cache", k_cache), ("out", out),
-                                 ("block_tables", block_tables), ("seq_lens", seq_lens),
-                                 ("workspace_buffer", workspace_buffer))
+                                 ("block_tables", block_tables), ("seq_lens", seq_lens))
+    if workspace_buffer is not None:
+        require_gpu(workspace_buffer, "workspace_buffer")
+        require_same_device(("query", query), ("workspace_buffer", workspace_buffer))
     out_fp8, scale_ptr, scale_host = _quant_args(quant_scale, device)
     if query.dim() != 3 or query.shape[2] != dim or (dim > 1 and query.stride(2) != 1):
         raise ValueError(f"query must be [batch, num_q_heads, {dim}] with a contiguous last dimension, "
@@ -113,13 +114,18 @@ def _decode(query, kv_cache, workspace_buffer, block_tables, seq_lens, bmm1_scal
             k_cache.data_ptr(), v_cache.data_ptr(), pstride, estride, hstride, pages, page_size, block_tables.data_ptr(),
             block_tables.stride(0), block_tables.shape[1], seq_lens.data_ptr(), batch, hq, hk, dim, float(bmm1_scale),
             float(bmm2_scale), out_fp8, scale_ptr, scale_host)
-    nbytes = workspace_buffer.numel() * workspace_buffer.element_size()
-    st = _lib.load().mas_paged_decode_attention_bf16(*args, workspace_buffer.data_ptr(), nbytes,
-                                                     error_word(error_flags, device), _lib.stream_handle(device))
+    if workspace_buffer is None:
+        # the library's own scratch: no allocation in the call (graph capture, allocation-free loops)
+        st = _lib.load().mas_paged_decode_attention_bf16_noalloc(*args, error_word(error_flags, device),
+                                                                 _lib.stream_handle(device))
+    else:
+        nbytes = workspace_buffer.numel() * workspace_buffer.element_size()
+        st = _lib.load().mas_paged_decode_attention_bf16(*args, workspace_buffer.data_ptr(), nbytes,
+                                                         error_word(error_flags, device), _lib.stream_handle(device))
     _lib.check(st, "trtllm_batch_decode_with_kv_cache")
 
 
-def trtllm_batch_decode_with_kv_cache(query: torch.Tensor, kv_cache, workspace_buffer: torch.Tensor,
+def trtllm_batch_decode_with_kv_cache(query: torch.Tensor, kv_cache, workspace_buffer: torch.Tensor | None,
                                       block_tables: torch.Tensor, seq_lens: torch.Tensor, max_seq_len: int,
                                       bmm1_scale: float = 1.0, bmm2_scale: float = 1.0, window_left: int = -1,
                                       out: torch.Tensor | None = None, out_dtype=None, o_sf_scale=None,
@@ -131,6 +137,9 @@ def trtllm_batch_decode_with_kv_cache(query: torch.Tensor, kv_cache, workspace_b
     not given), bf16 ``[batch, num_q_heads, head_dim]``, or its fp8 quantize with ``out_quant_scale``.
 
     ``kv_cache`` is ``(k_cache, v_cache)`` or one ``[pages, 2, ...]`` tensor, in ``kv_layout``.
+    ``workspace_buffer=None`` uses the library's own scratch instead (no allocation in the call;
+    at most ``MAS_DECODE_ATTENTION_SCRATCH_BYTES`` of partials, one buffer per GPU shared by every
+    such call, so such calls must not overlap on two streams of one GPU).
     ``max_seq_len`` is accepted and unused: the reach of ``block_tables`` bounds the positions.
     Not supported (raise): a sliding window, attention sinks, block-scaled outputs.
     ``enable_pdl`` is ignored. ``error_flags`` as for the other ops (page 8, seq_len 2).

@@ -20,6 +20,9 @@
 // Scores live in the log2 domain (bmm1_scale * log2 e folded in), so every exponential is one
 // v_exp_f32. A position whose page id is out of range is skipped (MAS_ERRBIT_PAGE); seq_lens past
 // the block table's reach is clamped to it (MAS_ERRBIT_POSITION); a row with no position gets zeros.
+#include <atomic>
+#include <mutex>
+
 #include "device.h"
 
 namespace mas {
@@ -542,17 +545,20 @@ extern "C" int64_t mas_paged_decode_attention_workspace_bytes(int64_t batch, int
   return batch * num_q_heads * (splits > 0 ? splits : 1) * (head_dim + 2) * 4;
 }
 
-extern "C" int mas_paged_decode_attention_bf16(void* out, int64_t out_stride, int64_t out_head_stride, const void* q,
-                                               int64_t q_stride, int64_t q_head_stride, const void* k_cache,
-                                               const void* v_cache, int64_t page_stride, int64_t entry_stride,
-                                               int64_t head_stride, int64_t num_pages, int64_t page_size,
-                                               const int32_t* block_tables, int64_t block_table_stride,
-                                               int64_t max_blocks, const int32_t* seq_lens, int64_t batch,
-                                               int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
-                                               float bmm1_scale, float bmm2_scale, int out_fp8,
-                                               const float* out_scale_dev, float out_scale_host, void* workspace,
-                                               int64_t workspace_bytes, uint32_t* err, hipStream_t stream) {
-  using namespace mas;
+namespace mas {
+namespace {
+
+// Returned by decode_attention when even one split per row does not fit the workspace.
+constexpr int kWorkspaceTooSmall = -1000;
+
+int decode_attention(void* out, int64_t out_stride, int64_t out_head_stride, const void* q, int64_t q_stride,
+                     int64_t q_head_stride, const void* k_cache, const void* v_cache, int64_t page_stride,
+                     int64_t entry_stride, int64_t head_stride, int64_t num_pages, int64_t page_size,
+                     const int32_t* block_tables, int64_t block_table_stride, int64_t max_blocks,
+                     const int32_t* seq_lens, int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                     int64_t head_dim, float bmm1_scale, float bmm2_scale, int out_fp8, const float* out_scale_dev,
+                     float out_scale_host, void* workspace, int64_t workspace_bytes, uint32_t* err,
+                     hipStream_t stream) {
   if (batch < 0 || num_q_heads < 0 || num_kv_heads < 0 || num_pages < 0 || page_size <= 0 || max_blocks < 0 ||
       workspace_bytes < 0)
     return MAS_ERR_INVALID_VALUE;
@@ -589,10 +595,10 @@ extern "C" int mas_paged_decode_attention_bf16(void* out, int64_t out_stride, in
           cdiv(chunks, per_split) > kMaxRowSplits || batch * num_kv_heads * cdiv(chunks, per_split) > kMaxSplitItems))
     per_split *= 2;
   if (per_split > chunks) per_split = chunks > 0 ? chunks : 1;
+  if (workspace == nullptr) return MAS_ERR_INVALID_VALUE;
   if (mas_paged_decode_attention_workspace_bytes(batch, num_q_heads, head_dim, max_blocks, page_size, per_split) >
-          workspace_bytes ||
-      workspace == nullptr)
-    return MAS_ERR_INVALID_VALUE;
+      workspace_bytes)
+    return kWorkspaceTooSmall;
   const int64_t splits = chunks > 0 ? cdiv(chunks, per_split) : 1;
 
   int log2_page = 0;
@@ -633,4 +639,75 @@ extern "C" int mas_paged_decode_attention_bf16(void* out, int64_t out_stride, in
     case 128: return dispatch_group<128>(a, batch, num_kv_heads, stream);
     default: return dispatch_group<256>(a, batch, num_kv_heads, stream);
   }
+}
+
+// Scratch of the no-allocation entry point: the split partials in the library's own device memory,
+// one copy per GPU the library runs on, kept until the process ends. Host code uses the address
+// hipGetSymbolAddress returns for the current device (the array's name is a host-side stand-in).
+constexpr int64_t kScratchBytes = MAS_DECODE_ATTENTION_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mutex;
+
+// The scratch array's address on the stream's device, looked up once per device with that device
+// current (and the caller's current device restored).
+int scratch_address(hipStream_t stream, void** ptr) {
+  int dev = 0;
+  if (hipStreamGetDevice(stream, &dev) != hipSuccess) return MAS_ERR_DEVICE;
+  if (dev < 0 || dev >= kMaxDevices) return MAS_ERR_UNSUPPORTED;
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      int current = 0;
+      if (hipGetDevice(&current) != hipSuccess) return MAS_ERR_DEVICE;
+      if (current != dev && hipSetDevice(dev) != hipSuccess) return MAS_ERR_DEVICE;
+      const hipError_t st = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (current != dev && hipSetDevice(current) != hipSuccess) return MAS_ERR_DEVICE;
+      if (st != hipSuccess || p == nullptr) return MAS_ERR_DEVICE;
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *ptr = p;
+  return MAS_OK;
+}
+
+}  // namespace
+}  // namespace mas
+
+extern "C" int mas_paged_decode_attention_bf16(void* out, int64_t out_stride, int64_t out_head_stride, const void* q,
+                                               int64_t q_stride, int64_t q_head_stride, const void* k_cache,
+                                               const void* v_cache, int64_t page_stride, int64_t entry_stride,
+                                               int64_t head_stride, int64_t num_pages, int64_t page_size,
+                                               const int32_t* block_tables, int64_t block_table_stride,
+                                               int64_t max_blocks, const int32_t* seq_lens, int64_t batch,
+                                               int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                                               float bmm1_scale, float bmm2_scale, int out_fp8,
+                                               const float* out_scale_dev, float out_scale_host, void* workspace,
+                                               int64_t workspace_bytes, uint32_t* err, hipStream_t stream) {
+  const int st = mas::decode_attention(out, out_stride, out_head_stride, q, q_stride, q_head_stride, k_cache, v_cache,
+                                       page_stride, entry_stride, head_stride, num_pages, page_size, block_tables,
+                                       block_table_stride, max_blocks, seq_lens, batch, num_q_heads, num_kv_heads,
+                                       head_dim, bmm1_scale, bmm2_scale, out_fp8, out_scale_dev, out_scale_host,
+                                       workspace, workspace_bytes, err, stream);
+  return st == mas::kWorkspaceTooSmall ? MAS_ERR_INVALID_VALUE : st;
+}
+
+extern "C" int mas_paged_decode_attention_bf16_noalloc(
+    void* out, int64_t out_stride, int64_t out_head_stride, const void* q, int64_t q_stride, int64_t q_head_stride,
+    const void* k_cache, const void* v_cache, int64_t page_stride, int64_t entry_stride, int64_t head_stride,
+    int64_t num_pages, int64_t page_size, const int32_t* block_tables, int64_t block_table_stride,
+    int64_t max_blocks, const int32_t* seq_lens, int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+    int64_t head_dim, float bmm1_scale, float bmm2_scale, int out_fp8, const float* out_scale_dev,
+    float out_scale_host, uint32_t* err, hipStream_t stream) {
+  void* ws = nullptr;
+  if (const int st = mas::scratch_address(stream, &ws); st != MAS_OK) return st;
+  const int st = mas::decode_attention(out, out_stride, out_head_stride, q, q_stride, q_head_stride, k_cache, v_cache,
+                                       page_stride, entry_stride, head_stride, num_pages, page_size, block_tables,
+                                       block_table_stride, max_blocks, seq_lens, batch, num_q_heads, num_kv_heads,
+                                       head_dim, bmm1_scale, bmm2_scale, out_fp8, out_scale_dev, out_scale_host, ws,
+                                       mas::kScratchBytes, err, stream);
+  return st == mas::kWorkspaceTooSmall ? MAS_ERR_SCRATCH : st;
 }

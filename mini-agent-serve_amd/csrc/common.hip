@@ -34,6 +34,7 @@ extern "C" const char* mas_status_string(int status) {
     case MAS_ERR_UNSUPPORTED: return "unsupported shape";
     case MAS_ERR_MISALIGNED: return "pointer or stride breaks the kernel's 16-byte alignment";
     case MAS_ERR_DEVICE: return "device query failed";
+    case MAS_ERR_SCRATCH: return "the call needs more scratch than the no-allocation entry point holds";
     default: break;
   }
   if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));
