@@ -3,10 +3,11 @@
 // Semantics: nn.Embedding.forward at miniagentserve/models/devstral2/devstral2.py:260,282 (ids are
 // int64, miniagentserve/engine/model_runner.py:45). A bit copy of one table row per token.
 //
-// Grid: x = groups of 4 tokens (one wavefront each), y = chunks of 64 * kUnroll 16-byte vectors
-// of the row, so short batches still spread over many CUs. The id is wave-uniform and read
-// through the scalar cache; an id outside [0, vocab) zero-fills its row and sets
-// MAS_ERRBIT_TOKEN_ID (torch raises on such an id; the table is never read out of bounds).
+// Grid: x = token, y = chunks of 64 * kVpl 16-byte vectors of the row; one wavefront per
+// workgroup, so a 64-token decode step spreads over 640 wavefronts (hidden 5120), as many as a plain
+// copy of the same bytes. The id is wave-uniform and read through the scalar cache; an id outside
+// [0, vocab) zero-fills its row and sets MAS_ERRBIT_TOKEN_ID (torch raises on such an id; the table
+// is never read out of bounds).
 //
 // Placeholder form (the step-input path at miniagentserve/engine/model_runner.py:149-154 fused with
 // the gather): an id -1 - r stands for row r of the previous step's samples (int32, still on the
@@ -20,10 +21,8 @@
 namespace mas {
 namespace {
 
-constexpr int kBlock = 256;
-constexpr int kWavesPerBlock = kBlock / kWave;
-constexpr int kUnroll = 8;
-constexpr int kChunkVec = kWave * kUnroll;
+constexpr int kBlock = 256;          // scalar-path and fill-only workgroups
+constexpr int kVpl = 1;              // 16-byte vectors per lane in the vector path
 
 // Resolves a placeholder id (-1 - r -> last[r]); writes the resolved id back when `write` is set.
 // Returns -1 (and reports) for a placeholder past the samples.
@@ -41,14 +40,13 @@ __device__ __forceinline__ int64_t resolve_id(int64_t* ids, int64_t t, int64_t i
 }
 
 template <bool kFill>
-__global__ __launch_bounds__(kBlock) void embedding_gather(uint16_t* __restrict__ out, int64_t out_stride,
-                                                           const uint16_t* __restrict__ weight, int64_t weight_stride,
-                                                           int64_t vocab, int64_t* ids, int64_t rows, int nvec,
-                                                           const int32_t* __restrict__ last, int64_t num_last,
-                                                           uint32_t* err) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_id_uniform();
-  if (t >= rows) return;
+__global__ __launch_bounds__(kWave) void embedding_gather(uint16_t* __restrict__ out, int64_t out_stride,
+                                                          const uint16_t* __restrict__ weight, int64_t weight_stride,
+                                                          int64_t vocab, int64_t* ids, int64_t rows, int nvec,
+                                                          const int32_t* __restrict__ last, int64_t num_last,
+                                                          uint32_t* err) {
+  const int lane = threadIdx.x;
+  const int64_t t = blockIdx.x;
   int64_t id = ids[t];
   const bool leader = lane == 0 && blockIdx.y == 0;
   bool placeholder_bad = false;
@@ -58,13 +56,13 @@ __global__ __launch_bounds__(kBlock) void embedding_gather(uint16_t* __restrict_
       id = resolve_id(ids, t, id, last, num_last, leader, err);
     }
   }
-  const int v0 = blockIdx.y * kChunkVec + lane;
+  const int v0 = blockIdx.y * (kWave * kVpl) + lane;
   uint16_t* dst = out + t * out_stride;
   if (id < 0 || id >= vocab) {
     if (leader && !placeholder_bad) report(err, MAS_ERRBIT_TOKEN_ID);
     const u32x4 zero = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int j = 0; j < kUnroll; ++j) {
+    for (int j = 0; j < kVpl; ++j) {
       const int v = v0 + j * kWave;
       if (v < nvec) store_stream(dst + 8 * v, zero);
     }
@@ -73,15 +71,15 @@ __global__ __launch_bounds__(kBlock) void embedding_gather(uint16_t* __restrict_
   const uint16_t* src = weight + id * weight_stride;
   // Unconditional loads (indices past the row end clamped to its last vector) so they issue
   // back to back; only the stores are guarded.
-  u32x4 x[kUnroll];
+  u32x4 x[kVpl];
 #pragma unroll
-  for (int j = 0; j < kUnroll; ++j) {
+  for (int j = 0; j < kVpl; ++j) {
     const int v = v0 + j * kWave;
     x[j] = load_stream(src + 8 * (v < nvec ? v : nvec - 1));
   }
   load_fence();
 #pragma unroll
-  for (int j = 0; j < kUnroll; ++j) {
+  for (int j = 0; j < kVpl; ++j) {
     const int v = v0 + j * kWave;
     if (v < nvec) store_stream(dst + 8 * v, x[j]);
   }
@@ -128,16 +126,15 @@ int gather(void* out, int64_t out_stride, const void* weight, int64_t weight_str
                       weight_stride % 8 == 0 && hidden / 8 <= INT32_MAX;
   if (vec_ok) {
     const int nvec = static_cast<int>(hidden / 8);
-    const int64_t gx = cdiv(rows, kWavesPerBlock);
-    const int64_t gy = cdiv(nvec, kChunkVec);
-    if (gx > INT32_MAX || gy > 65535) return MAS_ERR_UNSUPPORTED;
-    const dim3 grid(static_cast<uint32_t>(gx), static_cast<uint32_t>(gy));
+    const int64_t gy = cdiv(nvec, kWave * kVpl);
+    if (rows > INT32_MAX || gy > 65535) return MAS_ERR_UNSUPPORTED;
+    const dim3 grid(static_cast<uint32_t>(rows), static_cast<uint32_t>(gy));
     if (last != nullptr) {
-      hipLaunchKernelGGL(embedding_gather<true>, grid, dim3(kBlock), 0, stream, static_cast<uint16_t*>(out),
+      hipLaunchKernelGGL(embedding_gather<true>, grid, dim3(kWave), 0, stream, static_cast<uint16_t*>(out),
                          out_stride, static_cast<const uint16_t*>(weight), weight_stride, vocab, ids, rows, nvec, last,
                          num_last, err);
     } else {
-      hipLaunchKernelGGL(embedding_gather<false>, grid, dim3(kBlock), 0, stream, static_cast<uint16_t*>(out),
+      hipLaunchKernelGGL(embedding_gather<false>, grid, dim3(kWave), 0, stream, static_cast<uint16_t*>(out),
                          out_stride, static_cast<const uint16_t*>(weight), weight_stride, vocab, ids, rows, nvec, last,
                          num_last, err);
     }

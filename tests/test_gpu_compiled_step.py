@@ -7,9 +7,9 @@ place (miniagentserve/models/devstral2/devstral2.py:158-166), the append reads v
 buffer (:170-173), decode and context attention write the ``[:d]`` and ``[d:]`` slices of one output
 (:181-213), and the embedding gather (:282) follows the runner's placeholder fill
 (model_runner.py:149-154). ``MiniModel`` below is that forward with two layers at small sizes and
-with the GEMMs replaced by elementwise stand-ins (one rounding each, on fp8 codes read as bytes, so
-eager and compiled code give the same bits). Layer 0 uses the reference's separate RoPE and append
-calls and its torch llama-4 query scale; layer 1 the fused RoPE + KV + q-scale op.
+with the GEMMs replaced by opaque elementwise stand-ins (below). Layer 0 uses the reference's
+separate RoPE and append calls and its torch llama-4 query scale; layer 1 the fused RoPE + KV +
+q-scale op.
 
 The compiled, graph-replayed step must reproduce the eager step bit for bit: the final hidden
 states, the residual stream, both KV caches and the resolved token ids. Run as a script
@@ -25,10 +25,38 @@ import pytest
 import torch
 import torch.nn.functional as F
 from torch import nn
+from torch.library import custom_op
 
 pytestmark = pytest.mark.gpu
 
 FP8 = torch.float8_e4m3fn
+
+
+# GEMM stand-ins. Like the reference's FP8Linear (devstral2.py:100-115), each is an opaque op that
+# returns a freshly allocated output, so the compiled graph holds qkv, the o_proj output and gate_up
+# as realized buffers whose column views RoPE and the KV append mutate and read in place. Their
+# values are elementwise, computed in eager torch inside the op, so eager and compiled runs agree.
+@custom_op("mas_test::gemm_from_codes", mutates_args=())
+def gemm_from_codes(x: torch.Tensor, base: torch.Tensor) -> torch.Tensor:
+    """bf16(f32(base) + first fp8 code of each row of x, read as a byte): [rows, base width]."""
+    return (base.float() + x.view(torch.uint8)[:, :1].float()).to(torch.bfloat16)
+
+
+@gemm_from_codes.register_fake
+def _(x, base):
+    return base.new_empty((x.shape[0], base.shape[1]))
+
+
+@custom_op("mas_test::gemm_scaled", mutates_args=())
+def gemm_scaled(x: torch.Tensor, base: torch.Tensor, factor: float) -> torch.Tensor:
+    """bf16(f32(x) * factor + f32(base)) with fp8 x read as bytes; x is [rows, base width]."""
+    xf = x.view(torch.uint8).float() if x.dtype == FP8 else x.float()
+    return (xf * factor + base.float()).to(torch.bfloat16)
+
+
+@gemm_scaled.register_fake
+def _(x, base, factor):
+    return base.new_empty((x.shape[0], base.shape[1]))
 
 # Small Devstral-shaped sizes: hidden = q_heads * head_dim so the o_proj stand-in is elementwise.
 HIDDEN, INTER, HQ, HK, D, VOCAB, LAYERS = 512, 512, 4, 2, 128, 1000, 2
@@ -74,7 +102,7 @@ class MiniModel(nn.Module):
             kc, vc = k_cache[layer], v_cache[layer]
             x = torch.empty(hidden.shape, dtype=FP8, device=hidden.device)
             mas.fused_add_rmsnorm_quant(x, hidden, residual, self.w_in[layer], self.act_scale, EPS)
-            qkv = (self.qkv_base[layer].float() + x.view(torch.uint8)[:, :1].float()).to(torch.bfloat16)  # qkv_proj
+            qkv = gemm_from_codes(x, self.qkv_base[layer])                               # qkv_proj
             q, k, v = qkv.split([HQ * D, HK * D, HK * D], dim=-1)
             v = v.unflatten(-1, (-1, D))
             if layer == 0:
@@ -107,11 +135,11 @@ class MiniModel(nn.Module):
                     bmm1_scale=self.scaling, bmm2_scale=1.0, batch_size=num_prefills, cum_seq_lens_q=cu_seqlens_q,
                     cum_seq_lens_kv=F.pad(seq_lens[d:].cumsum(0, dtype=torch.int32), (1, 0)), out=attn_output[d:],
                     kv_layout="NHD", error_flags=error_flags)
-            hidden = (attn_output.flatten(1).float() * 0.5 + self.o_base[layer].float()).to(torch.bfloat16)
+            hidden = gemm_scaled(attn_output.flatten(1), self.o_base[layer], 0.5)          # o_proj
             mas.fused_add_rmsnorm_quant(x, hidden, residual, self.w_post[layer], self.act_scale, EPS)
-            gate_up = (self.gu_base[layer].float() + x.view(torch.uint8)[:, :1].float()).to(torch.bfloat16)  # gate_up
+            gate_up = gemm_from_codes(x, self.gu_base[layer])                             # gate_up_proj
             y = mas.activation.silu_and_mul_quant(gate_up, self.act_scale)
-            hidden = (y.view(torch.uint8).float() * 0.25 + self.o_base[layer].float()).to(torch.bfloat16)  # down_proj
+            hidden = gemm_scaled(y, self.o_base[layer], 0.25)                             # down_proj
         mas.fused_add_rmsnorm(hidden, residual, self.w_final, EPS)
         return hidden, residual
 
