@@ -72,8 +72,12 @@ def parse_args():
                    help="the reference's FP8 dataflow: norms write fp8 for the qkv / gate_up GEMMs and SiluAndMul "
                         "writes the quantized down_proj input")
     p.add_argument("--pmc-probe", action="store_true",
-                   help="short run for rocprofv3 --pmc: the dominant kernel 20 times on the cold layer sets, "
-                        "then a 256 MiB device copy (the calibration reference for FETCH_SIZE / WRITE_SIZE)")
+                   help="short run for rocprofv3 --pmc: one kernel (--pmc-op, default the dominant one) 20 times "
+                        "on the cold layer sets, then a 256 MiB device copy (the calibration reference for "
+                        "FETCH_SIZE / WRITE_SIZE)")
+    p.add_argument("--pmc-op", default=None,
+                   help="kernel for --pmc-probe: fused_add_rmsnorm, rope, append_paged_kv_cache, silu_and_mul, "
+                        "rope_append, fused_add_rmsnorm_quant or silu_and_mul_quant")
     p.add_argument("--separate-rope-kv", action="store_true",
                    help="run RoPE and the KV append as the reference's two calls (default: one fused kernel, "
                         "same results, one launch fewer per layer); the other form is timed alongside")
@@ -894,14 +898,15 @@ def cpu_oracle_attention(inp, seconds: float) -> dict:
 
 
 def pmc_probe(mas, args, shape, dev) -> None:
-    """Launches only what a counter pass needs: the workload's dominant kernel (SiluAndMul, or the
-    norm for the norm-only case) 20 times across the cold layer sets, then 4 copies of 256 MiB."""
+    """Launches only what a counter pass needs: one kernel (``--pmc-op``; default the workload's
+    dominant kernel, SiluAndMul or the norm for the norm-only case) 20 times across the cold layer
+    sets, then 4 copies of 256 MiB."""
     wl, lp = mas.workloads, mas.layer_pass
     n_sets = max(2, math.ceil(COLD_BYTES / footprint_bytes(shape)))
     table = mas.rope.cos_sin_cache(shape.max_position, shape.head_dim, shape.theta).to(dev)
     sets = [lp.LayerBuffers(wl.make_layer_inputs(shape, dev, seed=i, fill_on_device=True, table=table,
-                                                 zero_cache=False)) for i in range(n_sets)]
-    op = step_ops(shape, False)[0 if shape.norm_only else 3]
+                                                 zero_cache=False), fp8=args.fp8) for i in range(n_sets)]
+    op = args.pmc_op or step_ops(shape, False)[0 if shape.norm_only else 3]
     for i in range(20):
         op_launcher(mas, sets[i % n_sets], op)()
     torch.cuda.synchronize()

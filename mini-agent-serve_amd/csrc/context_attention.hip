@@ -68,7 +68,17 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-template <int D, bool kTilePages, int kWaves>
+// How a tile's key / value rows find their pages (the block-table reads of a tile):
+//   kPagesTile  - pages of at least a tile: the tile lies in one page, one scalar read per tile;
+//   kPagesStep  - pages of at least half of a thread-row step (kPosStep positions): the rows of step
+//                 u lie in one or two pages, read with scalar loads, each lane picking its own;
+//   kPagesLane  - smaller pages: each lane reads the page of each of its rows (vector loads).
+// Vector loads of block-table entries make the compiler wait for them, and such waits cover every
+// vector load issued before them, the next tiles' key / value loads included: they stall the
+// software pipeline, which the scalar reads do not.
+constexpr int kPagesLane = 0, kPagesStep = 1, kPagesTile = 2;
+
+template <int D, int kPages, int kWaves>
 __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextArgs a) {
   constexpr int kCtxWaves = kWaves;
   constexpr int kCtxThreads = 64 * kWaves;
@@ -155,8 +165,9 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
     bool full;  // every chunk of the tile valid: stores need no zeroing
   };
   bool page_bad = false;  // a real position's page id outside the cache (reported once, at the end)
+  const int last_page = kv_len > 0 ? (kv_len - 1) >> a.log2_page : 0;  // the sequence's last block-table entry
   auto issue_tile = [&](TileRegs& tr, int base) {
-    if constexpr (kTilePages) {
+    if constexpr (kPages == kPagesTile) {
       const int32_t page = bt[base >> a.log2_page];
       const bool ok = page >= 0 && page < a.num_pages;
       page_bad |= !ok;
@@ -169,6 +180,51 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
         tr.k[u] = load_cached(a.k_cache + off);
         tr.v[u] = load_cached(a.v_cache + off);
         tr.lok[u] = ok && base + prow + kPosStep * u < kv_len;
+      }
+    } else if constexpr (kPages == kPagesStep) {
+      const int sub = prow >> a.log2_page;  // 0 or 1: which of the step's pages holds this lane's row
+      if (base + kTileP <= kv_len) {
+        // A full tile: every row is real, so the lane's row offset in its page is fixed (the step
+        // starts a page when it spans two) and only the page bases change.
+        bool all_ok = true;
+#pragma unroll
+        for (int u = 0; u < LOADS; ++u) {
+          const int gp = base + kPosStep * u;  // the step's first position (wave-uniform)
+          const int i0 = gp >> a.log2_page;
+          const int32_t page0 = bt[i0];
+          const int32_t page1 = bt[min(i0 + 1, last_page)];
+          const bool ok0 = page0 >= 0 && page0 < a.num_pages, ok1 = page1 >= 0 && page1 < a.num_pages;
+          const int32_t page = sub ? page1 : page0;
+          const bool ok = sub ? ok1 : ok0;
+          all_ok = all_ok && ok0 && (kPosStep <= (1 << a.log2_page) || ok1);
+          page_bad |= !ok;
+          const int64_t off = (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
+                              static_cast<int64_t>((gp + prow) & pmask) * a.entry_stride + kvh * a.head_stride +
+                              8 * dcol;
+          tr.k[u] = load_cached(a.k_cache + off);
+          tr.v[u] = load_cached(a.v_cache + off);
+          tr.lok[u] = ok;
+        }
+        tr.full = all_ok;
+      } else {
+        tr.full = false;
+#pragma unroll
+        for (int u = 0; u < LOADS; ++u) {
+          const int gp = base + kPosStep * u;
+          const int i0 = min(gp >> a.log2_page, last_page);
+          const int32_t page0 = bt[i0];
+          const int32_t page1 = bt[min(i0 + 1, last_page)];
+          const int32_t page = sub ? page1 : page0;
+          const int p = gp + prow;
+          const int pc = p < kv_len ? p : kv_len - 1;
+          const bool ok = page >= 0 && page < a.num_pages;
+          page_bad |= !ok && p < kv_len;
+          const int64_t off = (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
+                              static_cast<int64_t>(pc & pmask) * a.entry_stride + kvh * a.head_stride + 8 * dcol;
+          tr.k[u] = load_cached(a.k_cache + off);
+          tr.v[u] = load_cached(a.v_cache + off);
+          tr.lok[u] = ok && p < kv_len;
+        }
       }
     } else {
       tr.full = false;
@@ -439,32 +495,30 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   a.quant_scale_host = out_scale_host;
   a.err = err;
   const dim3 grid(static_cast<uint32_t>(gx), static_cast<uint32_t>(gy), static_cast<uint32_t>(num_rows));
-  // Pages of at least a tile: each tile lies in one page (one block-table read per tile).
-  const bool tile_pages = page_size >= kTileP;
+  // Page mode: a tile within one page, a thread-row step within one or two pages, or per lane.
+  const int64_t pos_step = 64 * waves / (head_dim / 8);
+  const int mode = page_size >= kTileP ? kPagesTile : (2 * page_size >= pos_step ? kPagesStep : kPagesLane);
   const dim3 block(static_cast<uint32_t>(64 * waves));
+  auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, 0, stream, a); };
   if (head_dim == 64) {
     if (waves == 8) {
-      if (tile_pages)
-        hipLaunchKernelGGL((context_attn<64, true, 8>), grid, block, 0, stream, a);
-      else
-        hipLaunchKernelGGL((context_attn<64, false, 8>), grid, block, 0, stream, a);
+      if (mode == kPagesTile) go(context_attn<64, kPagesTile, 8>);
+      else if (mode == kPagesStep) go(context_attn<64, kPagesStep, 8>);
+      else go(context_attn<64, kPagesLane, 8>);
     } else {
-      if (tile_pages)
-        hipLaunchKernelGGL((context_attn<64, true, 4>), grid, block, 0, stream, a);
-      else
-        hipLaunchKernelGGL((context_attn<64, false, 4>), grid, block, 0, stream, a);
+      if (mode == kPagesTile) go(context_attn<64, kPagesTile, 4>);
+      else if (mode == kPagesStep) go(context_attn<64, kPagesStep, 4>);
+      else go(context_attn<64, kPagesLane, 4>);
     }
   } else {
     if (waves == 8) {
-      if (tile_pages)
-        hipLaunchKernelGGL((context_attn<128, true, 8>), grid, block, 0, stream, a);
-      else
-        hipLaunchKernelGGL((context_attn<128, false, 8>), grid, block, 0, stream, a);
+      if (mode == kPagesTile) go(context_attn<128, kPagesTile, 8>);
+      else if (mode == kPagesStep) go(context_attn<128, kPagesStep, 8>);
+      else go(context_attn<128, kPagesLane, 8>);
     } else {
-      if (tile_pages)
-        hipLaunchKernelGGL((context_attn<128, true, 4>), grid, block, 0, stream, a);
-      else
-        hipLaunchKernelGGL((context_attn<128, false, 4>), grid, block, 0, stream, a);
+      if (mode == kPagesTile) go(context_attn<128, kPagesTile, 4>);
+      else if (mode == kPagesStep) go(context_attn<128, kPagesStep, 4>);
+      else go(context_attn<128, kPagesLane, 4>);
     }
   }
   return launch_status();

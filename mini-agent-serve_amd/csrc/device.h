@@ -19,6 +19,7 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr int kWave = 64;
+constexpr int kXcds = 8;  // MI355X: workgroups go to its 8 XCDs (each with its own L2) round-robin by id
 
 // ---- memory ------------------------------------------------------------------------------
 // Streaming accesses carry the non-temporal hint: every byte these kernels move is touched once.

@@ -42,10 +42,14 @@ __global__ __launch_bounds__(kBlock) void rope_inplace(RopeArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
   const int slot = lane / LPH;
   const int chunk = lane % LPH;
-  const int64_t work = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_id_uniform();
-  const int64_t t = work / a.groups_per_token;
+  // Workgroups go to the 8 XCDs round-robin by id; token t's wavefronts all run on XCD t % 8, so
+  // its cos/sin row is fetched into one L2.
+  const int64_t xcd = blockIdx.x % kXcds;
+  const int64_t work = static_cast<int64_t>(blockIdx.x / kXcds) * kWavesPerBlock + wave_id_uniform();
+  const int64_t tx = work / a.groups_per_token;
+  const int64_t t = tx * kXcds + xcd;
   if (t >= a.rows) return;
-  const int group = static_cast<int>(work - t * a.groups_per_token);
+  const int group = static_cast<int>(work - tx * a.groups_per_token);
 
   // Offsets of the two 16-byte vectors this lane owns inside a head.
   const int off_a = kNeox ? chunk * 8 : chunk * 16;
@@ -122,8 +126,7 @@ template <int LPH, bool kNeox, bool kPos64, int PASSES>
 int launch_rope(RopeArgs a, hipStream_t s) {
   constexpr int kHeadsPerWave = (kWave / LPH) * PASSES;
   a.groups_per_token = static_cast<int>(cdiv(a.num_heads, kHeadsPerWave));
-  const int64_t waves = a.rows * a.groups_per_token;
-  const int64_t blocks = cdiv(waves, kWavesPerBlock);
+  const int64_t blocks = kXcds * cdiv(cdiv(a.rows, kXcds) * a.groups_per_token, kWavesPerBlock);
   if (blocks > INT32_MAX) return MAS_ERR_UNSUPPORTED;
   hipLaunchKernelGGL((rope_inplace<LPH, kNeox, kPos64, PASSES>), dim3(static_cast<uint32_t>(blocks)), dim3(kBlock),
                      0, s, a);

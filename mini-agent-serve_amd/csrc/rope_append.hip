@@ -90,10 +90,15 @@ __global__ __launch_bounds__(kBlock) void rope_append(FusedArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
   const int slot = lane / LPH;
   const int chunk = lane % LPH;
-  const int64_t work = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_id_uniform();
-  const int64_t t = work / a.groups_per_token;
+  // Workgroups go to the 8 XCDs round-robin by id; token t's wavefronts all run on XCD t % 8, so
+  // its cos/sin row is fetched into one L2 (and tokens 8k apart, the same position in sequences of
+  // a multiple of 8 tokens, share it).
+  const int64_t xcd = blockIdx.x % kXcds;
+  const int64_t work = static_cast<int64_t>(blockIdx.x / kXcds) * kWavesPerBlock + wave_id_uniform();
+  const int64_t tx = work / a.groups_per_token;
+  const int64_t t = tx * kXcds + xcd;
   if (t >= a.rows) return;
-  const int group = static_cast<int>(work - t * a.groups_per_token);
+  const int group = static_cast<int>(work - tx * a.groups_per_token);
   const int hq = a.num_q_heads, hkv = a.num_kv_heads;
   const int total = hq + 2 * hkv;
 
@@ -226,7 +231,7 @@ template <int LPH, bool kNeox, int PASSES>
 int launch(FusedArgs a, hipStream_t s) {
   constexpr int kHeadsPerWave = (kWave / LPH) * PASSES;
   a.groups_per_token = static_cast<int>(cdiv(a.num_q_heads + 2 * a.num_kv_heads, kHeadsPerWave));
-  const int64_t blocks = cdiv(a.rows * a.groups_per_token, kWavesPerBlock);
+  const int64_t blocks = kXcds * cdiv(cdiv(a.rows, kXcds) * a.groups_per_token, kWavesPerBlock);
   if (blocks > INT32_MAX) return MAS_ERR_UNSUPPORTED;
   hipLaunchKernelGGL((rope_append<LPH, kNeox, PASSES>), dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, s, a);
   return launch_status();

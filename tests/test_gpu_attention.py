@@ -49,6 +49,8 @@ CASES = [
     (3, 6, 2, 128, 4, [9, 40, 2]),                 # 3 per kv head (padded), pages of 4
     (2, 16, 4, 128, 512, [700, 1500]),             # pages of two chunks
     (2, 8, 2, 128, 256, [9000, 100]),              # 36 splits: the combine's path past 32 splits
+    (2, 16, 2, 64, 256, [600, 257]),               # head_dim 64 on pages of a chunk (scalar page ids)
+    (2, 16, 1, 256, 512, [1100, 300]),             # head_dim 256 on pages of two chunks
 ]
 
 
@@ -63,6 +65,19 @@ def test_decode_attention_matches_oracle(mas, dev, batch, hq, hk, dim, page_size
     assert int(flags.item()) == 0
     if 0 in lens:
         assert not out[lens.index(0)].any()
+
+
+@pytest.mark.parametrize("page_size", [16, 256])
+def test_decode_attention_hnd_layout(mas, dev, page_size):
+    """kv_layout="HND" ([pages, kv_heads, page_size, head_dim]): the same results as NHD."""
+    batch, hq, hk, dim, lens = 3, 32, 8, 128, [300, 1, 777]
+    q, kc, vc, tables, seq = _case(21 + page_size, batch, hq, hk, dim, page_size, lens)
+    ws = torch.zeros(128 << 20, dtype=torch.uint8, device=dev)
+    kh, vh = kc.transpose(1, 2).contiguous().to(dev), vc.transpose(1, 2).contiguous().to(dev)
+    out = mas.attention.trtllm_batch_decode_with_kv_cache(q.to(dev), (kh, vh), ws, tables.to(dev), seq.to(dev), 0,
+                                                          dim ** -0.5, 1.0, kv_layout="HND")
+    want = ops.paged_decode_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), dim ** -0.5)
+    _check(bits(out), want)
 
 
 def test_decode_attention_long_splits_and_bmm2_scale(mas, dev):

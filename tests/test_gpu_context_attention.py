@@ -53,6 +53,11 @@ CASES = [
     ([20, 0, 7], [30, 10, 7], 8, 2, 128, 64),      # a row with no new tokens between two others
     ([45, 19], [80, 19], 16, 2, 64, 16),           # 8 per kv head (eight-wavefront groups), head_dim 64, small pages
     ([70, 33], [90, 33], 24, 2, 128, 32),          # 12 per kv head, pages smaller than a tile
+    ([50, 23], [75, 23], 32, 8, 128, 8),           # a thread-row step over two pages (four wavefronts)
+    ([60, 31], [99, 40], 96, 8, 128, 16),          # two pages per step, eight wavefronts (123B group)
+    ([41], [77], 8, 4, 64, 16),                    # two pages per step, head_dim 64
+    ([90, 17], [150, 17], 16, 8, 64, 64),          # head_dim 64 on pages of one tile
+    ([70], [200], 32, 8, 64, 128),                 # head_dim 64 on pages of two tiles
 ]
 
 
@@ -65,6 +70,20 @@ def test_context_attention_matches_oracle(mas, dev, q_lens, kv_lens, hq, hk, dim
     want = ops.paged_context_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), cu.numpy(), scale)
     _check(bits(out), want)
     assert int(flags.item()) == 0
+
+
+@pytest.mark.parametrize("page_size", [16, 256])
+def test_context_attention_hnd_layout(mas, dev, page_size):
+    """kv_layout="HND" ([pages, kv_heads, page_size, head_dim]): the same results as NHD."""
+    q_lens, kv_lens, hq, hk, dim = [50, 9], [120, 9], 32, 8, 128
+    q, kc, vc, tables, seq, cu = _case(31 + page_size, q_lens, kv_lens, hq, hk, dim, page_size)
+    kh, vh = kc.transpose(1, 2).contiguous().to(dev), vc.transpose(1, 2).contiguous().to(dev)
+    ws = torch.empty(16, dtype=torch.uint8, device=dev)
+    out = mas.attention.trtllm_batch_context_with_kv_cache(
+        q.to(dev), (kh, vh), ws, tables.to(dev), seq.to(dev), max(q_lens), 0, 0.09, 1.0, len(q_lens), cu.to(dev),
+        None, kv_layout="HND")
+    want = ops.paged_context_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), cu.numpy(), 0.09)
+    _check(bits(out), want)
 
 
 def test_context_attention_strided_views_and_bmm2_scale(mas, dev):
