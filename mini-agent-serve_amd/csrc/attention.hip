@@ -17,6 +17,8 @@
 //     layout, then P.V on MFMA with P and the value rows passed through LDS (read back
 //     transposed). The split's running (max, sum) and unnormalised O go to the caller's workspace.
 //  2. decode_attn_combine - one wavefront per (query head, row) merges the splits and writes bf16.
+// A row whose positions fit one split skips both steps' partials: the split kernel writes its output
+// straight from the registers (as merging one split gives) and the combine kernel leaves it alone.
 // Scores live in the log2 domain (bmm1_scale * log2 e folded in), so every exponential is one
 // v_exp_f32. A position whose page id is out of range is skipped (MAS_ERRBIT_PAGE); seq_lens past
 // the block table's reach is clamped to it (MAS_ERRBIT_POSITION); a row with no position gets zeros.
@@ -72,6 +74,49 @@ __device__ __forceinline__ int kv_len(const DecodeArgs& a, int b) {
   const int64_t L = a.seq_lens[b];
   const int64_t cap = a.max_blocks << a.log2_page;
   return static_cast<int>(L < 0 ? 0 : (L > cap ? cap : L));
+}
+
+// The output element(s) of row b, query head h, starting at head-dim column `col`: bf16 y, or its
+// fp8 quantize (the o_proj input quantize of devstral2.py:93-95,110-111) with out_fp8.
+template <int N>
+__device__ __forceinline__ void store_output(const DecodeArgs& a, int b, int h, int col, const float (&y)[N]) {
+  const int64_t at = b * a.out_stride + h * a.out_head_stride + col;
+  uint32_t w[(N + 1) / 2];  // bf16 pairs
+  if constexpr (N == 1) {
+    w[0] = pack_bf16x2(y[0], 0.f);
+  } else {
+#pragma unroll
+    for (int e = 0; e < N / 2; ++e) w[e] = pack_bf16x2(y[2 * e], y[2 * e + 1]);
+  }
+  if (a.out_fp8) {
+    const float qs = a.quant_scale_dev != nullptr ? *a.quant_scale_dev : a.quant_scale_host;
+    const float rcp = 1.0f / qs;
+    float qv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int ee = e < N ? e : 0;
+      const float v = (ee & 1) ? bf16_hi(w[ee / 2]) : bf16_lo(w[ee / 2]);
+      qv[e] = div_by_scale(v, qs, rcp);
+    }
+    const uint32_t codes = fp8x4_saturate_encode(qv[0], qv[1], qv[2], qv[3]);
+    uint8_t* dst = static_cast<uint8_t*>(a.out) + at;
+    if constexpr (N == 1) {
+      dst[0] = static_cast<uint8_t>(codes);
+    } else if constexpr (N == 2) {
+      *reinterpret_cast<uint16_t*>(dst) = static_cast<uint16_t>(codes);
+    } else {
+      *reinterpret_cast<uint32_t*>(dst) = codes;
+    }
+  } else {
+    uint16_t* dst = static_cast<uint16_t*>(a.out) + at;
+    if constexpr (N == 1) {
+      dst[0] = static_cast<uint16_t>(w[0]);
+    } else if constexpr (N == 2) {
+      *reinterpret_cast<uint32_t*>(dst) = w[0];
+    } else {
+      *reinterpret_cast<u32x2*>(dst) = u32x2{w[0], w[1]};
+    }
+  }
 }
 
 // Key loads go through the cache hierarchy: a wavefront's load instruction reads 64 bytes of each
@@ -349,6 +394,23 @@ __global__ __launch_bounds__(64 * kAttnWaves, D <= 128 ? kAttnMinWaves : 1) void
   }
   if (__builtin_amdgcn_ballot_w64(bad) != 0 && lane == 0) report(a.err, MAS_ERRBIT_PAGE);
 
+  if (L <= a.chunks_per_split * kChunk) {
+    // The row's only split: its output is O / l * bmm2_scale, what merging one split gives.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int g = 4 * r + j;
+      if (g < G) {
+        const float sc = l_run[j] > 0.f ? a.out_scale / l_run[j] : 0.f;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const float y[1] = {acc[dt][j] * sc};
+          store_output<1>(a, b, kvh * G + g, 16 * dt + n, y);
+        }
+      }
+    }
+    return;
+  }
+
   // ---- partials: lane (n, r) holds O[head 4r+j][16 dt + n]
   const int64_t base = (static_cast<int64_t>(b) * a.hq + kvh * G) * a.max_splits + split;
 #pragma unroll
@@ -390,6 +452,10 @@ __global__ __launch_bounds__(64) void decode_attn_combine(DecodeArgs a) {
   const int L = static_cast<int>(raw < 0 ? 0 : (raw > cap ? cap : raw));
   const int split_len = a.chunks_per_split * kChunk;
   const int nsplit = (L + split_len - 1) / split_len;
+  if (nsplit == 1) {  // the split kernel wrote this row's output
+    if (len_bad && h == 0 && lane == 0) report(a.err, MAS_ERRBIT_POSITION);
+    return;
+  }
   const int64_t base = (static_cast<int64_t>(b) * a.hq + h) * a.max_splits;
   float acc[DPL];
 #pragma unroll
@@ -465,44 +531,10 @@ __global__ __launch_bounds__(64) void decode_attn_combine(DecodeArgs a) {
   if (len_bad && h == 0 && lane == 0) report(a.err, MAS_ERRBIT_POSITION);
   const float denom = wave_sum(lsum);
   const float scale = denom > 0.f ? a.out_scale / denom : 0.f;
-  const int64_t at = b * a.out_stride + h * a.out_head_stride + DPL * lane;
-  uint32_t y[(DPL + 1) / 2];  // bf16 pairs
-  if constexpr (DPL == 1) {
-    y[0] = pack_bf16x2(acc[0] * scale, 0.f);
-  } else {
+  float y[DPL];
 #pragma unroll
-    for (int e = 0; e < DPL / 2; ++e) y[e] = pack_bf16x2(acc[2 * e] * scale, acc[2 * e + 1] * scale);
-  }
-  if (a.out_fp8) {
-    // the quantize the reference applies to the bf16 attention output (devstral2.py:93-95,110-111)
-    const float qs = a.quant_scale_dev != nullptr ? *a.quant_scale_dev : a.quant_scale_host;
-    const float rcp = 1.0f / qs;
-    float qv[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int ee = e < DPL ? e : 0;
-      const float v = (ee & 1) ? bf16_hi(y[ee / 2]) : bf16_lo(y[ee / 2]);
-      qv[e] = div_by_scale(v, qs, rcp);
-    }
-    const uint32_t codes = fp8x4_saturate_encode(qv[0], qv[1], qv[2], qv[3]);
-    uint8_t* dst = static_cast<uint8_t*>(a.out) + at;
-    if constexpr (DPL == 1) {
-      dst[0] = static_cast<uint8_t>(codes);
-    } else if constexpr (DPL == 2) {
-      *reinterpret_cast<uint16_t*>(dst) = static_cast<uint16_t>(codes);
-    } else {
-      *reinterpret_cast<uint32_t*>(dst) = codes;
-    }
-  } else {
-    uint16_t* dst = static_cast<uint16_t*>(a.out) + at;
-    if constexpr (DPL == 1) {
-      dst[0] = static_cast<uint16_t>(y[0]);
-    } else if constexpr (DPL == 2) {
-      *reinterpret_cast<uint32_t*>(dst) = y[0];
-    } else {
-      *reinterpret_cast<u32x2*>(dst) = u32x2{y[0], y[1]};
-    }
-  }
+  for (int e = 0; e < DPL; ++e) y[e] = acc[e] * scale;
+  store_output<DPL>(a, b, h, DPL * lane, y);
 }
 
 template <int GP, int D>

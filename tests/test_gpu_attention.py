@@ -80,6 +80,21 @@ def test_decode_attention_hnd_layout(mas, dev, page_size):
     _check(bits(out), want)
 
 
+def test_decode_attention_single_and_multi_split_rows(mas, dev):
+    """Rows that fit one split are written by the split kernel and skipped by the combine kernel;
+    longer rows go through the partials. A batch mixing both (and empty rows), on a workspace whose
+    previous contents are garbage (0xff), matches the oracle."""
+    ws = torch.full((8 << 20,), 255, dtype=torch.uint8, device=dev)
+    for seed, (batch, hq, hk, lens) in enumerate([(4, 32, 8, [3000, 1, 0, 700]), (2, 96, 8, [9000, 5]),
+                                                  (3, 16, 2, [256, 257, 5000])]):
+        q, kc, vc, tables, seq = _case(40 + seed, batch, hq, hk, 128, 256, lens)
+        out = mas.attention.trtllm_batch_decode_with_kv_cache(q.to(dev), (kc.to(dev), vc.to(dev)), ws,
+                                                              tables.to(dev), seq.to(dev), 0, 0.088, 1.0)
+        torch.cuda.synchronize()
+        want = ops.paged_decode_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), 0.088)
+        _check(bits(out), want)
+
+
 def test_decode_attention_long_splits_and_bmm2_scale(mas, dev):
     """A workspace too small for one split per 256 positions makes each wavefront walk several
     chunks, merging them with the running max: same results as the oracle."""
