@@ -411,21 +411,36 @@ __global__ __launch_bounds__(64 * kAttnWaves, D <= 128 ? kAttnMinWaves : 1) void
     return;
   }
 
-  // ---- partials: lane (n, r) holds O[head 4r+j][16 dt + n]
+  // ---- partials. Lane (n, r) holds O[head 4r+j][16 dt + n]: the rows go through LDS (the value
+  // buffer, free after the last step) so that each lane stores 16-byte pieces of whole head rows,
+  // a few wide stores per wavefront in place of 4 * DT scattered 4-byte ones.
+  constexpr int OROW = D + 4;  // floats per LDS row: the 4 lane groups' rows start 16 banks apart
+  static_assert(16 * OROW * 4 <= kStep * VROW * 2, "partial rows fit the value buffer");
+  float* o_lds = reinterpret_cast<float*>(v_lds);
+  wave_lds_sync();  // the last step's value reads are done
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o_lds[(4 * r + j) * OROW + 16 * dt + n] = acc[dt][j];
+  wave_lds_sync();
   const int64_t base = (static_cast<int64_t>(b) * a.hq + kvh * G) * a.max_splits + split;
+  constexpr int kVecs = D / 4;  // 16-byte pieces per head row
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int g = 4 * r + j;
+  for (int u = 0; u < GP * kVecs / 64; ++u) {
+    const int idx = 64 * u + lane;
+    const int g = idx / kVecs, c = idx % kVecs;
     if (g < G) {
-      float* dst = a.part_o + (base + static_cast<int64_t>(g) * a.max_splits) * D + n;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) dst[16 * dt] = acc[dt][j];
-      if (n == 0) {
-        *reinterpret_cast<f32x2*>(a.part_ml + (base + static_cast<int64_t>(g) * a.max_splits) * 2) =
-            f32x2{m_run[j], l_run[j]};
-      }
+      const f32x4 v = *reinterpret_cast<const f32x4*>(o_lds + g * OROW + 4 * c);
+      *reinterpret_cast<f32x4*>(a.part_o + (base + static_cast<int64_t>(g) * a.max_splits) * D + 4 * c) = v;
     }
   }
+  // (max, sum) of head 4r + n from the lanes n < 4 (every lane of a 16-lane group holds its 4 heads')
+  const int jn = n & 3;
+  const float m_sel = jn == 0 ? m_run[0] : jn == 1 ? m_run[1] : jn == 2 ? m_run[2] : m_run[3];
+  const float l_sel = jn == 0 ? l_run[0] : jn == 1 ? l_run[1] : jn == 2 ? l_run[2] : l_run[3];
+  if (n < 4 && 4 * r + n < G)
+    *reinterpret_cast<f32x2*>(a.part_ml + (base + static_cast<int64_t>(4 * r + n) * a.max_splits) * 2) =
+        f32x2{m_sel, l_sel};
 }
 
 // Max over the 64 lanes of a wavefront.
