@@ -16,6 +16,8 @@ second clock store and one more step. Each graph is replayed once untimed (a gra
 also uploads it), then the chunks' stamped intervals are summed: exactly --steps steps, with no
 graph launch or host gap inside (ROCm does not allow timing events inside graphs). Beside it: HIP events around replays of graphs of the timed steps
 alone (graph launch included, ``graph_us_per_step``) and the host clock (``host_us_per_step``).
+At decode sizes the line also carries the host time of one eager call of each op's wrapper
+(``eager_host_us_per_call``): the reference runs steps past its graph sizes eagerly.
 
 Printed on one JSON line: the metric (credited HBM bytes per step / time per step), microseconds
 per layer, each kernel's average launch duration and bandwidth (HIP events around a graph of
@@ -56,16 +58,17 @@ COLD_BYTES = 768 << 20         # working set cycled by the cold protocol (3x the
 MEASURED_TRAFFIC = {("decode64_24b", "silu_and_mul"): 12_611_644,
                     ("prefill8192_24b", "silu_and_mul"): 1_610_374_077,
                     ("prefill16384_123b", "silu_and_mul"): 2_818_327_781,
-                    ("decode_attn_64x8192_24b", "paged_decode_attention"): 1_114_384_294}
+                    ("decode_attn_64x8192_24b", "paged_decode_attention"): 1_115_001_551,
+                    ("decode_attn_64x8192_123b", "paged_decode_attention"): 1_188_456_517}
 # Average per-dispatch duration (µs) of a workload's dominant kernel in a committed rocprofv3 kernel
 # trace (profiles/), beside the bench's own HIP-event figure: the tracer lengthens decode-sized
 # dispatches (~15%); at prefill sizes the two agree within 2%. Re-trace when the kernel changes.
 TRACED_LAUNCH_US = {("decode64_24b", "silu_and_mul"): (4.170, "profiles/layer_decode64_kernel_trace.md"),
                     ("prefill8192_24b", "silu_and_mul"): (244.647, "profiles/layer_prefill8192_kernel_trace.md"),
                     ("decode_attn_64x8192_24b", "paged_decode_attention"):
-                        (208.193 + 6.814, "profiles/decode_attention_64x8192_kernel_trace.md"),
+                        (205.223 + 7.225, "profiles/decode_attention_64x8192_kernel_trace.md"),
                     ("decode_attn_64x8192_123b", "paged_decode_attention"):
-                        (229.745 + 13.461, "profiles/decode_attention_64x8192_kernel_trace.md")}
+                        (225.285 + 13.855, "profiles/decode_attention_64x8192_kernel_trace.md")}
 
 
 def parse_args():
@@ -272,6 +275,25 @@ def time_ops(mas, layer_sets, launches: int, ops: tuple[str, ...], replays: int 
         times = sorted(start.elapsed_time(stop) for start, stop in events)
         out[op] = 1000.0 * times[len(times) // 2] / launches
         del g
+    return out
+
+
+def eager_host_us(mas, layer_sets, ops: tuple[str, ...], calls: int = 500) -> dict[str, float]:
+    """Host time (µs) of one eager call of each op's Python wrapper (argument checks, stream query,
+    ctypes call and kernel launch): ``calls`` back-to-back calls on the launch stream, timed on the
+    host clock without waiting for the GPU (these decode-sized kernels run shorter than a call), after
+    50 untimed calls."""
+    out = {}
+    for op in ops:
+        fns = [op_launcher(mas, layer_sets[i % len(layer_sets)], op) for i in range(calls + 50)]
+        for f in fns[:50]:
+            f()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for f in fns[50:]:
+            f()
+        out[op] = round((time.perf_counter() - t0) / calls * 1e6, 2)
+        torch.cuda.synchronize()
     return out
 
 
@@ -643,6 +665,7 @@ def run_layer_workload(mas, args, shape, dev) -> dict:
 
     launches = max(2 * n_sets, 100) if shape.decode else 4 * n_sets
     kernels = step_ops(shape, args.fp8)
+    eager = eager_host_us(mas, sets, kernels) if shape.decode else None
     skeletons = tuple(f"skeleton:{op}" for op in kernels if op in SKELETON_OPS and shape.tokens <= 65535) \
         if _skeleton_fn is not None else ()
     op_us = time_ops(mas, sets, launches, kernels + skeletons)
@@ -663,7 +686,7 @@ def run_layer_workload(mas, args, shape, dev) -> dict:
            "value": per_step / (ms_per_step * 1e-3) / 1e9, "stream_us_per_step": stream_us, "ops": ops,
            "sets": n_sets, "dominant": dominant, "dominant_bytes": cb[dominant], "dominant_us": op_us[dominant],
            "graph_us_per_step": timing["graph_s"] / steps * 1e6, "host_us_per_step": timing["host_s"] / steps * 1e6,
-           "step_inputs": step_inputs}
+           "step_inputs": step_inputs, "eager_host_us_per_call": eager}
     if other_us is not None:
         res["separate_us_per_layer" if fused else "fused_us_per_layer"] = other_us
     return res
@@ -828,21 +851,25 @@ def cpu_torch_attention(inp, seconds: float) -> dict:
 
 
 def cpu_torch_context(inp, seconds: float) -> dict:
-    """The CPU baseline for context attention: causal attention of the first row's query tokens in
-    blocks of 64 from its end (the longest reach first) as torch CPU code in fp32 on all of torch's
-    host threads, for about ``seconds``; algorithmic flops done per second."""
+    """The CPU baseline for context attention: causal attention of the prompt rows' query tokens in
+    blocks of 64 from each row's end (the longest reach first) as torch CPU code in fp32 on all of
+    torch's host threads, cycling over the rows (and again from the first) for about ``seconds``;
+    algorithmic flops done per second."""
     s = inp.shape
     kv_len = s.cached + s.q_len
-    q = inp.q.cpu()[: s.q_len].float()                                  # row 0's tokens
     kc, vc = _cpu_kv(inp)
-    idx = _cpu_rows(inp.block_tables.cpu()[0], kv_len, s.page_size)
-    k = kc[idx].permute(1, 2, 0)                                        # [Hk, D, kv_len]
-    v = vc[idx].permute(1, 0, 2)                                        # [Hk, kv_len, D]
+    q_all = inp.q.cpu().float()
+    tables = inp.block_tables.cpu()
     g = s.q_heads // s.kv_heads
     scale = s.head_dim ** -0.5
-    done, tokens, t0 = 0, 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds and tokens < s.q_len:
-        hi = s.q_len - tokens
+    rows = []
+    for r in range(s.rows):
+        idx = _cpu_rows(tables[r], kv_len, s.page_size)
+        rows.append((q_all[r * s.q_len:(r + 1) * s.q_len], kc[idx].permute(1, 2, 0), vc[idx].permute(1, 0, 2)))
+    done, tokens, blocks, t0 = 0, 0, 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        q, k, v = rows[(blocks // -(-s.q_len // 64)) % s.rows]          # [tokens, Hq, D], [Hk, D, kv], [Hk, kv, D]
+        hi = s.q_len - (blocks % -(-s.q_len // 64)) * 64
         lo = max(0, hi - 64)
         reach = s.cached + hi                                           # positions the block's last token sees
         qb = q[lo:hi].view(hi - lo, s.kv_heads, g, s.head_dim).permute(1, 2, 0, 3).reshape(s.kv_heads, -1, s.head_dim)
@@ -852,10 +879,12 @@ def cpu_torch_context(inp, seconds: float) -> dict:
         (torch.softmax(sc, dim=-1) @ v[:, :reach]).to(torch.bfloat16)
         done += sum(s.cached + i + 1 for i in range(lo, hi)) * s.q_heads * s.head_dim * 4
         tokens += hi - lo
+        blocks += 1
     elapsed = time.perf_counter() - t0
     return {"value": round(done / elapsed / 1e12, 6), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
-            "kind": "port", "sample": f"{tokens} query tokens of one row (longest reach first) as torch CPU code, "
-                                      f"fp32 ({elapsed:.1f} s, {torch.get_num_threads()} threads)"}
+            "kind": "port", "sample": f"{tokens} query tokens of the workload's prompt rows, cycled (longest reach "
+                                      f"first in each row) as torch CPU code, fp32 ({elapsed:.1f} s, "
+                                      f"{torch.get_num_threads()} threads)"}
 
 
 def cpu_oracle_context(inp, seconds: float) -> dict:
@@ -1002,6 +1031,8 @@ def main() -> int:
             line[key] = round(res[key], 3)
     if res.get("step_inputs"):
         line["step_inputs"] = res["step_inputs"]
+    if res.get("eager_host_us_per_call"):
+        line["eager_host_us_per_call"] = res["eager_host_us_per_call"]
     line["copy_ceiling_GBps"] = round(copy_ceiling_gbs(dev), 1)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_torch_layer(shape, args.cpu_seconds, args.fp8)
