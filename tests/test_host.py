@@ -92,7 +92,7 @@ def test_status_strings_and_version(mas):
                                                  "page slot past kv_indices or page id outside the cache"
 
 
-def test_rows_view():
+def test_rows_view(mas):
     from mini_agent_serve_amd._tensors import rows_view
     t = torch.empty(6, 10)
     assert rows_view(t, "t") == (6, 10)
@@ -106,6 +106,61 @@ def test_rows_view():
     assert rows_view(torch.empty(3, 4, 8)[:, ::2], "t") == (6, 16)     # every other row: one stride
     with pytest.raises(ValueError, match="one row index"):
         rows_view(torch.empty(3, 4, 8)[:, :2], "t")
+
+
+def test_rows_view_against_brute_force(mas):
+    """Random shapes and strides: rows_view accepts exactly the layouts whose rows, enumerated in
+    row-major order of the leading dimensions, start at r * row_stride, and returns that stride."""
+    import itertools
+    import random
+    from mini_agent_serve_amd._tensors import rows_view
+    rng = random.Random(7)
+    storage = torch.empty(1 << 16)
+    checked = rejected = 0
+    for _ in range(3000):
+        nd = rng.randint(1, 4)
+        shape = [rng.choice([1, 1, 2, 3, 4]) for _ in range(nd - 1)] + [rng.choice([1, 2, 5, 8])]
+        strides = [rng.choice([0, 1, 3, 8, 16, 40, 64, 99]) for _ in range(nd - 1)] + [rng.choice([1, 1, 1, 2])]
+        t = storage.as_strided(shape, strides)
+        w = shape[-1]
+        offsets = [sum(i * s for i, s in zip(idx, strides[:-1]))
+                   for idx in itertools.product(*[range(n) for n in shape[:-1]])]
+        rows = len(offsets)
+        if w > 1 and strides[-1] != 1:
+            want = None
+        elif rows == 1:
+            want = (1, max(w, 1))
+        else:
+            step = offsets[1] - offsets[0]
+            want = (rows, step) if all(o == r * step + offsets[0] for r, o in enumerate(offsets)) else None
+        if want is None:
+            with pytest.raises(ValueError):
+                rows_view(t, "t")
+            rejected += 1
+        else:
+            assert rows_view(t, "t") == want, (shape, strides)
+            checked += 1
+    assert checked > 500 and rejected > 500
+
+
+def test_device_checks_compare_device_indices(mas):
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    from mini_agent_serve_amd._tensors import require_gpu, require_same_device
+    a, b = torch.empty(2), torch.empty(3)
+    assert require_same_device(("a", a), ("b", b)) == torch.device("cpu")
+    with pytest.raises(ValueError, match="GPU"):
+        require_gpu(a, "a")
+    with pytest.raises(TypeError, match="torch.Tensor"):
+        require_gpu([1, 2], "a")
+    with FakeTensorMode():
+        g0 = torch.empty(2, device="cuda:0")
+        g1 = torch.empty(2, device="cuda:1")
+        require_gpu(g0, "g0")
+        assert require_same_device(("x", g0), ("y", torch.empty(5, device="cuda:0"))) == torch.device("cuda:0")
+        with pytest.raises(ValueError, match="y is on cuda:1"):
+            require_same_device(("x", g0), ("y", g1))
+        with pytest.raises(ValueError, match="y is on cpu"):
+            require_same_device(("x", g0), ("y", a))
 
 
 def test_arguments_are_validated_before_launch(mas):
