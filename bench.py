@@ -86,7 +86,8 @@ def parse_args():
     p.add_argument("--pmc-probe", action="store_true",
                    help="short run for rocprofv3 --pmc: one kernel (--pmc-op, default the dominant one) 20 times "
                         "on the cold layer sets, then a 256 MiB device copy (the calibration reference for "
-                        "FETCH_SIZE / WRITE_SIZE)")
+                        "FETCH_SIZE / WRITE_SIZE); decode attention workloads: 5 calls, then the copies; context "
+                        "attention workloads: 5 calls")
     p.add_argument("--pmc-op", default=None,
                    help="kernel for --pmc-probe: fused_add_rmsnorm, rope, append_paged_kv_cache, silu_and_mul, "
                         "rope_append, fused_add_rmsnorm_quant or silu_and_mul_quant")
@@ -770,6 +771,14 @@ def context_main(mas, args, shape, dev) -> int:
                                                          inp.seq_lens, shape.q_len, shape.q_len + shape.cached,
                                                          scale, 1.0, shape.rows, inp.cu_seqlens_q, None, out=out)
 
+    if args.pmc_probe:
+        # 5 calls of the op and nothing else: a counter pass then sees only its dispatches
+        for _ in range(5):
+            call()
+        torch.cuda.synchronize()
+        print(json.dumps({"pmc_probe": "paged_context_attention", "launches": 5, "flops_per_launch": flops}),
+              flush=True)
+        return 0
     steps = args.steps if args.steps is not None else 20
     warmup = args.warmup if args.warmup is not None else 3
     call()
