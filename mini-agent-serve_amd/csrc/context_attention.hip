@@ -70,13 +70,15 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
 
 // How a tile's key / value rows find their pages (the block-table reads of a tile):
 //   kPagesTile  - pages of at least a tile: the tile lies in one page, one scalar read per tile;
-//   kPagesStep  - pages of at least half of a thread-row step (kPosStep positions): the rows of step
-//                 u lie in one or two pages, read with scalar loads, each lane picking its own;
+//   kPagesStep1 - pages of at least a thread-row step (kPosStep positions): each step of a tile lies
+//                 in one page, one scalar read per step, each lane adding its fixed row offset;
+//   kPagesStep  - pages of at least half of a thread-row step: the rows of step u lie in one or two
+//                 pages, read with scalar loads, each lane picking its own;
 //   kPagesLane  - smaller pages: each lane reads the page of each of its rows (vector loads).
 // Vector loads of block-table entries make the compiler wait for them, and such waits cover every
 // vector load issued before them, the next tiles' key / value loads included: they stall the
 // software pipeline, which the scalar reads do not.
-constexpr int kPagesLane = 0, kPagesStep = 1, kPagesTile = 2;
+constexpr int kPagesLane = 0, kPagesStep = 1, kPagesTile = 2, kPagesStep1 = 3;
 
 template <int D, int kPages, int kWaves>
 __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextArgs a) {
@@ -181,6 +183,26 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
         tr.v[u] = load_cached(a.v_cache + off);
         tr.lok[u] = ok && base + prow + kPosStep * u < kv_len;
       }
+    } else if constexpr (kPages == kPagesStep1) {
+      // Step u starts at a multiple of kPosStep <= page size, so its rows lie in one page at entries
+      // (gp & pmask) + prow: a wave-uniform base per step plus the lane's fixed offset. Rows past
+      // kv_len are read from inside that page (the sequence's last page for steps past its end) and
+      // zeroed when staged.
+      bool all_ok = true;
+#pragma unroll
+      for (int u = 0; u < LOADS; ++u) {
+        const int gp = base + kPosStep * u;  // the step's first position (wave-uniform)
+        const int32_t page = bt[min(gp >> a.log2_page, last_page)];
+        const bool ok = page >= 0 && page < a.num_pages;
+        page_bad |= !ok && gp < kv_len;
+        all_ok = all_ok && ok;
+        const int64_t off = (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
+                            static_cast<int64_t>(gp & pmask) * a.entry_stride + lane_off;
+        tr.k[u] = load_cached(a.k_cache + off);
+        tr.v[u] = load_cached(a.v_cache + off);
+        tr.lok[u] = ok && gp + prow < kv_len;
+      }
+      tr.full = all_ok && base + kTileP <= kv_len;
     } else if constexpr (kPages == kPagesStep) {
       const int sub = prow >> a.log2_page;  // 0 or 1: which of the step's pages holds this lane's row
       if (base + kTileP <= kv_len) {
@@ -497,26 +519,33 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   const dim3 grid(static_cast<uint32_t>(gx), static_cast<uint32_t>(gy), static_cast<uint32_t>(num_rows));
   // Page mode: a tile within one page, a thread-row step within one or two pages, or per lane.
   const int64_t pos_step = 64 * waves / (head_dim / 8);
-  const int mode = page_size >= kTileP ? kPagesTile : (2 * page_size >= pos_step ? kPagesStep : kPagesLane);
+  const int mode = page_size >= kTileP     ? kPagesTile
+                   : page_size >= pos_step ? kPagesStep1
+                   : 2 * page_size >= pos_step ? kPagesStep
+                                               : kPagesLane;
   const dim3 block(static_cast<uint32_t>(64 * waves));
   auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, 0, stream, a); };
   if (head_dim == 64) {
     if (waves == 8) {
       if (mode == kPagesTile) go(context_attn<64, kPagesTile, 8>);
+      else if (mode == kPagesStep1) go(context_attn<64, kPagesStep1, 8>);
       else if (mode == kPagesStep) go(context_attn<64, kPagesStep, 8>);
       else go(context_attn<64, kPagesLane, 8>);
     } else {
       if (mode == kPagesTile) go(context_attn<64, kPagesTile, 4>);
+      else if (mode == kPagesStep1) go(context_attn<64, kPagesStep1, 4>);
       else if (mode == kPagesStep) go(context_attn<64, kPagesStep, 4>);
       else go(context_attn<64, kPagesLane, 4>);
     }
   } else {
     if (waves == 8) {
       if (mode == kPagesTile) go(context_attn<128, kPagesTile, 8>);
+      else if (mode == kPagesStep1) go(context_attn<128, kPagesStep1, 8>);
       else if (mode == kPagesStep) go(context_attn<128, kPagesStep, 8>);
       else go(context_attn<128, kPagesLane, 8>);
     } else {
       if (mode == kPagesTile) go(context_attn<128, kPagesTile, 4>);
+      else if (mode == kPagesStep1) go(context_attn<128, kPagesStep1, 4>);
       else if (mode == kPagesStep) go(context_attn<128, kPagesStep, 4>);
       else go(context_attn<128, kPagesLane, 4>);
     }

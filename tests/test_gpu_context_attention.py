@@ -101,8 +101,9 @@ def test_context_attention_strided_views_and_bmm2_scale(mas, dev):
     assert torch.all(out_base[:, 0] == 5.0) and torch.all(out_base[:, hq + 1] == 5.0)
 
 
-def test_context_attention_error_paths(mas, dev):
-    q_lens, kv_lens, hq, hk, dim, ps = [20, 10], [40, 10], 8, 2, 64, 8
+@pytest.mark.parametrize("ps", [8, 16, 32])   # head_dim 64, four wavefronts (32-row steps): per-lane, two-page and one-page steps
+def test_context_attention_error_paths(mas, dev, ps):
+    q_lens, kv_lens, hq, hk, dim = [20, 10], [40, 10], 8, 2, 64
     q, kc, vc, tables, _, cu = _case(8, q_lens, kv_lens, hq, hk, dim, ps)
     seq = torch.tensor([40, 4], dtype=torch.int32)       # row 1: kv_len 4 < q_len 10
     flags = torch.zeros(1, dtype=torch.int32, device=dev)
@@ -112,7 +113,7 @@ def test_context_attention_error_paths(mas, dev):
     _check(bits(out), want)
     assert not out[20:26].any()                           # the tokens before position 0 get zeros
     bad = tables.clone()
-    bad[0, 2] = kc.shape[0] + 3                           # positions 16..23 of row 0 point past the cache
+    bad[0, 16 // ps] = kc.shape[0] + 3                    # the page of row 0's position 16 points past the cache
     flags.zero_()
     _run(mas, dev, q, kc, vc, bad, torch.tensor([40, 10], dtype=torch.int32), cu, 0.1, flags=flags)
     assert int(flags.item()) == 8
