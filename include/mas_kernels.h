@@ -230,7 +230,9 @@ int mas_embedding_fill_placeholders_bf16(void* out, int64_t out_stride, const vo
  * `workspace` (16-byte aligned, workspace_bytes long) holds the per-split partials: a split is
  * chunks_per_split chunks of 256 positions, with chunks_per_split the smallest power of two whose
  * partials fit (mas_paged_decode_attention_workspace_bytes), with at most 64 splits per row and
- * batch * num_kv_heads * splits within 16384 work items (longer splits past those). A page id
+ * batch * num_kv_heads * splits within 16384 work items (longer splits past those). Grids of fewer
+ * such items than the GPU has SIMDs split rows into 128 or 64 positions instead (at most 128 splits
+ * per row), when the workspace holds those partials. A page id
  * outside [0, num_pages) skips its position (MAS_ERRBIT_PAGE); a seq_len outside
  * [0, max_blocks * page_size] is clamped (MAS_ERRBIT_POSITION); a row with no position gets zeros.
  * With out_fp8, `out` receives e4m3fn codes (strides in elements, as for bf16): the output is

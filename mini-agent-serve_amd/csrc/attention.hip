@@ -8,9 +8,9 @@
 // in fp32 from the bf16 inputs, rounded once to bf16.
 //
 // Split-KV in two kernels:
-//  1. decode_attn_split - one wavefront per (kv head, split of chunks_per_split * 256 positions,
-//     row), kv heads adjacent in the grid so that the 256-byte slices of each 2 KB position block
-//     are read close together. The split is walked in steps of 32 positions with the next step's
+//  1. decode_attn_split - one wavefront per (kv head, split of split_len positions, row), kv heads
+//     adjacent in the grid so that the 256-byte slices of each 2 KB position block are read close
+//     together. The split is walked in steps of 32 positions with the next step's
 //     key and value loads in flight: Q.K^T on MFMA (v_mfma_f32_16x16x32_bf16; the kv head's G
 //     query heads are the rows of A, zero-padded to 16; 16 positions per tile are the
 //     columns of B, read straight from the cache rows), an online softmax in the MFMA result
@@ -42,7 +42,8 @@ struct DecodeArgs {
   const int32_t* block_tables;
   int64_t bt_stride, max_blocks;
   const int32_t* seq_lens;
-  int hq, hk, group, log2_page, chunks_per_split, max_splits;
+  int hq, hk, group, log2_page, max_splits;
+  int split_len;     // positions per split: 64, 128, or a multiple of the 256-position chunk
   float scale_log2;  // bmm1_scale * log2(e)
   float out_scale;   // bmm2_scale
   float* part_o;     // [batch][hq][max_splits][D]
@@ -204,7 +205,8 @@ __device__ __forceinline__ void issue_step(const DecodeArgs& a, StepLoads<D>& st
   }
 }
 
-// One wavefront per (kv head, split, row); a split is chunks_per_split chunks of 256 positions,
+// One wavefront per (kv head, split, row); a split is split_len positions (whole chunks of 256, or
+// 64 / 128 for small grids),
 // walked in steps of 32 with the next step's loads in flight (head_dim <= 128). Per step:
 // Q.K^T on MFMA -> online softmax (the running max, sum and O rescale live in the MFMA result
 // layout: lane (n, r) holds heads 4r..4r+3) -> P and the value rows through LDS, where they are
@@ -239,9 +241,9 @@ __global__ __launch_bounds__(64 * kAttnWaves, D <= 128 ? kAttnMinWaves : 1) void
   uint16_t(*p_lds)[16 * PROW] = p_lds_all[wave];
   int32_t* pg_lds = pg_lds_all[wave];
   const int L = kv_len(a, b);
-  const int start = split * a.chunks_per_split * kChunk;
+  const int start = split * a.split_len;
   if (start >= L) return;
-  const int end = min(start + a.chunks_per_split * kChunk, L);
+  const int end = min(start + a.split_len, L);
   const int G = a.group;
   const int n = lane & 15, r = lane >> 4;
   const int pv_d = lane % LPP, pv_grp = lane / LPP;
@@ -394,7 +396,7 @@ __global__ __launch_bounds__(64 * kAttnWaves, D <= 128 ? kAttnMinWaves : 1) void
   }
   if (__builtin_amdgcn_ballot_w64(bad) != 0 && lane == 0) report(a.err, MAS_ERRBIT_PAGE);
 
-  if (L <= a.chunks_per_split * kChunk) {
+  if (L <= a.split_len) {
     // The row's only split: its output is O / l * bmm2_scale, what merging one split gives.
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -465,7 +467,7 @@ __global__ __launch_bounds__(64) void decode_attn_combine(DecodeArgs a) {
   // reported at the end: a global atomic here would turn the loads below into waits on every load
   const bool len_bad = raw < 0 || raw > cap;
   const int L = static_cast<int>(raw < 0 ? 0 : (raw > cap ? cap : raw));
-  const int split_len = a.chunks_per_split * kChunk;
+  const int split_len = a.split_len;
   const int nsplit = (L + split_len - 1) / split_len;
   if (nsplit == 1) {  // the split kernel wrote this row's output
     if (len_bad && h == 0 && lane == 0) report(a.err, MAS_ERRBIT_POSITION);
@@ -581,6 +583,15 @@ int dispatch_group(const DecodeArgs& a, int64_t batch, int64_t hk, hipStream_t s
 }  // namespace
 }  // namespace mas
 
+namespace mas {
+namespace {
+// Workspace bytes of the partials: (max, sum) and an unnormalised O row per (row, query head, split).
+int64_t decode_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t head_dim, int64_t splits) {
+  return batch * num_q_heads * (splits > 0 ? splits : 1) * (head_dim + 2) * 4;
+}
+}  // namespace
+}  // namespace mas
+
 extern "C" int64_t mas_paged_decode_attention_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t head_dim,
                                                                int64_t max_blocks, int64_t page_size,
                                                                int64_t chunks_per_split) {
@@ -588,8 +599,7 @@ extern "C" int64_t mas_paged_decode_attention_workspace_bytes(int64_t batch, int
   if (batch < 0 || num_q_heads < 0 || head_dim <= 0 || max_blocks < 0 || page_size <= 0 || chunks_per_split < 1)
     return -1;
   const int64_t chunks = cdiv(max_blocks * page_size, kChunk);
-  const int64_t splits = cdiv(chunks, chunks_per_split);
-  return batch * num_q_heads * (splits > 0 ? splits : 1) * (head_dim + 2) * 4;
+  return decode_workspace_bytes(batch, num_q_heads, head_dim, cdiv(chunks, chunks_per_split));
 }
 
 namespace mas {
@@ -646,7 +656,22 @@ int decode_attention(void* out, int64_t out_stride, int64_t out_head_stride, con
   if (mas_paged_decode_attention_workspace_bytes(batch, num_q_heads, head_dim, max_blocks, page_size, per_split) >
       workspace_bytes)
     return kWorkspaceTooSmall;
-  const int64_t splits = chunks > 0 ? cdiv(chunks, per_split) : 1;
+  int64_t split_len = per_split * kChunk;
+  // Small grids: splits of 128 or 64 positions while the grid holds fewer work items than the GPU
+  // has SIMDs, at most 128 splits per row and within the workspace. A split of 256 positions is 8
+  // dependent steps; with few wavefronts those steps' latencies, not bandwidth, set the time (on
+  // MI355X: 16 rows of up to 512 positions 15.8 -> 10.1 us, one row of up to 4096 14.8 -> 9.6 us;
+  // at one item per SIMD and more, shorter splits lost: 64 rows of up to 512, 22.0 -> 23.5 us).
+  if (per_split == 1 && cap > 0) {
+    int cus = 0;
+    if (const int st = device_cu_count(&cus); st != MAS_OK) return st;
+    const int64_t simds = static_cast<int64_t>(cus) * 4;
+    while (split_len > 64 && batch * num_kv_heads * cdiv(cap, split_len) < simds &&
+           cdiv(cap, split_len / 2) <= 2 * kMaxRowSplits &&
+           decode_workspace_bytes(batch, num_q_heads, head_dim, cdiv(cap, split_len / 2)) <= workspace_bytes)
+      split_len /= 2;
+  }
+  const int64_t splits = cap > 0 ? cdiv(cap, split_len) : 1;
 
   int log2_page = 0;
   while ((int64_t{1} << log2_page) < page_size) ++log2_page;
@@ -668,7 +693,7 @@ int decode_attention(void* out, int64_t out_stride, int64_t out_head_stride, con
   a.hk = static_cast<int>(num_kv_heads);
   a.group = static_cast<int>(group);
   a.log2_page = log2_page;
-  a.chunks_per_split = static_cast<int>(per_split);
+  a.split_len = static_cast<int>(split_len);
   a.max_splits = static_cast<int>(splits);
   a.scale_log2 = bmm1_scale * 1.4426950408889634f;
   a.out_scale = bmm2_scale;

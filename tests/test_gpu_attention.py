@@ -95,6 +95,22 @@ def test_decode_attention_single_and_multi_split_rows(mas, dev):
         _check(bits(out), want)
 
 
+@pytest.mark.parametrize("batch,hq,hk,page_size,lens", [
+    (1, 32, 8, 256, [4096]),              # one row: 64 splits of 64 positions (big pages)
+    (2, 96, 8, 16, [2000, 129]),          # 123B heads, small pages: block-table entries from mid-chunk starts
+    (3, 16, 2, 64, [63, 64, 65]),         # rows at the edge of one short split
+])
+def test_decode_attention_small_grids_take_short_splits(mas, dev, batch, hq, hk, page_size, lens):
+    """Grids of fewer (row, kv head, split) items than the GPU has SIMDs split rows into 128- or
+    64-position pieces (more wavefronts, fewer dependent steps each); results as the oracle's."""
+    q, kc, vc, tables, seq = _case(50 + batch, batch, hq, hk, 128, page_size, lens)
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = _run(mas, dev, q, kc, vc, tables, seq, 0.088, flags=flags)
+    want = ops.paged_decode_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), 0.088)
+    _check(bits(out), want)
+    assert int(flags.item()) == 0
+
+
 def test_decode_attention_long_splits_and_bmm2_scale(mas, dev):
     """A workspace too small for one split per 256 positions makes each wavefront walk several
     chunks, merging them with the running max: same results as the oracle."""
