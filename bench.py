@@ -764,7 +764,7 @@ def context_main(mas, args, shape, dev) -> int:
     out = torch.empty_like(inp.q)
     flops = wl.context_flops(shape)
     scale = shape.head_dim ** -0.5
-    ws = torch.empty(16, dtype=torch.uint8, device=dev)
+    ws = torch.empty(128 << 20, dtype=torch.uint8, device=dev)  # the reference's workspace (devstral2.py:35)
 
     def call():
         mas.attention.trtllm_batch_context_with_kv_cache(inp.q, (inp.k_cache, inp.v_cache), ws, inp.block_tables,

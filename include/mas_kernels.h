@@ -264,6 +264,14 @@ int mas_paged_decode_attention_bf16(void* out, int64_t out_stride, int64_t out_h
  * [q_len, max_blocks * page_size] is clamped (MAS_ERRBIT_POSITION; tokens left before position 0
  * get zeros); a page id outside [0, num_pages) skips its position (MAS_ERRBIT_PAGE).
  * out_fp8 / out_scale_dev / out_scale_host: the fp8 output as for mas_paged_decode_attention_bf16.
+ * `workspace` (16-byte aligned, workspace_bytes long; NULL / 0 for none; its contents on entry do
+ * not matter): when the grid (kv heads x token tiles of max_q_len x rows) has fewer workgroups
+ * than the GPU has CUs, each token tile's key range is split over up to 16 workgroups whose
+ * partials go here - rows * ceil(max_q_len / tile) * tile * num_q_heads * splits * (head_dim + 2)
+ * * 4 bytes, tile = 32 tokens x (workgroup wavefronts / heads per workgroup) - and a second kernel
+ * merges them; with less workspace, fewer splits or none. max_kv_len (<= 0: none) is a hint that
+ * sizes the splits (they divide max_kv_len evenly, else the block table's reach); a longer row is
+ * still attended in full, its last split taking the rest.
  * Replaces flashinfer.prefill.trtllm_batch_context_with_kv_cache at
  * miniagentserve/models/devstral2/devstral2.py:198-213 (kv_layout "NHD", no sliding window).
  */
@@ -273,10 +281,10 @@ int mas_paged_context_attention_bf16(void* out, int64_t out_stride, int64_t out_
                                      int64_t head_stride, int64_t num_pages, int64_t page_size,
                                      const int32_t* block_tables, int64_t block_table_stride, int64_t max_blocks,
                                      const int32_t* seq_lens, const int32_t* cu_seqlens_q, int64_t num_rows,
-                                     int64_t max_q_len, int64_t num_q_heads, int64_t num_kv_heads,
+                                     int64_t max_q_len, int64_t max_kv_len, int64_t num_q_heads, int64_t num_kv_heads,
                                      int64_t head_dim, float bmm1_scale, float bmm2_scale, int out_fp8,
-                                     const float* out_scale_dev, float out_scale_host, uint32_t* err,
-                                     hipStream_t stream);
+                                     const float* out_scale_dev, float out_scale_host, void* workspace,
+                                     int64_t workspace_bytes, uint32_t* err, hipStream_t stream);
 
 /*
  * mas_paged_decode_attention_bf16 without a workspace argument: the same kernels and results, with

@@ -200,19 +200,20 @@ def _(query, k_cache, v_cache, workspace, block_tables, seq_lens, bmm1_scale, bm
     return None
 
 
-@custom_op("mas::paged_context_attention", mutates_args=("out", "error_flags"))
-def _paged_context_attention(query: Tensor, k_cache: Tensor, v_cache: Optional[Tensor], block_tables: Tensor,
-                             seq_lens: Tensor,
-                             cu_seqlens_q: Tensor, max_q_len: int, bmm1_scale: float, bmm2_scale: float, out: Tensor,
-                             kv_layout: str, quant_scale: Optional[Tensor], quant_scale_host: float,
-                             error_flags: Optional[Tensor]) -> None:
+@custom_op("mas::paged_context_attention", mutates_args=("workspace", "out", "error_flags"))
+def _paged_context_attention(query: Tensor, k_cache: Tensor, v_cache: Optional[Tensor], workspace: Optional[Tensor],
+                             block_tables: Tensor, seq_lens: Tensor,
+                             cu_seqlens_q: Tensor, max_q_len: int, max_kv_len: int, bmm1_scale: float,
+                             bmm2_scale: float, out: Tensor, kv_layout: str, quant_scale: Optional[Tensor],
+                             quant_scale_host: float, error_flags: Optional[Tensor]) -> None:
     attention._context(query, _cache(k_cache, v_cache), block_tables, seq_lens, cu_seqlens_q, max_q_len, bmm1_scale,
-                       bmm2_scale, out, kv_layout, error_flags, _quant_scale(quant_scale, quant_scale_host))
+                       bmm2_scale, out, kv_layout, error_flags, _quant_scale(quant_scale, quant_scale_host),
+                       workspace, max_kv_len)
 
 
 @_paged_context_attention.register_fake
-def _(query, k_cache, v_cache, block_tables, seq_lens, cu_seqlens_q, max_q_len, bmm1_scale, bmm2_scale, out,
-      kv_layout, quant_scale, quant_scale_host, error_flags):
+def _(query, k_cache, v_cache, workspace, block_tables, seq_lens, cu_seqlens_q, max_q_len, max_kv_len, bmm1_scale,
+      bmm2_scale, out, kv_layout, quant_scale, quant_scale_host, error_flags):
     return None
 
 

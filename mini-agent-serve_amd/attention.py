@@ -167,7 +167,7 @@ def trtllm_batch_decode_with_kv_cache(query: torch.Tensor, kv_cache, workspace_b
 
 
 def _context(query, kv_cache, block_tables, seq_lens, cu_seqlens_q, max_q_len, bmm1_scale, bmm2_scale, out,
-             kv_layout, error_flags, quant_scale=None) -> None:
+             kv_layout, error_flags, quant_scale=None, workspace=None, max_kv_len=0) -> None:
     k_cache, v_cache, pstride, estride, hstride, pages, page_size, hk, dim = _cache_geometry(kv_cache, kv_layout)
     for name, t in (("query", query), ("out", out), ("block_tables", block_tables), ("seq_lens", seq_lens),
                     ("cum_seq_lens_q", cu_seqlens_q)):
@@ -200,12 +200,19 @@ def _context(query, kv_cache, block_tables, seq_lens, cu_seqlens_q, max_q_len, b
         raise ValueError("block_tables must be [rows, max_blocks] int32 with a contiguous last dimension")
     if seq_lens.dim() != 1 or seq_lens.shape[0] < rows or not seq_lens.is_contiguous():
         raise ValueError("seq_lens must be a contiguous int32 [rows] tensor")
+    ws_ptr, ws_bytes = None, 0
+    if workspace is not None:
+        require_gpu(workspace, "workspace_buffer")
+        require_same_device(("query", query), ("workspace_buffer", workspace))
+        if not workspace.is_contiguous():
+            raise ValueError("workspace_buffer must be contiguous")
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     st = _lib.load().mas_paged_context_attention_bf16(
         out.data_ptr(), out.stride(0), out.stride(1), query.data_ptr(), query.stride(0), query.stride(1),
         k_cache.data_ptr(), v_cache.data_ptr(), pstride, estride, hstride, pages, page_size, block_tables.data_ptr(),
         block_tables.stride(0), block_tables.shape[1], seq_lens.data_ptr(), cu_seqlens_q.data_ptr(), rows,
-        int(max_q_len), hq, hk, dim, float(bmm1_scale), float(bmm2_scale), out_fp8, scale_ptr, scale_host,
-        error_word(error_flags, device), _lib.stream_handle(device))
+        int(max_q_len), int(max_kv_len), hq, hk, dim, float(bmm1_scale), float(bmm2_scale), out_fp8, scale_ptr, scale_host, ws_ptr,
+        ws_bytes, error_word(error_flags, device), _lib.stream_handle(device))
     _lib.check(st, "trtllm_batch_context_with_kv_cache")
 
 
@@ -223,10 +230,14 @@ def trtllm_batch_context_with_kv_cache(query: torch.Tensor, kv_cache, workspace_
     positions) over their paged KV. Returns ``out`` (allocated when not given), bf16
     ``[tokens, num_q_heads, head_dim]``, or its fp8 quantize with ``out_quant_scale``.
 
-    ``max_q_len`` must bound every row's query length (it sizes the grid); ``max_kv_len``,
-    ``cum_seq_lens_kv`` and ``workspace_buffer`` are accepted and unused (the kernel needs no
-    workspace). Not supported (raise): a sliding window, attention sinks, block-scaled outputs.
-    ``enable_pdl`` is ignored.
+    ``max_q_len`` must bound every row's query length (it sizes the grid); ``cum_seq_lens_kv`` is
+    accepted and unused. ``workspace_buffer`` (or None) holds split-KV partials when the grid is
+    small (few new tokens after a long cached prefix): each token tile's key range is then split
+    over several workgroups and merged by a second kernel; its contents on entry do not matter, and
+    with too little of it the kernel splits less or not at all. ``max_kv_len`` sizes those splits
+    (a hint: a longer row is still attended in full, only less evenly split). Not
+    supported (raise): a sliding window, attention sinks, block-scaled outputs. ``enable_pdl`` is
+    ignored.
     """
     if window_left != -1:
         raise ValueError("sliding-window attention (window_left != -1) is not supported")
@@ -237,16 +248,16 @@ def trtllm_batch_context_with_kv_cache(query: torch.Tensor, kv_cache, workspace_
         raise TypeError("bmm1_scale and bmm2_scale must be Python floats")
     if cum_seq_lens_q.shape[0] != batch_size + 1:
         raise ValueError(f"cum_seq_lens_q has {cum_seq_lens_q.shape[0]} entries, expected batch_size + 1")
-    del workspace_buffer, max_kv_len, cum_seq_lens_kv, enable_pdl
+    del cum_seq_lens_kv, enable_pdl
     if out is None:
         out = torch.empty(query.shape, dtype=dtype, device=query.device)
     if torch.compiler.is_compiling():
         k_cache, v_cache = (kv_cache if isinstance(kv_cache, (tuple, list)) else (kv_cache, None))
         qs, qs_host = _custom_op_scale(out_quant_scale)
-        torch.ops.mas.paged_context_attention(query, k_cache, v_cache, block_tables, seq_lens, cum_seq_lens_q,
-                                              int(max_q_len), float(bmm1_scale), float(bmm2_scale), out, kv_layout,
-                                              qs, qs_host, error_flags)
+        torch.ops.mas.paged_context_attention(query, k_cache, v_cache, workspace_buffer, block_tables, seq_lens,
+                                              cum_seq_lens_q, int(max_q_len), int(max_kv_len), float(bmm1_scale),
+                                              float(bmm2_scale), out, kv_layout, qs, qs_host, error_flags)
         return out
     _context(query, kv_cache, block_tables, seq_lens, cum_seq_lens_q, max_q_len, bmm1_scale, bmm2_scale, out,
-             kv_layout, error_flags, out_quant_scale)
+             kv_layout, error_flags, out_quant_scale, workspace_buffer, max_kv_len)
     return out

@@ -56,19 +56,6 @@ struct DecodeArgs {
   uint32_t* err;
 };
 
-__device__ __forceinline__ float row_max16(float v) {
-  v = fmaxf(v, dpp_move<0xb1>(v));   // quad_perm [1,0,3,2]
-  v = fmaxf(v, dpp_move<0x4e>(v));   // quad_perm [2,3,0,1]
-  v = fmaxf(v, dpp_move<0x141>(v));  // row_half_mirror
-  return fmaxf(v, dpp_move<0x140>(v));  // row_mirror
-}
-
-__device__ __forceinline__ float row_sum16(float v) {
-  v += dpp_move<0xb1>(v);
-  v += dpp_move<0x4e>(v);
-  v += dpp_move<0x141>(v);
-  return v + dpp_move<0x140>(v);
-}
 
 // seq_lens[b] clamped to [0, max_blocks * page_size].
 __device__ __forceinline__ int kv_len(const DecodeArgs& a, int b) {

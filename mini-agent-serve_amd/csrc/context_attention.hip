@@ -23,6 +23,8 @@
 //   a, a + 4, a + 8, a + 12 point at), two per operand, in the position order the packing implies.
 // Tiles are software-pipelined over two LDS buffers: while tile i is in the softmax, tile i + 1's
 // score MFMAs run and tile i + 2's key and value loads are in flight.
+#include <algorithm>
+
 #include "device.h"
 
 namespace mas {
@@ -30,6 +32,7 @@ namespace {
 
 constexpr int kTileP = 64;        // key positions per tile
 constexpr int kRowsPerWave = 32;  // query rows (tokens of one head) per wavefront
+constexpr int kMaxCtxSplits = 16;  // split-KV: key-range splits per token tile, at most
 constexpr float kNegInf = -__builtin_huge_valf();
 
 struct ContextArgs {
@@ -43,6 +46,13 @@ struct ContextArgs {
   const int32_t* seq_lens;
   const int32_t* cu_seqlens_q;
   int hq, hk, group, heads_per_wg, log2_page;
+  // Split-KV (kv_splits > 1, for grids smaller than one round of resident workgroups): split s of a
+  // token tile walks key tiles [s * split_tiles, (s + 1) * split_tiles) (the last split: to the
+  // end) and writes its (max, sum, unnormalised O) per (token, head) to part_ml / part_o, indexed by
+  // (row * row_tokens + token, head, split); context_combine merges them.
+  int kv_splits, split_tiles, row_tokens;
+  float* part_o;
+  float* part_ml;
   float scale_log2;
   float out_scale;
   void* out;                // bf16, or fp8 e4m3fn codes when out_fp8
@@ -80,7 +90,8 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
 // software pipeline, which the scalar reads do not.
 constexpr int kPagesLane = 0, kPagesStep = 1, kPagesTile = 2, kPagesStep1 = 3;
 
-template <int D, int kPages, int kWaves>
+// kSplit: a split-KV launch (a separate instance, so that the one-kernel instances keep their code).
+template <int D, int kPages, int kWaves, bool kSplit>
 __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextArgs a) {
   constexpr int kCtxWaves = kWaves;
   constexpr int kCtxThreads = 64 * kWaves;
@@ -100,7 +111,8 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   const int n = lane & 31, hf = lane >> 5;  // this lane's query row (token) and lane half
   const int hgroups = (a.group + a.heads_per_wg - 1) / a.heads_per_wg;
   const int kvh = blockIdx.x / hgroups, hg = blockIdx.x - kvh * hgroups;
-  const int row = blockIdx.z;
+  const int row = kSplit ? blockIdx.z / a.kv_splits : blockIdx.z;
+  const int split = kSplit ? blockIdx.z - row * a.kv_splits : 0;
   const int q0 = a.cu_seqlens_q[row], q_len = a.cu_seqlens_q[row + 1] - q0;
   const int tokens_per_wg = kRowsPerWave * (kCtxWaves / a.heads_per_wg);
   // Token tiles in reverse launch order: the last tiles reach the most positions, so they start first.
@@ -145,6 +157,13 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   const int last_tok = min(tile_tok + tokens_per_wg, q_len) - 1;
   const int reach = shift + last_tok + 1;  // <= kv_len
   const int ntiles = reach > 0 ? (reach + kTileP - 1) / kTileP : 0;
+  // This workgroup's key tiles: all of them, or its split's share.
+  const int it_begin = kSplit ? split * a.split_tiles : 0;
+  const int it_end = !kSplit || split == a.kv_splits - 1 ? ntiles : min(ntiles, it_begin + a.split_tiles);
+  if (kSplit && it_begin >= it_end) {  // an empty split (uniform): the merge skips it
+    if (len_bad && tid == 0 && blockIdx.x == 0 && tile_idx == 0 && split == 0) report(a.err, MAS_ERRBIT_POSITION);
+    return;
+  }
 
   float m_run = kNegInf, l_run = 0.f;  // token n's running max (raw score units) and sum
   f32x16 acc[DB];                      // O^T: element j of block db holds O[token n][32 db + 8 (j/4) + 4 hf + j%4]
@@ -384,21 +403,21 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   // Buffer it & 1 holds tile it, buffer (it + 1) & 1 tile it + 1 (staged after the barrier that
   // ends every read of tile it - 1, which used that buffer).
   f32x16 s_a[2], s_b[2];
-  if (ntiles > 0) {
-    issue_tile(tr, 0);
-    stage(tr, 0);
+  if (it_begin < it_end) {
+    issue_tile(tr, it_begin * kTileP);
+    stage(tr, it_begin & 1);
     __syncthreads();
-    if (ntiles > 1) issue_tile(tr, kTileP);
-    if (wave_live) scores(0, s_a);
+    if (it_begin + 1 < it_end) issue_tile(tr, (it_begin + 1) * kTileP);
+    if (wave_live) scores(it_begin & 1, s_a);
   }
   // One tile; `cur` holds its scores, `nxt` receives the next tile's. Called with the two score
   // arrays in turn (no copy between them).
   auto step = [&](int it, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
     const int buf = it & 1;
     __syncthreads();  // tile it - 1's reads (of buffer buf ^ 1) are done
-    if (it + 1 < ntiles) stage(tr, buf ^ 1);
+    if (it + 1 < it_end) stage(tr, buf ^ 1);
     __syncthreads();
-    if (it + 2 < ntiles) issue_tile(tr, (it + 2) * kTileP);
+    if (it + 2 < it_end) issue_tile(tr, (it + 2) * kTileP);
     if (wave_live) {
       mask(cur, it * kTileP);
       bf16x8 pbo[4];
@@ -408,18 +427,34 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
       pv(buf, pbo);
     }
   };
-  int it = 0;
-  for (; it + 1 < ntiles; it += 2) {
+  int it = it_begin;
+  for (; it + 1 < it_end; it += 2) {
     step(it, s_a, s_b);
     step(it + 1, s_b, s_a);
   }
-  if (it < ntiles) step(it, s_a, s_b);
+  if (it < it_end) step(it, s_a, s_b);
   if (__builtin_amdgcn_ballot_w64(page_bad) != 0 && lane == 0) report(a.err, MAS_ERRBIT_PAGE);
-  if (len_bad && tid == 0 && blockIdx.x == 0 && blockIdx.y == 0) report(a.err, MAS_ERRBIT_POSITION);
+  // reported by the workgroup of token tile 0, which every row with a query token has
+  if (len_bad && tid == 0 && blockIdx.x == 0 && tile_idx == 0) report(a.err, MAS_ERRBIT_POSITION);
 
   if (!wave_live) return;
   const int t = tok + n;
   if (t >= q_len) return;
+  if constexpr (kSplit) {
+    // ---- this split's partial: O row (lane half hf holds columns 32 db + 8 q + 4 hf .. + 3) and
+    // (max, sum), both halves holding the same (max, sum)
+    const int64_t pi = ((static_cast<int64_t>(row) * a.row_tokens + t) * a.hq + h) * a.kv_splits + split;
+    float* po = a.part_o + pi * D + 4 * hf;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x16& o = acc[db];
+        *reinterpret_cast<f32x4*>(po + 32 * db + 8 * q) = f32x4{o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]};
+      }
+    if (hf == 0) *reinterpret_cast<f32x2*>(a.part_ml + pi * 2) = f32x2{m_run, l_run};
+    return;
+  }
   // ---- out[token][h][32 db + 8 q + 4 hf + i] = O / l * bmm2_scale (bf16), or its fp8 quantize
   const float qs = a.out_fp8 ? (a.quant_scale_dev != nullptr ? *a.quant_scale_dev : a.quant_scale_host) : 1.f;
   const float rcp = 1.0f / qs;
@@ -445,6 +480,122 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   }
 }
 
+// One wavefront per (row, token, query head) of a split-KV launch: merges the token's non-empty
+// splits with weights 2^(c (m_s - max m)) (c = bmm1_scale * log2 e, maxima in raw score units as
+// the split kernel keeps them) and writes O / l * bmm2_scale as bf16, or its fp8 quantize. Every
+// load is issued in one round trip: lane s reads split s's (max, sum) and all kMaxCtxSplits
+// partial O rows are loaded (indices past the last split clamped to it, weighted 0) before the
+// max is known. A token that sees no position (all maxima -inf) gets zeros.
+template <int D>
+__global__ __launch_bounds__(64) void context_combine(ContextArgs a, int tokens_per_wg) {
+  constexpr int DPL = D / 64;  // head-dim elements per lane
+  const int lane = threadIdx.x;
+  const int id = static_cast<int>(blockIdx.x);  // < rows * row_tokens * hq <= 2^31 - 1 (host-checked)
+  const int rt = id / a.hq, h = id - rt * a.hq;
+  const int row = rt / a.row_tokens, t = rt - row * a.row_tokens;
+  const int q0 = a.cu_seqlens_q[row], q_len = a.cu_seqlens_q[row + 1] - q0;
+  if (t >= q_len) return;
+  // the token tile's key tiles, as the split kernel counts them
+  const int64_t cap = a.max_blocks << a.log2_page;
+  const int64_t raw_len = a.seq_lens[row];
+  const int kv_len = static_cast<int>(raw_len < 0 ? 0 : (raw_len > cap ? cap : raw_len));
+  const int tile_tok = t / tokens_per_wg * tokens_per_wg;
+  const int reach = kv_len - q_len + min(tile_tok + tokens_per_wg, q_len);
+  const int ntiles = reach > 0 ? (reach + kTileP - 1) / kTileP : 0;
+  const int nsplit = min(a.kv_splits, (ntiles + a.split_tiles - 1) / a.split_tiles);  // <= kMaxCtxSplits
+  const int64_t base = ((static_cast<int64_t>(row) * a.row_tokens + t) * a.hq + h) * a.kv_splits;
+  float acc[DPL], l = 0.f;
+#pragma unroll
+  for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
+  if (nsplit > 0) {
+    const int sl = lane < nsplit ? lane : nsplit - 1;
+    const f32x2 ml = *reinterpret_cast<const f32x2*>(a.part_ml + (base + sl) * 2);
+    const float* po = a.part_o + base * D + DPL * lane;
+    float v[kMaxCtxSplits][DPL];
+#pragma unroll
+    for (int u = 0; u < kMaxCtxSplits; ++u) {
+      const float* src = po + min(u, nsplit - 1) * D;
+      if constexpr (DPL == 2) {
+        const f32x2 x = *reinterpret_cast<const f32x2*>(src);
+        v[u][0] = x[0];
+        v[u][1] = x[1];
+      } else {
+        v[u][0] = src[0];
+      }
+    }
+    const float m_lane = lane < nsplit ? ml[0] : kNegInf;
+    const float mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, row_max16(m_lane)), 0));
+    if (mx != kNegInf) {
+      const float c = a.scale_log2;
+      const float wgt = lane < nsplit ? __builtin_amdgcn_exp2f(__builtin_fmaf(m_lane, c, -mx * c)) : 0.f;
+      l = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, row_sum16(wgt * ml[1])), 0));
+      // every split slot, in order: the weight is 0 past the last split (its value a finite copy)
+#pragma unroll
+      for (int u = 0; u < kMaxCtxSplits; ++u) {
+        const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wgt), u));
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) acc[e] = __builtin_fmaf(wj, v[u][e], acc[e]);
+      }
+    }
+  }
+  const float sc = l > 0.f ? a.out_scale / l : 0.f;
+  const int64_t at = static_cast<int64_t>(q0 + t) * a.out_stride + h * a.out_head_stride + DPL * lane;
+  uint32_t y[(DPL + 1) / 2];
+  if constexpr (DPL == 1) {
+    y[0] = pack_bf16x2(acc[0] * sc, 0.f);
+  } else {
+#pragma unroll
+    for (int e = 0; e < DPL / 2; ++e) y[e] = pack_bf16x2(acc[2 * e] * sc, acc[2 * e + 1] * sc);
+  }
+  if (a.out_fp8) {
+    // the quantize the reference applies to the bf16 attention output (devstral2.py:93-95,110-111)
+    const float qs = a.quant_scale_dev != nullptr ? *a.quant_scale_dev : a.quant_scale_host;
+    const float rcp = 1.0f / qs;
+    float qv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int ee = e < DPL ? e : 0;
+      qv[e] = div_by_scale((ee & 1) ? bf16_hi(y[ee / 2]) : bf16_lo(y[ee / 2]), qs, rcp);
+    }
+    const uint32_t codes = fp8x4_saturate_encode(qv[0], qv[1], qv[2], qv[3]);
+    uint8_t* dst = static_cast<uint8_t*>(a.out) + at;
+    if constexpr (DPL == 1) {
+      dst[0] = static_cast<uint8_t>(codes);
+    } else {
+      *reinterpret_cast<uint16_t*>(dst) = static_cast<uint16_t>(codes);
+    }
+  } else {
+    uint16_t* dst = static_cast<uint16_t*>(a.out) + at;
+    if constexpr (DPL == 1) {
+      dst[0] = static_cast<uint16_t>(y[0]);
+    } else {
+      *reinterpret_cast<uint32_t*>(dst) = y[0];
+    }
+  }
+}
+
+template <int D, int kWaves, bool kSplit>
+void launch_context_mode(int mode, dim3 grid, dim3 block, hipStream_t stream, const ContextArgs& a) {
+  if (mode == kPagesTile) hipLaunchKernelGGL((context_attn<D, kPagesTile, kWaves, kSplit>), grid, block, 0, stream, a);
+  else if (mode == kPagesStep1)
+    hipLaunchKernelGGL((context_attn<D, kPagesStep1, kWaves, kSplit>), grid, block, 0, stream, a);
+  else if (mode == kPagesStep)
+    hipLaunchKernelGGL((context_attn<D, kPagesStep, kWaves, kSplit>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((context_attn<D, kPagesLane, kWaves, kSplit>), grid, block, 0, stream, a);
+}
+
+template <bool kSplit>
+void launch_context(int64_t head_dim, int waves, int mode, dim3 grid, dim3 block, hipStream_t stream,
+                    const ContextArgs& a) {
+  if (head_dim == 64) {
+    if (waves == 8) launch_context_mode<64, 8, kSplit>(mode, grid, block, stream, a);
+    else launch_context_mode<64, 4, kSplit>(mode, grid, block, stream, a);
+  } else {
+    if (waves == 8) launch_context_mode<128, 8, kSplit>(mode, grid, block, stream, a);
+    else launch_context_mode<128, 4, kSplit>(mode, grid, block, stream, a);
+  }
+}
+
 }  // namespace
 }  // namespace mas
 
@@ -455,13 +606,13 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
                                                 const int32_t* block_tables, int64_t block_table_stride,
                                                 int64_t max_blocks, const int32_t* seq_lens,
                                                 const int32_t* cu_seqlens_q, int64_t num_rows, int64_t max_q_len,
-                                                int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                                                int64_t max_kv_len, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
                                                 float bmm1_scale, float bmm2_scale, int out_fp8,
-                                                const float* out_scale_dev, float out_scale_host, uint32_t* err,
-                                                hipStream_t stream) {
+                                                const float* out_scale_dev, float out_scale_host, void* workspace,
+                                                int64_t workspace_bytes, uint32_t* err, hipStream_t stream) {
   using namespace mas;
   if (num_rows < 0 || max_q_len < 0 || num_q_heads < 0 || num_kv_heads < 0 || num_pages < 0 || page_size <= 0 ||
-      max_blocks < 0)
+      max_blocks < 0 || workspace_bytes < 0)
     return MAS_ERR_INVALID_VALUE;
   if (num_rows == 0 || max_q_len == 0 || num_q_heads == 0) return MAS_OK;
   if (num_kv_heads == 0 || num_q_heads % num_kv_heads != 0) return MAS_ERR_INVALID_VALUE;
@@ -485,6 +636,33 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   const int64_t tokens_per_wg = kRowsPerWave * (waves / heads_per_wg);
   const int64_t gx = num_kv_heads * hgroups, gy = cdiv(max_q_len, tokens_per_wg);
   if (gx > INT32_MAX || gy > 65535) return MAS_ERR_UNSUPPORTED;
+
+  // Split-KV for grids of fewer workgroups than CUs (few new tokens after a long cached prefix):
+  // each token tile's key range is split over up to kMaxCtxSplits workgroups of at least 4 key
+  // tiles each, aiming at two rounds of resident workgroups, when the workspace holds the partials
+  // (workspace_bytes 0: no split). The splits divide max_kv_len (if positive, else the block
+  // table's reach) evenly; a longer row's last split takes the rest, so the hint sizes the work
+  // and never bounds it. On MI355X, one row of 128 new tokens after 4096 cached positions (32
+  // workgroups of 66 tiles) took 115 us unsplit and 37 us in 14 splits; a grid with a workgroup
+  // on every CU gained nothing from splitting (4 rows of 256 after 8192: 256 workgroups, 237 us
+  // either way), the partials' traffic eating what a second workgroup per CU brings.
+  const int64_t row_tokens = gy * tokens_per_wg;
+  auto partial_bytes = [&](int64_t splits) { return num_rows * row_tokens * num_q_heads * splits * (head_dim + 2) * 4; };
+  int64_t kv_splits = 1, split_tiles = 1;
+  const int64_t base_wgs = gx * gy * num_rows;
+  if (workspace != nullptr && workspace_bytes > 0 && (reinterpret_cast<uintptr_t>(workspace) & 15u) == 0) {
+    int cus = 0;
+    if (const int st = device_cu_count(&cus); st != MAS_OK) return st;
+    const int64_t resident = static_cast<int64_t>(cus) * (8 / waves);
+    const int64_t max_tiles = cdiv(cap, kTileP);
+    const int64_t hint_tiles = max_kv_len > 0 ? std::min(max_tiles, cdiv(max_kv_len, kTileP)) : max_tiles;
+    if (base_wgs < cus && num_rows * row_tokens * num_q_heads <= INT32_MAX) {
+      kv_splits = std::min<int64_t>({kMaxCtxSplits, cdiv(2 * resident, base_wgs), hint_tiles / 4, 65535 / num_rows});
+      while (kv_splits > 1 && partial_bytes(kv_splits) > workspace_bytes) --kv_splits;
+      if (kv_splits > 1) split_tiles = cdiv(hint_tiles, kv_splits);
+      else kv_splits = 1;
+    }
+  }
   int log2_page = 0;
   while ((int64_t{1} << log2_page) < page_size) ++log2_page;
   ContextArgs a{};
@@ -516,7 +694,12 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   a.quant_scale_dev = out_scale_dev;
   a.quant_scale_host = out_scale_host;
   a.err = err;
-  const dim3 grid(static_cast<uint32_t>(gx), static_cast<uint32_t>(gy), static_cast<uint32_t>(num_rows));
+  a.kv_splits = static_cast<int>(kv_splits);
+  a.split_tiles = static_cast<int>(split_tiles);
+  a.row_tokens = static_cast<int>(row_tokens);
+  a.part_o = static_cast<float*>(workspace);
+  a.part_ml = kv_splits > 1 ? a.part_o + num_rows * row_tokens * num_q_heads * kv_splits * head_dim : nullptr;
+  const dim3 grid(static_cast<uint32_t>(gx), static_cast<uint32_t>(gy), static_cast<uint32_t>(num_rows * kv_splits));
   // Page mode: a tile within one page, a thread-row step within one or two pages, or per lane.
   const int64_t pos_step = 64 * waves / (head_dim / 8);
   const int mode = page_size >= kTileP     ? kPagesTile
@@ -524,31 +707,15 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
                    : 2 * page_size >= pos_step ? kPagesStep
                                                : kPagesLane;
   const dim3 block(static_cast<uint32_t>(64 * waves));
-  auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, 0, stream, a); };
-  if (head_dim == 64) {
-    if (waves == 8) {
-      if (mode == kPagesTile) go(context_attn<64, kPagesTile, 8>);
-      else if (mode == kPagesStep1) go(context_attn<64, kPagesStep1, 8>);
-      else if (mode == kPagesStep) go(context_attn<64, kPagesStep, 8>);
-      else go(context_attn<64, kPagesLane, 8>);
-    } else {
-      if (mode == kPagesTile) go(context_attn<64, kPagesTile, 4>);
-      else if (mode == kPagesStep1) go(context_attn<64, kPagesStep1, 4>);
-      else if (mode == kPagesStep) go(context_attn<64, kPagesStep, 4>);
-      else go(context_attn<64, kPagesLane, 4>);
-    }
-  } else {
-    if (waves == 8) {
-      if (mode == kPagesTile) go(context_attn<128, kPagesTile, 8>);
-      else if (mode == kPagesStep1) go(context_attn<128, kPagesStep1, 8>);
-      else if (mode == kPagesStep) go(context_attn<128, kPagesStep, 8>);
-      else go(context_attn<128, kPagesLane, 8>);
-    } else {
-      if (mode == kPagesTile) go(context_attn<128, kPagesTile, 4>);
-      else if (mode == kPagesStep1) go(context_attn<128, kPagesStep1, 4>);
-      else if (mode == kPagesStep) go(context_attn<128, kPagesStep, 4>);
-      else go(context_attn<128, kPagesLane, 4>);
-    }
-  }
+  if (kv_splits > 1) launch_context<true>(head_dim, waves, mode, grid, block, stream, a);
+  else launch_context<false>(head_dim, waves, mode, grid, block, stream, a);
+  if (const int st = launch_status(); st != MAS_OK || kv_splits == 1) return st;
+  const int64_t merges = num_rows * row_tokens * num_q_heads;  // <= INT32_MAX when split
+  if (head_dim == 64)
+    hipLaunchKernelGGL(context_combine<64>, dim3(static_cast<uint32_t>(merges)), dim3(64), 0, stream, a,
+                       static_cast<int>(tokens_per_wg));
+  else
+    hipLaunchKernelGGL(context_combine<128>, dim3(static_cast<uint32_t>(merges)), dim3(64), 0, stream, a,
+                       static_cast<int>(tokens_per_wg));
   return launch_status();
 }

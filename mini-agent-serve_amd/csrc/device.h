@@ -111,6 +111,21 @@ __device__ __forceinline__ float dpp_move(float v) {
                                                                false));
 }
 
+// Max / sum over each row of 16 lanes; every lane of the row receives the result.
+__device__ __forceinline__ float row_max16(float v) {
+  v = fmaxf(v, dpp_move<0xb1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_move<0x4e>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_move<0x141>(v));  // row_half_mirror
+  return fmaxf(v, dpp_move<0x140>(v));  // row_mirror
+}
+
+__device__ __forceinline__ float row_sum16(float v) {
+  v += dpp_move<0xb1>(v);
+  v += dpp_move<0x4e>(v);
+  v += dpp_move<0x141>(v);
+  return v + dpp_move<0x140>(v);
+}
+
 // Sum over the 64 lanes of a wavefront; every lane receives the total. Rows of 16 lanes reduce
 // through DPP (quad_perm xor1, xor2, row_half_mirror, row_mirror), then the four row sums are
 // read out and added in a fixed order.

@@ -294,6 +294,11 @@ CONTEXT_SHAPES: dict[str, ContextShape] = {s.name: s for s in [
     ContextShape("context_attn_4x4096_123b", 4, 4096, 0, 96, 8, 128, 256),
     # the reference engine's default 16-slot pages (serving_engine.py:24)
     ContextShape("context_attn_4x2048_24b_p16", 4, 2048, 0, 32, 8, 128, 16),
+    # an agent turn: a few new tokens after a long cached conversation prefix (few token tiles, long
+    # key ranges: the split-KV shapes), 16-slot pages
+    ContextShape("context_attn_1x128_after4096_24b", 1, 128, 4096, 32, 8, 128, 16),
+    ContextShape("context_attn_4x256_after8192_24b", 4, 256, 8192, 32, 8, 128, 16),
+    ContextShape("context_attn_1x128_after4096_123b", 1, 128, 4096, 96, 8, 128, 16),
 ]}
 
 

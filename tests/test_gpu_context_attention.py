@@ -28,12 +28,22 @@ def _case(seed, q_lens, kv_lens, hq, hk, dim, page_size):
     return q, kc, vc, tables, torch.tensor(kv_lens, dtype=torch.int32), cu
 
 
-def _run(mas, dev, q, kc, vc, tables, seq, cu, scale, out=None, flags=None, scale2=1.0):
-    ws = torch.zeros(16, dtype=torch.uint8, device=dev)
+def _workspace(dev, nbytes):
+    """A workspace whose bytes are all 0xff (NaN as float32): its contents on entry must not matter."""
+    return torch.full((nbytes,), 255, dtype=torch.uint8, device=dev)
+
+
+SPLIT_WS = 256 << 20  # holds 16 splits' partials for every split case below
+
+
+def _run(mas, dev, q, kc, vc, tables, seq, cu, scale, out=None, flags=None, scale2=1.0, ws_bytes=16, max_kv=0,
+         quant=None):
+    ws = _workspace(dev, ws_bytes)
     max_q = int((cu[1:] - cu[:-1]).max()) if len(cu) > 1 else 0
     return mas.attention.trtllm_batch_context_with_kv_cache(
         q.to(dev) if q.device.type == "cpu" else q, (kc.to(dev), vc.to(dev)), ws, tables.to(dev), seq.to(dev),
-        max_q, 0, scale, scale2, len(cu) - 1, cu.to(dev), None, out=out, kv_layout="NHD", error_flags=flags)
+        max_q, max_kv, scale, scale2, len(cu) - 1, cu.to(dev), None, out=out, kv_layout="NHD", error_flags=flags,
+        out_quant_scale=quant)
 
 
 def _check(got, want, min_exact=0.6):
@@ -137,15 +147,16 @@ def test_context_attention_max_q_len_too_small_is_flagged(mas, dev):
     assert torch.all(out[32:40] == 7.0)
 
 
-def test_context_attention_in_graph_replays(mas, dev):
-    q_lens, kv_lens, hq, hk, dim, ps = [128, 64], [256, 64], 32, 8, 128, 64
+@pytest.mark.parametrize("kv0,ws_bytes", [(256, 16), (2048, SPLIT_WS)])  # one kernel; split-KV and its merge
+def test_context_attention_in_graph_replays(mas, dev, kv0, ws_bytes):
+    q_lens, kv_lens, hq, hk, dim, ps = [128, 64], [kv0, 64], 32, 8, 128, 64
     q, kc, vc, tables, seq, cu = _case(12, q_lens, kv_lens, hq, hk, dim, ps)
     qd, kd, vd, td, sd, cd = q.to(dev), kc.to(dev), vc.to(dev), tables.to(dev), seq.to(dev), cu.to(dev)
-    ws = torch.zeros(16, dtype=torch.uint8, device=dev)
+    ws = _workspace(dev, ws_bytes)
     out = torch.empty_like(qd)
 
     def call():
-        mas.attention.trtllm_batch_context_with_kv_cache(qd, (kd, vd), ws, td, sd, 128, 256, 0.088, 1.0, 2, cd,
+        mas.attention.trtllm_batch_context_with_kv_cache(qd, (kd, vd), ws, td, sd, 128, kv0, 0.088, 1.0, 2, cd,
                                                          None, out=out)
 
     call()
@@ -165,6 +176,10 @@ def test_context_attention_in_graph_replays(mas, dev):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, want)
+    if ws_bytes > 16:
+        got = bits(want)
+        ref = ops.paged_context_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), cu.numpy(), 0.088)
+        _check(got, ref)
 
 
 @pytest.mark.parametrize("dim,hq,hk,scale_kind", [(128, 32, 8, "tensor"), (64, 6, 2, "float")])
@@ -186,3 +201,106 @@ def test_context_attention_fp8_output_is_the_o_proj_quantize(mas, dev, dim, hq, 
         torch_q = (ref.float() / s).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
         assert torch.equal(out.view(torch.uint8), torch_q.view(torch.uint8))
     assert np.mean(np.abs(on.bf16_to_f32(bits(ref))) / 0.004 > 448.0) > 0.01
+
+
+def test_context_attention_short_row_position_error_is_flagged(mas, dev):
+    """A bad seq_len on a row with fewer query tokens than max_q_len (its later token tiles are
+    empty) is still flagged: tile 0's workgroup reports it."""
+    q_lens, kv_lens, hq, hk, dim, ps = [70, 10], [70, 10], 8, 2, 128, 16   # 3 token tiles of 32
+    q, kc, vc, tables, _, cu = _case(21, q_lens, kv_lens, hq, hk, dim, ps)
+    for row1 in (4, 10_000):                       # below q_len, past the block table's reach
+        seq = torch.tensor([70, row1], dtype=torch.int32)
+        flags = torch.zeros(1, dtype=torch.int32, device=dev)
+        out = _run(mas, dev, q, kc, vc, tables, seq, cu, 0.1, flags=flags)
+        assert int(flags.item()) == 2, row1
+        clamped = torch.tensor([70, min(row1, tables.shape[1] * ps)], dtype=torch.int32)
+        want = ops.paged_context_attention(bits(q), bits(kc), bits(vc), tables.numpy(), clamped.numpy(), cu.numpy(),
+                                           0.1)
+        _check(bits(out), want)
+
+
+# Split-KV (few new tokens after a long cached prefix: a grid smaller than one round of resident
+# workgroups, and a workspace): each token tile's keys are split over several workgroups and
+# merged by a second kernel. The split result differs from the one-kernel result in rounding
+# only, so the two are not bit-identical: that inequality shows the split path ran.
+SPLIT_CASES = [
+    # q_lens, kv_lens, hq, hk, dim, page_size, max_kv_len
+    ([128], [4224], 32, 8, 128, 16, 4224),                # 128 new tokens after 4096 cached, Devstral-Small-2 heads
+    ([64, 1, 9], [3000, 777, 9], 96, 8, 128, 256, 3000),  # the 123B head group, ragged rows
+    ([33], [1500], 16, 8, 64, 32, 1500),                  # head_dim 64, two heads per kv head
+    ([20, 7], [2000, 7], 24, 2, 128, 8, 2000),            # per-lane pages (8 slots), eight wavefronts
+    ([40], [2500], 8, 8, 128, 64, 0),                     # no max_kv_len: splits over the block table's reach
+    ([40], [2500], 8, 8, 128, 64, 1024),                  # max_kv_len below the real length: the last split takes the rest
+    ([96], [1200], 32, 8, 128, 128, 1200),                # pages of two tiles, three token tiles of 32
+]
+
+
+@pytest.mark.parametrize("q_lens,kv_lens,hq,hk,dim,page_size,max_kv", SPLIT_CASES)
+def test_context_attention_split_kv_matches_oracle(mas, dev, q_lens, kv_lens, hq, hk, dim, page_size, max_kv):
+    q, kc, vc, tables, seq, cu = _case(sum(kv_lens) + 7 * hq, q_lens, kv_lens, hq, hk, dim, page_size)
+    scale = dim ** -0.5
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = _run(mas, dev, q, kc, vc, tables, seq, cu, scale, flags=flags, ws_bytes=SPLIT_WS, max_kv=max_kv)
+    assert int(flags.item()) == 0
+    want = ops.paged_context_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), cu.numpy(), scale)
+    one_kernel = _run(mas, dev, q, kc, vc, tables, seq, cu, scale, max_kv=max_kv)
+    assert not torch.equal(out, one_kernel)
+    # Over thousands of positions the outputs are small averages and P's bf16 rounding leaves fewer
+    # of them bit-identical to the oracle: the split result must match as often as the one-kernel
+    # result does, less 2 points.
+    exact = np.mean(bits(out) == want)
+    exact_one = np.mean(bits(one_kernel) == want)
+    assert exact >= min(0.6, exact_one - 0.02), (exact, exact_one)
+    _check(bits(out), want, min_exact=0.0)
+    _check(bits(one_kernel), want, min_exact=0.0)
+
+
+def test_context_attention_split_kv_small_workspace(mas, dev):
+    """A workspace too small for 16 splits' partials gets fewer splits (here 3): still the oracle's
+    result; one too small for 2 gets the one-kernel result, bit for bit."""
+    q_lens, kv_lens, hq, hk, dim, ps = [32], [3000], 8, 8, 128, 16
+    q, kc, vc, tables, seq, cu = _case(5, q_lens, kv_lens, hq, hk, dim, ps)
+    want = ops.paged_context_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), cu.numpy(), 0.09)
+    one_kernel = _run(mas, dev, q, kc, vc, tables, seq, cu, 0.09, max_kv=3000)
+    per_split = 128 * hq * (dim + 2) * 4   # one token tile (one head per kv head: 4 wavefronts x 32 tokens)
+    three = _run(mas, dev, q, kc, vc, tables, seq, cu, 0.09, ws_bytes=3 * per_split + 100, max_kv=3000)
+    _check(bits(three), want)
+    assert not torch.equal(three, one_kernel)
+    full = _run(mas, dev, q, kc, vc, tables, seq, cu, 0.09, ws_bytes=SPLIT_WS, max_kv=3000)
+    assert not torch.equal(three, full)                   # 3 splits, not 16
+    tiny = _run(mas, dev, q, kc, vc, tables, seq, cu, 0.09, ws_bytes=2 * per_split - 16, max_kv=3000)
+    assert torch.equal(tiny, one_kernel)
+
+
+@pytest.mark.parametrize("ps", [8, 64])
+def test_context_attention_split_kv_error_paths(mas, dev, ps):
+    """Under split-KV: a row with kv_len < q_len (flag 2, zeros before position 0) and a page id past
+    the cache in a late split (flag 8, its positions skipped as the oracle skips them)."""
+    q_lens, kv_lens, hq, hk, dim = [20, 10], [2000, 10], 8, 2, 64
+    q, kc, vc, tables, _, cu = _case(9, q_lens, kv_lens, hq, hk, dim, ps)
+    seq = torch.tensor([2000, 4], dtype=torch.int32)
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = _run(mas, dev, q, kc, vc, tables, seq, cu, 0.1, flags=flags, ws_bytes=SPLIT_WS, max_kv=2000)
+    assert int(flags.item()) == 2
+    want = ops.paged_context_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), cu.numpy(), 0.1)
+    _check(bits(out), want)
+    assert not out[20:26].any()
+    bad = tables.clone()
+    bad[0, 1500 // ps] = kc.shape[0] + 3                  # the page of row 0's position 1500
+    flags.zero_()
+    _run(mas, dev, q, kc, vc, bad, torch.tensor([2000, 10], dtype=torch.int32), cu, 0.1, flags=flags,
+         ws_bytes=SPLIT_WS, max_kv=2000)
+    assert int(flags.item()) == 8
+
+
+@pytest.mark.parametrize("dim,hq,hk", [(128, 32, 8), (64, 6, 2)])
+def test_context_attention_split_kv_fp8_output(mas, dev, dim, hq, hk):
+    """The merge kernel's fp8 output is the o_proj input quantize of its own bf16 output, bit for bit."""
+    q_lens, kv_lens, ps = [40, 3], [1800, 3], 16
+    q, kc, vc, tables, seq, cu = _case(dim + 3 * hq, q_lens, kv_lens, hq, hk, dim, ps)
+    ref = _run(mas, dev, q, kc, vc, tables, seq, cu, 0.2, scale2=4.0, ws_bytes=SPLIT_WS, max_kv=1800)
+    for s in (0.004, 0.37):
+        out = _run(mas, dev, q, kc, vc, tables, seq, cu, 0.2, scale2=4.0, ws_bytes=SPLIT_WS, max_kv=1800,
+                   quant=torch.tensor(s, dtype=torch.float32, device=dev))
+        assert out.dtype == torch.float8_e4m3fn
+        np.testing.assert_array_equal(out.view(torch.uint8).cpu().numpy(), ops.quantize_activation(bits(ref), s))
