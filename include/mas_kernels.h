@@ -322,6 +322,16 @@ int mas_paged_decode_attention_bf16_noalloc(void* out, int64_t out_stride, int64
 int64_t mas_paged_decode_attention_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t head_dim,
                                                    int64_t max_blocks, int64_t page_size, int64_t chunks_per_split);
 
+/*
+ * Workspace bytes that let mas_paged_context_attention_bf16 split every small grid of these
+ * sizes the most (16 splits per token tile); less gets fewer splits or none. -1 for invalid
+ * arguments (num_q_heads not a multiple of num_kv_heads, head_dim not 64 or 128).
+ * No counterpart in the reference (its caller passes a fixed 128 MiB workspace,
+ * miniagentserve/models/devstral2/devstral2.py:36-42).
+ */
+int64_t mas_paged_context_attention_workspace_bytes(int64_t num_rows, int64_t max_q_len, int64_t num_q_heads,
+                                                    int64_t num_kv_heads, int64_t head_dim);
+
 #ifdef __cplusplus
 }
 #endif

@@ -53,12 +53,14 @@ _SIGNATURES: dict[str, list] = {
                                                 _i64, _i64, _i64, ctypes.c_float, ctypes.c_float, _i32, _c_void_p,
                                                 ctypes.c_float, _c_void_p, _c_void_p],
     "mas_paged_decode_attention_workspace_bytes": [_i64, _i64, _i64, _i64, _i64, _i64],
+    "mas_paged_context_attention_workspace_bytes": [_i64, _i64, _i64, _i64, _i64],
     "mas_paged_context_attention_bf16": [_c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64,
                                          _i64, _i64, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64,
                                          _i64, _i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_float, _i32, _c_void_p,
                                          ctypes.c_float, _c_void_p, _i64, _c_void_p, _c_void_p],
 }
-_RESTYPES = {"mas_status_string": ctypes.c_char_p, "mas_paged_decode_attention_workspace_bytes": ctypes.c_int64}
+_RESTYPES = {"mas_status_string": ctypes.c_char_p, "mas_paged_decode_attention_workspace_bytes": ctypes.c_int64,
+             "mas_paged_context_attention_workspace_bytes": ctypes.c_int64}
 
 ERROR_BITS = {
     1: "token id outside [0, vocab)",

@@ -26,7 +26,8 @@ from . import _lib
 from ._tensors import error_word, require_dtype, require_gpu, require_same_device
 from .page import _cache_geometry
 
-__all__ = ["trtllm_batch_decode_with_kv_cache", "trtllm_batch_context_with_kv_cache", "decode_workspace_bytes"]
+__all__ = ["trtllm_batch_decode_with_kv_cache", "trtllm_batch_context_with_kv_cache", "decode_workspace_bytes",
+           "context_workspace_bytes"]
 
 SUPPORTED_HEAD_DIMS = (64, 128, 256)
 FP8 = torch.float8_e4m3fn
@@ -73,6 +74,17 @@ def decode_workspace_bytes(batch: int, num_q_heads: int, head_dim: int, max_bloc
     16384 (row, kv head, split) work items make the kernel pick longer splits)."""
     n = _lib.load().mas_paged_decode_attention_workspace_bytes(batch, num_q_heads, head_dim, max_blocks, page_size,
                                                                 chunks_per_split)
+    if n < 0:
+        raise ValueError("invalid attention shape")
+    return n
+
+
+def context_workspace_bytes(num_rows: int, max_q_len: int, num_q_heads: int, num_kv_heads: int,
+                            head_dim: int) -> int:
+    """Workspace bytes with which context attention splits every small grid of these sizes the
+    most (16 splits per token tile); a smaller workspace gets fewer splits or none."""
+    n = _lib.load().mas_paged_context_attention_workspace_bytes(num_rows, max_q_len, num_q_heads, num_kv_heads,
+                                                                 head_dim)
     if n < 0:
         raise ValueError("invalid attention shape")
     return n

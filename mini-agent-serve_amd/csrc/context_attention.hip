@@ -584,6 +584,26 @@ void launch_context_mode(int mode, dim3 grid, dim3 block, hipStream_t stream, co
   else hipLaunchKernelGGL((context_attn<D, kPagesLane, kWaves, kSplit>), grid, block, 0, stream, a);
 }
 
+// Workgroup shape for a query-head group: heads per workgroup, wavefronts, and query tokens per
+// token tile (32 per wavefront, the wavefronts split between the heads).
+struct ContextLaunch {
+  int heads_per_wg, waves;
+  int64_t tokens_per_wg;
+};
+
+ContextLaunch context_launch(int64_t group) {
+  const int heads_per_wg = group >= 4 ? 4 : (group == 2 ? 2 : 1);
+  const int waves = group >= 8 ? 8 : 4;
+  return {heads_per_wg, waves, kRowsPerWave * (waves / heads_per_wg)};
+}
+
+// Bytes of split-KV partials: (max, sum) and an unnormalised fp32 O row per (row, token slot of
+// the grid, query head, split).
+int64_t context_partial_bytes(int64_t rows, int64_t row_tokens, int64_t num_q_heads, int64_t head_dim,
+                              int64_t splits) {
+  return rows * row_tokens * num_q_heads * splits * (head_dim + 2) * 4;
+}
+
 template <bool kSplit>
 void launch_context(int64_t head_dim, int waves, int mode, dim3 grid, dim3 block, hipStream_t stream,
                     const ContextArgs& a) {
@@ -630,10 +650,10 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
                        head_stride % 8 == 0;
   if (!aligned) return MAS_ERR_MISALIGNED;
   const int64_t group = num_q_heads / num_kv_heads;
-  const int heads_per_wg = group >= 4 ? 4 : (group == 2 ? 2 : 1);
+  const ContextLaunch shape = context_launch(group);
+  const int heads_per_wg = shape.heads_per_wg, waves = shape.waves;
+  const int64_t tokens_per_wg = shape.tokens_per_wg;
   const int64_t hgroups = cdiv(group, heads_per_wg);
-  const int waves = group >= 8 ? 8 : 4;
-  const int64_t tokens_per_wg = kRowsPerWave * (waves / heads_per_wg);
   const int64_t gx = num_kv_heads * hgroups, gy = cdiv(max_q_len, tokens_per_wg);
   if (gx > INT32_MAX || gy > 65535) return MAS_ERR_UNSUPPORTED;
 
@@ -647,7 +667,9 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   // on every CU gained nothing from splitting (4 rows of 256 after 8192: 256 workgroups, 237 us
   // either way), the partials' traffic eating what a second workgroup per CU brings.
   const int64_t row_tokens = gy * tokens_per_wg;
-  auto partial_bytes = [&](int64_t splits) { return num_rows * row_tokens * num_q_heads * splits * (head_dim + 2) * 4; };
+  auto partial_bytes = [&](int64_t splits) {
+    return context_partial_bytes(num_rows, row_tokens, num_q_heads, head_dim, splits);
+  };
   int64_t kv_splits = 1, split_tiles = 1;
   const int64_t base_wgs = gx * gy * num_rows;
   if (workspace != nullptr && workspace_bytes > 0 && (reinterpret_cast<uintptr_t>(workspace) & 15u) == 0) {
@@ -718,4 +740,15 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
     hipLaunchKernelGGL(context_combine<128>, dim3(static_cast<uint32_t>(merges)), dim3(64), 0, stream, a,
                        static_cast<int>(tokens_per_wg));
   return launch_status();
+}
+
+extern "C" int64_t mas_paged_context_attention_workspace_bytes(int64_t num_rows, int64_t max_q_len,
+                                                                int64_t num_q_heads, int64_t num_kv_heads,
+                                                                int64_t head_dim) {
+  using namespace mas;
+  if (num_rows < 0 || max_q_len < 0 || num_q_heads < 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
+      (head_dim != 64 && head_dim != 128))
+    return -1;
+  const int64_t tokens = context_launch(num_q_heads / num_kv_heads).tokens_per_wg;
+  return context_partial_bytes(num_rows, cdiv(max_q_len, tokens) * tokens, num_q_heads, head_dim, kMaxCtxSplits);
 }

@@ -82,15 +82,16 @@ def test_context_attention_matches_oracle(mas, dev, q_lens, kv_lens, hq, hk, dim
     assert int(flags.item()) == 0
 
 
-@pytest.mark.parametrize("page_size", [16, 256])
-def test_context_attention_hnd_layout(mas, dev, page_size):
-    """kv_layout="HND" ([pages, kv_heads, page_size, head_dim]): the same results as NHD."""
-    q_lens, kv_lens, hq, hk, dim = [50, 9], [120, 9], 32, 8, 128
+@pytest.mark.parametrize("page_size,kv0,ws_bytes", [(16, 120, 16), (256, 120, 16), (16, 2000, SPLIT_WS)])
+def test_context_attention_hnd_layout(mas, dev, page_size, kv0, ws_bytes):
+    """kv_layout="HND" ([pages, kv_heads, page_size, head_dim]): the same results as NHD (the last
+    case under split-KV)."""
+    q_lens, kv_lens, hq, hk, dim = [50, 9], [kv0, 9], 32, 8, 128
     q, kc, vc, tables, seq, cu = _case(31 + page_size, q_lens, kv_lens, hq, hk, dim, page_size)
     kh, vh = kc.transpose(1, 2).contiguous().to(dev), vc.transpose(1, 2).contiguous().to(dev)
-    ws = torch.empty(16, dtype=torch.uint8, device=dev)
+    ws = _workspace(dev, ws_bytes)
     out = mas.attention.trtllm_batch_context_with_kv_cache(
-        q.to(dev), (kh, vh), ws, tables.to(dev), seq.to(dev), max(q_lens), 0, 0.09, 1.0, len(q_lens), cu.to(dev),
+        q.to(dev), (kh, vh), ws, tables.to(dev), seq.to(dev), max(q_lens), kv0, 0.09, 1.0, len(q_lens), cu.to(dev),
         None, kv_layout="HND")
     want = ops.paged_context_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), cu.numpy(), 0.09)
     _check(bits(out), want)
@@ -232,6 +233,7 @@ SPLIT_CASES = [
     ([40], [2500], 8, 8, 128, 64, 0),                     # no max_kv_len: splits over the block table's reach
     ([40], [2500], 8, 8, 128, 64, 1024),                  # max_kv_len below the real length: the last split takes the rest
     ([96], [1200], 32, 8, 128, 128, 1200),                # pages of two tiles, three token tiles of 32
+    ([50], [2600], 16, 8, 64, 128, 2600),                 # head_dim 64 on pages of two tiles
 ]
 
 
@@ -270,6 +272,11 @@ def test_context_attention_split_kv_small_workspace(mas, dev):
     assert not torch.equal(three, full)                   # 3 splits, not 16
     tiny = _run(mas, dev, q, kc, vc, tables, seq, cu, 0.09, ws_bytes=2 * per_split - 16, max_kv=3000)
     assert torch.equal(tiny, one_kernel)
+    # context_workspace_bytes: exactly enough for the most splits this grid takes (11, under 16)
+    need = mas.attention.context_workspace_bytes(1, 32, hq, hk, dim)
+    assert need == 16 * per_split
+    exact = _run(mas, dev, q, kc, vc, tables, seq, cu, 0.09, ws_bytes=need, max_kv=3000)
+    assert torch.equal(exact, full)
 
 
 @pytest.mark.parametrize("ps", [8, 64])

@@ -49,6 +49,25 @@ def test_benchmark_skeletons_live_in_their_own_library(mas):
     assert fn(16, 8, None, 0, 40, 8, None, 0, 4, 8, None) == -1            # misaligned destination
 
 
+def test_context_workspace_bytes(mas):
+    """Bytes for 16 splits' fp32 partials, (head_dim + 2) floats per (row, token slot, head, split),
+    the token slots rounded up to whole token tiles: 32 tokens per wavefront of a workgroup of four
+    (eight for 8+ query heads per kv head) wavefronts shared among up to 4 heads."""
+    f = mas.attention.context_workspace_bytes
+    # one head per kv head: 4 wavefronts x 32 tokens = 128-token tiles; 40 tokens -> one tile
+    assert f(1, 40, 8, 8, 128) == 128 * 8 * 16 * 130 * 4
+    assert f(1, 128, 8, 8, 128) == f(1, 40, 8, 8, 128)
+    assert f(1, 129, 8, 8, 128) == 2 * f(1, 128, 8, 8, 128)
+    # 4 heads per kv head share a workgroup: 32-token tiles
+    assert f(3, 33, 32, 8, 128) == 3 * 64 * 32 * 16 * 130 * 4
+    # 12 per kv head (eight wavefronts, 4 heads each): 64-token tiles; head_dim 64
+    assert f(1, 64, 96, 8, 64) == 64 * 96 * 16 * 66 * 4
+    assert f(0, 64, 96, 8, 64) == 0
+    for bad in ((1, 64, 96, 7, 128), (1, 64, 32, 8, 256), (-1, 64, 32, 8, 128), (1, 64, 32, 0, 128)):
+        with pytest.raises(ValueError):
+            f(*bad)
+
+
 def test_fused_rope_append_rejects_an_empty_table(mas):
     """Every token's table row is loaded before its position is judged, so an empty table is an
     argument error (returned before anything is enqueued) rather than a per-token error bit."""
@@ -152,9 +171,17 @@ def test_device_checks_compare_device_indices(mas):
         require_gpu(a, "a")
     with pytest.raises(TypeError, match="torch.Tensor"):
         require_gpu([1, 2], "a")
+    class OnOtherGpu:
+        """Stands for a tensor on a second GPU, which a one-GPU machine cannot make even as a fake
+        tensor: what the check reads of a tensor."""
+        device, is_cuda = torch.device("cuda", 1), True
+
+        def get_device(self):
+            return 1
+
     with FakeTensorMode():
         g0 = torch.empty(2, device="cuda:0")
-        g1 = torch.empty(2, device="cuda:1")
+        g1 = OnOtherGpu()
         require_gpu(g0, "g0")
         assert require_same_device(("x", g0), ("y", torch.empty(5, device="cuda:0"))) == torch.device("cuda:0")
         with pytest.raises(ValueError, match="y is on cuda:1"):
