@@ -266,7 +266,7 @@ int mas_paged_decode_attention_bf16(void* out, int64_t out_stride, int64_t out_h
  * out_fp8 / out_scale_dev / out_scale_host: the fp8 output as for mas_paged_decode_attention_bf16.
  * `workspace` (16-byte aligned, workspace_bytes long; NULL / 0 for none; its contents on entry do
  * not matter): when the grid (kv heads x token tiles of max_q_len x rows) has fewer workgroups
- * than the GPU has CUs, each token tile's key range is split over up to 16 workgroups whose
+ * than the GPU has CUs, each token tile's key range is split over up to 32 workgroups whose
  * partials go here - rows * ceil(max_q_len / tile) * tile * num_q_heads * splits * (head_dim + 2)
  * * 4 bytes, tile = 32 tokens x (workgroup wavefronts / heads per workgroup) - and a second kernel
  * merges them; with less workspace, fewer splits or none. max_kv_len (<= 0: none) is a hint that
@@ -324,7 +324,7 @@ int64_t mas_paged_decode_attention_workspace_bytes(int64_t batch, int64_t num_q_
 
 /*
  * Workspace bytes that let mas_paged_context_attention_bf16 split every small grid of these
- * sizes the most (16 splits per token tile); less gets fewer splits or none. -1 for invalid
+ * sizes the most (32 splits per token tile); less gets fewer splits or none. -1 for invalid
  * arguments (num_q_heads not a multiple of num_kv_heads, head_dim not 64 or 128).
  * No counterpart in the reference (its caller passes a fixed 128 MiB workspace,
  * miniagentserve/models/devstral2/devstral2.py:36-42).

@@ -82,7 +82,7 @@ def decode_workspace_bytes(batch: int, num_q_heads: int, head_dim: int, max_bloc
 def context_workspace_bytes(num_rows: int, max_q_len: int, num_q_heads: int, num_kv_heads: int,
                             head_dim: int) -> int:
     """Workspace bytes with which context attention splits every small grid of these sizes the
-    most (16 splits per token tile); a smaller workspace gets fewer splits or none."""
+    most (32 splits per token tile); a smaller workspace gets fewer splits or none."""
     n = _lib.load().mas_paged_context_attention_workspace_bytes(num_rows, max_q_len, num_q_heads, num_kv_heads,
                                                                  head_dim)
     if n < 0:

@@ -32,7 +32,7 @@ namespace {
 
 constexpr int kTileP = 64;        // key positions per tile
 constexpr int kRowsPerWave = 32;  // query rows (tokens of one head) per wavefront
-constexpr int kMaxCtxSplits = 16;  // split-KV: key-range splits per token tile, at most
+constexpr int kMaxCtxSplits = 32;  // split-KV: key-range splits per token tile, at most
 constexpr float kNegInf = -__builtin_huge_valf();
 
 struct ContextArgs {
@@ -483,7 +483,7 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
 // One wavefront per (row, token, query head) of a split-KV launch: merges the token's non-empty
 // splits with weights 2^(c (m_s - max m)) (c = bmm1_scale * log2 e, maxima in raw score units as
 // the split kernel keeps them) and writes O / l * bmm2_scale as bf16, or its fp8 quantize. Every
-// load is issued in one round trip: lane s reads split s's (max, sum) and all kMaxCtxSplits
+// load is issued in one round trip: lane s reads split s's (max, sum) and 16 (32 past 16 splits)
 // partial O rows are loaded (indices past the last split clamped to it, weighted 0) before the
 // max is known. A token that sees no position (all maxima -inf) gets zeros.
 template <int D>
@@ -511,31 +511,45 @@ __global__ __launch_bounds__(64) void context_combine(ContextArgs a, int tokens_
     const int sl = lane < nsplit ? lane : nsplit - 1;
     const f32x2 ml = *reinterpret_cast<const f32x2*>(a.part_ml + (base + sl) * 2);
     const float* po = a.part_o + base * D + DPL * lane;
+    // slots in two halves of 16; the second only when there are more than 16 splits
     float v[kMaxCtxSplits][DPL];
+    auto load_half = [&](int u0) {
 #pragma unroll
-    for (int u = 0; u < kMaxCtxSplits; ++u) {
-      const float* src = po + min(u, nsplit - 1) * D;
-      if constexpr (DPL == 2) {
-        const f32x2 x = *reinterpret_cast<const f32x2*>(src);
-        v[u][0] = x[0];
-        v[u][1] = x[1];
-      } else {
-        v[u][0] = src[0];
+      for (int u = u0; u < u0 + 16; ++u) {
+        const float* src = po + min(u, nsplit - 1) * D;
+        if constexpr (DPL == 2) {
+          const f32x2 x = *reinterpret_cast<const f32x2*>(src);
+          v[u][0] = x[0];
+          v[u][1] = x[1];
+        } else {
+          v[u][0] = src[0];
+        }
       }
-    }
+    };
+    load_half(0);
+    if (nsplit > 16) load_half(16);
+    // max and sum over lanes 0..31 (the splits): two 16-lane rows, read out and combined
     const float m_lane = lane < nsplit ? ml[0] : kNegInf;
-    const float mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, row_max16(m_lane)), 0));
+    const float mr = row_max16(m_lane);
+    const float mx = fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mr), 0)),
+                           __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mr), 16)));
     if (mx != kNegInf) {
       const float c = a.scale_log2;
       const float wgt = lane < nsplit ? __builtin_amdgcn_exp2f(__builtin_fmaf(m_lane, c, -mx * c)) : 0.f;
-      l = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, row_sum16(wgt * ml[1])), 0));
-      // every split slot, in order: the weight is 0 past the last split (its value a finite copy)
+      const float lr = row_sum16(wgt * ml[1]);
+      l = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lr), 0)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lr), 16));
+      // every loaded slot, in order: the weight is 0 past the last split (its value a finite copy)
+      auto add_half = [&](int u0) {
 #pragma unroll
-      for (int u = 0; u < kMaxCtxSplits; ++u) {
-        const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wgt), u));
+        for (int u = u0; u < u0 + 16; ++u) {
+          const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wgt), u));
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) acc[e] = __builtin_fmaf(wj, v[u][e], acc[e]);
-      }
+          for (int e = 0; e < DPL; ++e) acc[e] = __builtin_fmaf(wj, v[u][e], acc[e]);
+        }
+      };
+      add_half(0);
+      if (nsplit > 16) add_half(16);
     }
   }
   const float sc = l > 0.f ? a.out_scale / l : 0.f;
@@ -659,13 +673,16 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
 
   // Split-KV for grids of fewer workgroups than CUs (few new tokens after a long cached prefix):
   // each token tile's key range is split over up to kMaxCtxSplits workgroups of at least 4 key
-  // tiles each, aiming at two rounds of resident workgroups, when the workspace holds the partials
-  // (workspace_bytes 0: no split). The splits divide max_kv_len (if positive, else the block
-  // table's reach) evenly; a longer row's last split takes the rest, so the hint sizes the work
-  // and never bounds it. On MI355X, one row of 128 new tokens after 4096 cached positions (32
-  // workgroups of 66 tiles) took 115 us unsplit and 37 us in 14 splits; a grid with a workgroup
-  // on every CU gained nothing from splitting (4 rows of 256 after 8192: 256 workgroups, 237 us
-  // either way), the partials' traffic eating what a second workgroup per CU brings.
+  // tiles each, when the workspace holds the partials (workspace_bytes 0: no split). The splits
+  // divide max_kv_len (if positive, else the block table's reach) evenly; a longer row's last
+  // split takes the rest, so the hint sizes the work and never bounds it. The split count
+  // minimises an estimate in key-tile times: rounds of resident workgroups x (tiles per split +
+  // 4.8, a workgroup's fixed cost: 20.9 ns per workgroup against 4.36 ns per workgroup-tile on
+  // MI355X) + the partials' bytes at 11 MB per tile time (5 TB/s over the 2.2 us a tile takes at
+  // full occupancy). Whole rounds matter most: one row of 256 new tokens after 2048 (64
+  // workgroups) took 39 us in 8 splits (512 workgroups, one round of two per CU) and 49 us in 9.
+  // A grid with a workgroup on every CU gained nothing from splitting (4 rows of 256 after 8192:
+  // 256 workgroups, 237 us either way).
   const int64_t row_tokens = gy * tokens_per_wg;
   auto partial_bytes = [&](int64_t splits) {
     return context_partial_bytes(num_rows, row_tokens, num_q_heads, head_dim, splits);
@@ -679,10 +696,24 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
     const int64_t max_tiles = cdiv(cap, kTileP);
     const int64_t hint_tiles = max_kv_len > 0 ? std::min(max_tiles, cdiv(max_kv_len, kTileP)) : max_tiles;
     if (base_wgs < cus && num_rows * row_tokens * num_q_heads <= INT32_MAX) {
-      kv_splits = std::min<int64_t>({kMaxCtxSplits, cdiv(2 * resident, base_wgs), hint_tiles / 4, 65535 / num_rows});
-      while (kv_splits > 1 && partial_bytes(kv_splits) > workspace_bytes) --kv_splits;
-      if (kv_splits > 1) split_tiles = cdiv(hint_tiles, kv_splits);
-      else kv_splits = 1;
+      const int64_t most = std::min<int64_t>({kMaxCtxSplits, hint_tiles / 4, 65535 / num_rows});
+      auto cost = [&](int64_t k, int64_t tiles) {
+        const double rounds = static_cast<double>(cdiv(base_wgs * k, resident));
+        const double partials = k > 1 ? static_cast<double>(partial_bytes(k)) / 11.0e6 : 0.0;
+        return rounds * (static_cast<double>(tiles) + 4.8) + partials;
+      };
+      double best = cost(1, hint_tiles);
+      for (int64_t k = 2; k <= most; ++k) {
+        const int64_t tiles = cdiv(hint_tiles, k);
+        const int64_t used = cdiv(hint_tiles, tiles);  // splits that get tiles at the hint's length
+        if (used != k) continue;                       // the same split as a smaller count
+        if (partial_bytes(k) > workspace_bytes) break;
+        if (const double c = cost(k, tiles); c < best) {
+          best = c;
+          kv_splits = k;
+          split_tiles = tiles;
+        }
+      }
     }
   }
   int log2_page = 0;

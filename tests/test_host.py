@@ -50,18 +50,18 @@ def test_benchmark_skeletons_live_in_their_own_library(mas):
 
 
 def test_context_workspace_bytes(mas):
-    """Bytes for 16 splits' fp32 partials, (head_dim + 2) floats per (row, token slot, head, split),
+    """Bytes for 32 splits' fp32 partials, (head_dim + 2) floats per (row, token slot, head, split),
     the token slots rounded up to whole token tiles: 32 tokens per wavefront of a workgroup of four
     (eight for 8+ query heads per kv head) wavefronts shared among up to 4 heads."""
     f = mas.attention.context_workspace_bytes
     # one head per kv head: 4 wavefronts x 32 tokens = 128-token tiles; 40 tokens -> one tile
-    assert f(1, 40, 8, 8, 128) == 128 * 8 * 16 * 130 * 4
+    assert f(1, 40, 8, 8, 128) == 128 * 8 * 32 * 130 * 4
     assert f(1, 128, 8, 8, 128) == f(1, 40, 8, 8, 128)
     assert f(1, 129, 8, 8, 128) == 2 * f(1, 128, 8, 8, 128)
     # 4 heads per kv head share a workgroup: 32-token tiles
-    assert f(3, 33, 32, 8, 128) == 3 * 64 * 32 * 16 * 130 * 4
+    assert f(3, 33, 32, 8, 128) == 3 * 64 * 32 * 32 * 130 * 4
     # 12 per kv head (eight wavefronts, 4 heads each): 64-token tiles; head_dim 64
-    assert f(1, 64, 96, 8, 64) == 64 * 96 * 16 * 66 * 4
+    assert f(1, 64, 96, 8, 64) == 64 * 96 * 32 * 66 * 4
     assert f(0, 64, 96, 8, 64) == 0
     for bad in ((1, 64, 96, 7, 128), (1, 64, 32, 8, 256), (-1, 64, 32, 8, 128), (1, 64, 32, 0, 128)):
         with pytest.raises(ValueError):
