@@ -301,6 +301,32 @@ def test_context_attention_split_kv_error_paths(mas, dev, ps):
     assert int(flags.item()) == 8
 
 
+def test_context_attention_split_kv_empty_row_and_short_grid(mas, dev):
+    """Under split-KV: a row whose seq_len is 0 (every split empty: zeros, flag 2), and max_q_len
+    below a row's query count (its tokens past the grid left unwritten, flag 2)."""
+    q_lens, kv_lens, hq, hk, dim, ps = [40, 8], [2000, 8], 32, 8, 128, 16
+    q, kc, vc, tables, _, cu = _case(17, q_lens, kv_lens, hq, hk, dim, ps)
+    seq = torch.tensor([2000, 0], dtype=torch.int32)
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = _run(mas, dev, q, kc, vc, tables, seq, cu, 0.1, flags=flags, ws_bytes=SPLIT_WS, max_kv=2000)
+    assert int(flags.item()) == 2
+    want = ops.paged_context_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), cu.numpy(), 0.1)
+    _check(bits(out), want, min_exact=0.5)
+    assert not out[40:].any()
+    # max_q_len 32 covers one 32-token tile of row 0's 40 tokens
+    out = torch.full(q.shape, 7.0, dtype=torch.bfloat16, device=dev)
+    flags.zero_()
+    seq = torch.tensor([2000, 8], dtype=torch.int32)
+    mas.attention.trtllm_batch_context_with_kv_cache(
+        q.to(dev), (kc.to(dev), vc.to(dev)), _workspace(dev, SPLIT_WS), tables.to(dev), seq.to(dev), 32, 2000, 0.1,
+        1.0, 2, cu.to(dev), None, out=out, kv_layout="NHD", error_flags=flags)
+    assert int(flags.item()) == 2
+    want = ops.paged_context_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), cu.numpy(), 0.1)
+    covered = [t for t in range(48) if not 32 <= t < 40]
+    _check(bits(out)[covered], want[covered], min_exact=0.0)
+    assert torch.all(out[32:40] == 7.0)
+
+
 @pytest.mark.parametrize("dim,hq,hk", [(128, 32, 8), (64, 6, 2)])
 def test_context_attention_split_kv_fp8_output(mas, dev, dim, hq, hk):
     """The merge kernel's fp8 output is the o_proj input quantize of its own bf16 output, bit for bit."""
