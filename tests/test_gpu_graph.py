@@ -110,26 +110,27 @@ def test_layer_pass_fused_and_separate_agree(mas, dev, fp8):
 
 def test_torch_compile_attention_matches_eager(mas, dev):
     """Both attention ops, bf16 and fp8 outputs (device-tensor scale), through torch.compile's custom
-    ops: the same bytes as eager."""
+    ops: the same bytes as eager (context attention with 40 new tokens after 1160 cached: split-KV
+    in the workspace)."""
     g = torch.Generator(device=dev).manual_seed(8)
-    pages, ps, hq, hk, d = 12, 64, 8, 2, 128
+    pages, ps, hq, hk, d = 48, 64, 8, 2, 128
     kc = torch.randn(pages, ps, hk, d, generator=g, device=dev).bfloat16()
     vc = torch.randn(pages, ps, hk, d, generator=g, device=dev).bfloat16()
-    tables = torch.randperm(pages, device=dev)[:8].reshape(2, 4).to(torch.int32)
-    seq = torch.tensor([200, 90], dtype=torch.int32, device=dev)
+    tables = torch.randperm(pages, device=dev).reshape(2, 24).to(torch.int32)
+    seq = torch.tensor([1200, 90], dtype=torch.int32, device=dev)
     qd = torch.randn(2, hq, d, generator=g, device=dev).bfloat16()
     cu = torch.tensor([0, 40, 70], dtype=torch.int32, device=dev)
     qc = torch.randn(70, hq, d, generator=g, device=dev).bfloat16()
-    ws = torch.zeros(1 << 20, dtype=torch.uint8, device=dev)
+    ws = torch.zeros(8 << 20, dtype=torch.uint8, device=dev)
     scale = torch.tensor(0.02, device=dev)
     att = mas.attention
 
     def f(qd, qc):
-        o1 = att.trtllm_batch_decode_with_kv_cache(qd, (kc, vc), ws, tables, seq, 256, 0.09, 1.0)
-        o2 = att.trtllm_batch_decode_with_kv_cache(qd, (kc, vc), ws, tables, seq, 256, 0.09, 1.0,
+        o1 = att.trtllm_batch_decode_with_kv_cache(qd, (kc, vc), ws, tables, seq, 1536, 0.09, 1.0)
+        o2 = att.trtllm_batch_decode_with_kv_cache(qd, (kc, vc), ws, tables, seq, 1536, 0.09, 1.0,
                                                    out_quant_scale=scale)
-        o3 = att.trtllm_batch_context_with_kv_cache(qc, (kc, vc), ws, tables, seq, 40, 200, 0.09, 1.0, 2, cu)
-        o4 = att.trtllm_batch_context_with_kv_cache(qc, (kc, vc), ws, tables, seq, 40, 200, 0.09, 1.0, 2, cu,
+        o3 = att.trtllm_batch_context_with_kv_cache(qc, (kc, vc), ws, tables, seq, 40, 1200, 0.09, 1.0, 2, cu)
+        o4 = att.trtllm_batch_context_with_kv_cache(qc, (kc, vc), ws, tables, seq, 40, 1200, 0.09, 1.0, 2, cu,
                                                     out_quant_scale=0.02)
         return o1 + 0, o2.view(torch.uint8) + 0, o3 + 0, o4.view(torch.uint8) + 0
 
@@ -138,3 +139,6 @@ def test_torch_compile_attention_matches_eager(mas, dev):
     got = compiled(qd, qc)
     for a, b in zip(got, want):
         assert torch.equal(a, b)
+    small_ws = torch.zeros(16, dtype=torch.uint8, device=dev)
+    one_kernel = att.trtllm_batch_context_with_kv_cache(qc, (kc, vc), small_ws, tables, seq, 40, 1200, 0.09, 1.0, 2, cu)
+    assert not torch.equal(one_kernel, want[2])   # the split ran (its rounding differs)
