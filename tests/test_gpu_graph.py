@@ -142,3 +142,30 @@ def test_torch_compile_attention_matches_eager(mas, dev):
     small_ws = torch.zeros(16, dtype=torch.uint8, device=dev)
     one_kernel = att.trtllm_batch_context_with_kv_cache(qc, (kc, vc), small_ws, tables, seq, 40, 1200, 0.09, 1.0, 2, cu)
     assert not torch.equal(one_kernel, want[2])   # the split ran (its rounding differs)
+
+
+def test_torch_compile_context_attention_keeps_lengths_symbolic(mas, dev):
+    """max_q_len taken from a traced shape, as the reference derives it (devstral2.py:295), stays
+    symbolic through the custom op: a second call with another token count runs the same compiled
+    graph (no recompilation) and gives eager's bytes."""
+    g = torch.Generator(device=dev).manual_seed(11)
+    pages, ps, hq, hk, d = 16, 64, 8, 2, 128
+    kc = torch.randn(pages, ps, hk, d, generator=g, device=dev).bfloat16()
+    vc = torch.randn(pages, ps, hk, d, generator=g, device=dev).bfloat16()
+    tables = torch.randperm(pages, device=dev).reshape(2, 8).to(torch.int32)
+    ws = torch.zeros(8 << 20, dtype=torch.uint8, device=dev)
+    att = mas.attention
+
+    def f(qc, cu, seq):
+        return att.trtllm_batch_context_with_kv_cache(qc, (kc, vc), ws, tables, seq, qc.shape[0],
+                                                      tables.shape[1] * ps, 0.09, 1.0, 2, cu) + 0
+
+    compiled = torch.compile(f, dynamic=True, fullgraph=True)
+    for n0 in (40, 57):
+        qc = torch.randn(n0 + 30, hq, d, generator=g, device=dev).bfloat16()
+        cu = torch.tensor([0, n0, n0 + 30], dtype=torch.int32, device=dev)
+        seq = torch.tensor([n0 + 300, 30], dtype=torch.int32, device=dev)
+        want = f(qc, cu, seq)
+        with torch._dynamo.config.patch(error_on_recompile=n0 != 40):
+            got = compiled(qc, cu, seq)
+        assert torch.equal(got, want)
