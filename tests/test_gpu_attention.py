@@ -260,3 +260,29 @@ def test_decode_attention_fp8_output_argument_checks(mas, dev):
         mas.attention.trtllm_batch_decode_with_kv_cache(*args, out_quant_scale=0.0)
     with pytest.raises(ValueError):
         mas.attention.trtllm_batch_decode_with_kv_cache(*args, out_quant_scale=torch.ones(2, device=dev))
+
+
+def _random_config(seed):
+    """A seeded mix: 1-40 rows of 0-3000 positions, group sizes 1-16, head_dim 64 / 128 / 256, pages
+    of 4-512 slots, the reference's workspace or a small one (longer splits)."""
+    rng = np.random.default_rng(seed)
+    batch = int(rng.choice([1, 2, 5, 16, 40]))
+    lens = [int(rng.integers(0, 3001)) for _ in range(batch)]
+    hk = int(rng.choice([1, 2, 8]))
+    group = int(rng.choice([1, 2, 3, 4, 6, 8, 12, 16]))
+    dim = int(rng.choice([64, 128, 256]))
+    ps = int(rng.choice([4, 16, 64, 256, 512]))
+    return batch, hk * group, hk, dim, ps, lens
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_decode_attention_random_configs(mas, dev, seed):
+    batch, hq, hk, dim, ps, lens = _random_config(seed)
+    q, kc, vc, tables, seq = _case(200 + seed, batch, hq, hk, dim, ps, lens)
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    full = mas.attention.decode_workspace_bytes(batch, hq, dim, tables.shape[1], ps, 1)
+    ws = full if seed % 3 else max(16, full // 4)
+    out = _run(mas, dev, q, kc, vc, tables, seq, dim ** -0.5, workspace_bytes=ws, flags=flags)
+    assert int(flags.item()) == 0
+    want = ops.paged_decode_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), dim ** -0.5)
+    _check(bits(out), want)

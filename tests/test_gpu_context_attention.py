@@ -338,3 +338,32 @@ def test_context_attention_split_kv_fp8_output(mas, dev, dim, hq, hk):
                    quant=torch.tensor(s, dtype=torch.float32, device=dev))
         assert out.dtype == torch.float8_e4m3fn
         np.testing.assert_array_equal(out.view(torch.uint8).cpu().numpy(), ops.quantize_activation(bits(ref), s))
+
+
+def _random_config(seed):
+    """A seeded mix: 1-3 rows of 1-96 new tokens after 0-2900 cached positions (some rows without
+    new tokens), group sizes 1-12, head_dim 64 / 128, pages of 8-256 slots, with and without a
+    split-KV workspace and max_kv_len."""
+    rng = np.random.default_rng(seed)
+    rows = int(rng.integers(1, 4))
+    q_lens = [int(rng.integers(0 if r else 1, 97)) for r in range(rows)]
+    kv_lens = [q + int(rng.choice([0, rng.integers(1, 2900)])) for q in q_lens]
+    hk = int(rng.choice([1, 2, 8]))
+    group = int(rng.choice([1, 2, 3, 4, 8, 12]))
+    dim = int(rng.choice([64, 128]))
+    ps = int(rng.choice([8, 16, 64, 256]))
+    ws = int(rng.choice([16, SPLIT_WS]))
+    max_kv = int(rng.choice([0, max(kv_lens)]))
+    return q_lens, kv_lens, hk * group, hk, dim, ps, ws, max_kv
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_context_attention_random_configs(mas, dev, seed):
+    q_lens, kv_lens, hq, hk, dim, ps, ws, max_kv = _random_config(seed)
+    q, kc, vc, tables, seq, cu = _case(100 + seed, q_lens, kv_lens, hq, hk, dim, ps)
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = _run(mas, dev, q, kc, vc, tables, seq, cu, dim ** -0.5, flags=flags, ws_bytes=ws, max_kv=max_kv)
+    assert int(flags.item()) == 0
+    want = ops.paged_context_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), cu.numpy(),
+                                       dim ** -0.5)
+    _check(bits(out), want, min_exact=0.5)
