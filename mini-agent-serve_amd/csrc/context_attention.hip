@@ -676,13 +676,16 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   // tiles each, when the workspace holds the partials (workspace_bytes 0: no split). The splits
   // divide max_kv_len (if positive, else the block table's reach) evenly; a longer row's last
   // split takes the rest, so the hint sizes the work and never bounds it. The split count
-  // minimises an estimate in key-tile times: rounds of resident workgroups x (tiles per split +
-  // 4.8, a workgroup's fixed cost: 20.9 ns per workgroup against 4.36 ns per workgroup-tile on
-  // MI355X) + the partials' bytes at 11 MB per tile time (5 TB/s over the 2.2 us a tile takes at
-  // full occupancy). Whole rounds matter most: one row of 256 new tokens after 2048 (64
-  // workgroups) took 39 us in 8 splits (512 workgroups, one round of two per CU) and 49 us in 9.
-  // A grid with a workgroup on every CU gained nothing from splitting (4 rows of 256 after 8192:
-  // 256 workgroups, 237 us either way).
+  // minimises an estimate in microseconds fitted on MI355X: (tiles per split + 4.8, a workgroup's
+  // fixed cost) x 1.8 us with at most one workgroup per CU, else x 2.1 us per round of resident
+  // workgroups, plus, when split, the merge (a launch, then its bytes at 5 TB/s or 0.6 ns per
+  // (token, head), whichever is longer); a split must beat the one-kernel estimate by 20%. Whole
+  // rounds matter:
+  // one row of 256 new tokens after 2048 (64 workgroups) took 39 us in 8 splits (512 workgroups,
+  // one round of two per CU) and 49 us in 9. The merge's per-(token, head) cost decides for
+  // many short rows: 24 rows of 32 new tokens after 512 took 26.6 us unsplit and 44.9 in 2
+  // splits. A grid with a workgroup on every CU gains nothing (4 rows of 256 after 8192: 256
+  // workgroups, 237 us either way) and is not split.
   const int64_t row_tokens = gy * tokens_per_wg;
   auto partial_bytes = [&](int64_t splits) {
     return context_partial_bytes(num_rows, row_tokens, num_q_heads, head_dim, splits);
@@ -697,12 +700,15 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
     const int64_t hint_tiles = max_kv_len > 0 ? std::min(max_tiles, cdiv(max_kv_len, kTileP)) : max_tiles;
     if (base_wgs < cus && num_rows * row_tokens * num_q_heads <= INT32_MAX) {
       const int64_t most = std::min<int64_t>({kMaxCtxSplits, hint_tiles / 4, 65535 / num_rows});
-      auto cost = [&](int64_t k, int64_t tiles) {
-        const double rounds = static_cast<double>(cdiv(base_wgs * k, resident));
-        const double partials = k > 1 ? static_cast<double>(partial_bytes(k)) / 11.0e6 : 0.0;
-        return rounds * (static_cast<double>(tiles) + 4.8) + partials;
+      const double merges = static_cast<double>(num_rows * row_tokens * num_q_heads);
+      auto cost = [&](int64_t k, int64_t tiles) {  // microseconds
+        const int64_t wgs = base_wgs * k;
+        const double per_wg = static_cast<double>(tiles) + 4.8;
+        double t = wgs <= cus ? per_wg * 1.8 : static_cast<double>(cdiv(wgs, resident)) * per_wg * 2.1;
+        if (k > 1) t += 2.0 + std::max(static_cast<double>(partial_bytes(k)) / 5.0e6, merges * 6.0e-4);
+        return t;
       };
-      double best = cost(1, hint_tiles);
+      double best = 0.8 * cost(1, hint_tiles);
       for (int64_t k = 2; k <= most; ++k) {
         const int64_t tiles = cdiv(hint_tiles, k);
         const int64_t used = cdiv(hint_tiles, tiles);  // splits that get tiles at the hint's length
