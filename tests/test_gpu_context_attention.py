@@ -367,3 +367,14 @@ def test_context_attention_random_configs(mas, dev, seed):
     want = ops.paged_context_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), cu.numpy(),
                                        dim ** -0.5)
     _check(bits(out), want, min_exact=0.5)
+
+
+def test_context_attention_medium_grid_stays_one_kernel(mas, dev):
+    """Many short rows (24 rows of 32 new tokens after 512 cached: 192 workgroups on MI355X's 256
+    CUs) are not split even with a workspace: the merge would cost more than the split saves, so
+    the result is the one-kernel result, bit for bit."""
+    rows, q_len, cached, hq, hk, dim, ps = 24, 32, 512, 32, 8, 128, 16
+    q, kc, vc, tables, seq, cu = _case(23, [q_len] * rows, [q_len + cached] * rows, hq, hk, dim, ps)
+    one_kernel = _run(mas, dev, q, kc, vc, tables, seq, cu, dim ** -0.5, max_kv=q_len + cached)
+    with_ws = _run(mas, dev, q, kc, vc, tables, seq, cu, dim ** -0.5, ws_bytes=SPLIT_WS, max_kv=q_len + cached)
+    assert torch.equal(one_kernel, with_ws)
