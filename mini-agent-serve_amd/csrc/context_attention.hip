@@ -680,12 +680,11 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   // fixed cost) x 1.8 us with at most one workgroup per CU, else x 2.1 us per round of resident
   // workgroups, plus, when split, the merge (a launch, then its bytes at 5 TB/s or 0.6 ns per
   // (token, head), whichever is longer); a split must beat the one-kernel estimate by 20%. Whole
-  // rounds matter:
-  // one row of 256 new tokens after 2048 (64 workgroups) took 39 us in 8 splits (512 workgroups,
-  // one round of two per CU) and 49 us in 9. The merge's per-(token, head) cost decides for
-  // many short rows: 24 rows of 32 new tokens after 512 took 26.6 us unsplit and 44.9 in 2
-  // splits. A grid with a workgroup on every CU gains nothing (4 rows of 256 after 8192: 256
-  // workgroups, 237 us either way) and is not split.
+  // rounds matter: one row of 256 new tokens after 2048 (64 workgroups) took 39 us in 8 splits
+  // (512 workgroups, one round of two per CU) and 49 us in 9. The merge's per-(token, head) cost
+  // decides for many short rows: 24 rows of 32 new tokens after 512 took 26.6 us unsplit and
+  // 44.9 in 2 splits. A grid with a workgroup on every CU gains nothing (4 rows of 256 after
+  // 8192: 256 workgroups, 237 us either way) and is not split.
   const int64_t row_tokens = gy * tokens_per_wg;
   auto partial_bytes = [&](int64_t splits) {
     return context_partial_bytes(num_rows, row_tokens, num_q_heads, head_dim, splits);
