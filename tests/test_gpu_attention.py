@@ -286,3 +286,13 @@ def test_decode_attention_random_configs(mas, dev, seed):
     assert int(flags.item()) == 0
     want = ops.paged_decode_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), dim ** -0.5)
     _check(bits(out), want)
+
+
+def test_decode_attention_peaked_scores(mas, dev):
+    """Scores spread over hundreds of units (q ~ N(0, 9), scale 1): nearly one-hot softmax rows whose
+    running max moves often, over single- and multi-split rows."""
+    q, kc, vc, tables, seq = _case(43, 4, 32, 8, 128, 16, [3000, 200, 17, 1])
+    q = (q.float() * 3.0).bfloat16()
+    out = _run(mas, dev, q, kc, vc, tables, seq, 1.0)
+    want = ops.paged_decode_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), 1.0)
+    _check(bits(out), want)

@@ -378,3 +378,15 @@ def test_context_attention_medium_grid_stays_one_kernel(mas, dev):
     one_kernel = _run(mas, dev, q, kc, vc, tables, seq, cu, dim ** -0.5, max_kv=q_len + cached)
     with_ws = _run(mas, dev, q, kc, vc, tables, seq, cu, dim ** -0.5, ws_bytes=SPLIT_WS, max_kv=q_len + cached)
     assert torch.equal(one_kernel, with_ws)
+
+
+@pytest.mark.parametrize("ws_bytes", [16, SPLIT_WS])
+def test_context_attention_peaked_scores(mas, dev, ws_bytes):
+    """Scores spread over hundreds of units (q ~ N(0, 9), scale 1): each row's softmax is nearly
+    one-hot and its running max moves often; one kernel and split-KV both match the oracle."""
+    q_lens, kv_lens, hq, hk, dim, ps = [40, 7], [1500, 7], 16, 4, 128, 16
+    q, kc, vc, tables, seq, cu = _case(41, q_lens, kv_lens, hq, hk, dim, ps)
+    q = (q.float() * 3.0).bfloat16()
+    out = _run(mas, dev, q, kc, vc, tables, seq, cu, 1.0, ws_bytes=ws_bytes, max_kv=1500)
+    want = ops.paged_context_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), cu.numpy(), 1.0)
+    _check(bits(out), want, min_exact=0.5)
