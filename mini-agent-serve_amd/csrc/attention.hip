@@ -22,6 +22,7 @@
 // Scores live in the log2 domain (bmm1_scale * log2 e folded in), so every exponential is one
 // v_exp_f32. A position whose page id is out of range is skipped (MAS_ERRBIT_PAGE); seq_lens past
 // the block table's reach is clamped to it (MAS_ERRBIT_POSITION); a row with no position gets zeros.
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 
@@ -43,7 +44,8 @@ struct DecodeArgs {
   int64_t bt_stride, max_blocks;
   const int32_t* seq_lens;
   int hq, hk, group, log2_page, max_splits;
-  int split_len;     // positions per split: 64, 128, or a multiple of the 256-position chunk
+  int split_len;     // longest split: 64, 128, or a multiple of the 256-position chunk
+  int row_target;    // small grids: splits wanted per row (the GPU's SIMDs over rows x kv heads)
   float scale_log2;  // bmm1_scale * log2(e)
   float out_scale;   // bmm2_scale
   float* part_o;     // [batch][hq][max_splits][D]
@@ -62,6 +64,21 @@ __device__ __forceinline__ int kv_len(const DecodeArgs& a, int b) {
   const int64_t L = a.seq_lens[b];
   const int64_t cap = a.max_blocks << a.log2_page;
   return static_cast<int>(L < 0 ? 0 : (L > cap ? cap : L));
+}
+
+// The split length of a row of L positions, chosen from the row's own length: 256 positions, or,
+// in small grids (4+ splits wanted per row), 128 or 64 when the row's share L / row_target is that
+// short; at most split_len, and at least the fewest 64-position units that keep the row within the
+// grid's max_splits. The grid is sized from the block table's reach, which can far exceed the rows
+// (a graph captured for the longest context): a row then still gets splits as short as its own
+// length calls for.
+__device__ __forceinline__ int row_split_len(const DecodeArgs& a, int L) {
+  // large grids: the host's split for rows of 4+ such splits, 256 positions for shorter rows
+  int len = L >= 4 * a.split_len ? a.split_len : 256;
+  if (a.row_target >= 4) len = L <= 64 * a.row_target ? 64 : (L <= 128 * a.row_target ? 128 : 256);
+  len = min(len, a.split_len);
+  if (L > len * a.max_splits) len = 64 * (((L + 63) / 64 + a.max_splits - 1) / a.max_splits);  // within the grid
+  return len;
 }
 
 // The output element(s) of row b, query head h, starting at head-dim column `col`: bf16 y, or its
@@ -228,9 +245,10 @@ __global__ __launch_bounds__(64 * kAttnWaves, D <= 128 ? kAttnMinWaves : 1) void
   uint16_t(*p_lds)[16 * PROW] = p_lds_all[wave];
   int32_t* pg_lds = pg_lds_all[wave];
   const int L = kv_len(a, b);
-  const int start = split * a.split_len;
+  const int split_len = row_split_len(a, L);
+  const int start = split * split_len;
   if (start >= L) return;
-  const int end = min(start + a.split_len, L);
+  const int end = min(start + split_len, L);
   const int G = a.group;
   const int n = lane & 15, r = lane >> 4;
   const int pv_d = lane % LPP, pv_grp = lane / LPP;
@@ -383,7 +401,7 @@ __global__ __launch_bounds__(64 * kAttnWaves, D <= 128 ? kAttnMinWaves : 1) void
   }
   if (__builtin_amdgcn_ballot_w64(bad) != 0 && lane == 0) report(a.err, MAS_ERRBIT_PAGE);
 
-  if (L <= a.split_len) {
+  if (L <= split_len) {
     // The row's only split: its output is O / l * bmm2_scale, what merging one split gives.
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -454,7 +472,7 @@ __global__ __launch_bounds__(64) void decode_attn_combine(DecodeArgs a) {
   // reported at the end: a global atomic here would turn the loads below into waits on every load
   const bool len_bad = raw < 0 || raw > cap;
   const int L = static_cast<int>(raw < 0 ? 0 : (raw > cap ? cap : raw));
-  const int split_len = a.split_len;
+  const int split_len = row_split_len(a, L);
   const int nsplit = (L + split_len - 1) / split_len;
   if (nsplit == 1) {  // the split kernel wrote this row's output
     if (len_bad && h == 0 && lane == 0) report(a.err, MAS_ERRBIT_POSITION);
@@ -681,6 +699,11 @@ int decode_attention(void* out, int64_t out_stride, int64_t out_head_stride, con
   a.group = static_cast<int>(group);
   a.log2_page = log2_page;
   a.split_len = static_cast<int>(split_len);
+  {
+    int cus = 0;
+    if (const int st = device_cu_count(&cus); st != MAS_OK) return st;
+    a.row_target = static_cast<int>(std::max<int64_t>(1, static_cast<int64_t>(cus) * 4 / std::max<int64_t>(1, batch * num_kv_heads)));
+  }
   a.max_splits = static_cast<int>(splits);
   a.scale_log2 = bmm1_scale * 1.4426950408889634f;
   a.out_scale = bmm2_scale;

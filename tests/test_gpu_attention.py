@@ -296,3 +296,19 @@ def test_decode_attention_peaked_scores(mas, dev):
     out = _run(mas, dev, q, kc, vc, tables, seq, 1.0)
     want = ops.paged_decode_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), 1.0)
     _check(bits(out), want)
+
+
+@pytest.mark.parametrize("reach,ps", [(32768, 16), (131072, 16), (32768, 256)])
+def test_decode_attention_block_table_wider_than_rows(mas, dev, reach, ps):
+    """A block table as wide as a graph captured for the longest context (the reference captures
+    its decode graphs with max_blocks columns) over rows far shorter: each row still gets short
+    splits; results match the oracle, and no padding column is read as a page."""
+    lens = [1, 300, 2000, 777, 4096, 60, 1500, 9]
+    q, kc, vc, tables, seq = _case(47 + ps, len(lens), 32, 8, 128, ps, lens)
+    wide = torch.full((len(lens), reach // ps), -7, dtype=torch.int32)   # out-of-range page ids
+    wide[:, : tables.shape[1]] = tables
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = _run(mas, dev, q, kc, vc, wide, seq, 0.088, flags=flags)
+    assert int(flags.item()) == 0
+    want = ops.paged_decode_attention(bits(q), bits(kc), bits(vc), wide.numpy(), seq.numpy(), 0.088)
+    _check(bits(out), want)
