@@ -269,9 +269,9 @@ int mas_paged_decode_attention_bf16(void* out, int64_t out_stride, int64_t out_h
  * than the GPU has CUs, each token tile's key range is split over up to 32 workgroups whose
  * partials go here - rows * ceil(max_q_len / tile) * tile * num_q_heads * splits * (head_dim + 2)
  * * 4 bytes, tile = 32 tokens x (workgroup wavefronts / heads per workgroup) - and a second kernel
- * merges them; with less workspace, fewer splits or none. max_kv_len (<= 0: none) is a hint that
- * sizes the splits (they divide max_kv_len evenly, else the block table's reach); a longer row is
- * still attended in full, its last split taking the rest.
+ * merges them; with less workspace, fewer splits or none. Each token tile divides its own key
+ * range among the splits; max_kv_len (<= 0: none; else the block table's reach) is a hint that
+ * only sizes the choice of the split count.
  * Replaces flashinfer.prefill.trtllm_batch_context_with_kv_cache at
  * miniagentserve/models/devstral2/devstral2.py:198-213 (kv_layout "NHD", no sliding window).
  */

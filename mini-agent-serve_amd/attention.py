@@ -246,8 +246,8 @@ def trtllm_batch_context_with_kv_cache(query: torch.Tensor, kv_cache, workspace_
     accepted and unused. ``workspace_buffer`` (or None) holds split-KV partials when the grid is
     small (few new tokens after a long cached prefix): each token tile's key range is then split
     over several workgroups and merged by a second kernel; its contents on entry do not matter, and
-    with too little of it the kernel splits less or not at all. ``max_kv_len`` sizes those splits
-    (a hint: a longer row is still attended in full, only less evenly split). Not
+    with too little of it the kernel splits less or not at all. ``max_kv_len`` is a hint for the
+    choice of the split count (each row divides its own positions among the splits). Not
     supported (raise): a sliding window, attention sinks, block-scaled outputs. ``enable_pdl`` is
     ignored.
     """

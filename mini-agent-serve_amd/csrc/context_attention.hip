@@ -46,11 +46,11 @@ struct ContextArgs {
   const int32_t* seq_lens;
   const int32_t* cu_seqlens_q;
   int hq, hk, group, heads_per_wg, log2_page;
-  // Split-KV (kv_splits > 1, for grids smaller than one round of resident workgroups): split s of a
-  // token tile walks key tiles [s * split_tiles, (s + 1) * split_tiles) (the last split: to the
-  // end) and writes its (max, sum, unnormalised O) per (token, head) to part_ml / part_o, indexed by
-  // (row * row_tokens + token, head, split); context_combine merges them.
-  int kv_splits, split_tiles, row_tokens;
+  // Split-KV (kv_splits > 1, for grids of fewer workgroups than CUs): split s of a token tile walks
+  // key tiles [s * t, (s + 1) * t), t = split_tiles(its key tiles, kv_splits) (the last split: to
+  // the end), and writes its (max, sum, unnormalised O) per (token, head) to part_ml / part_o,
+  // indexed by (row * row_tokens + token, head, split); context_combine merges them.
+  int kv_splits, row_tokens;
   float* part_o;
   float* part_ml;
   float scale_log2;
@@ -89,6 +89,14 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
 // vector load issued before them, the next tiles' key / value loads included: they stall the
 // software pipeline, which the scalar reads do not.
 constexpr int kPagesLane = 0, kPagesStep = 1, kPagesTile = 2, kPagesStep1 = 3;
+
+// Key tiles per split of a token tile that reaches `ntiles` key tiles: its kv_splits splits share
+// them evenly, at least 4 each (fewer splits then hold them all). From the tile's own reach, not
+// the block table's, so that a table much wider than the rows (a graph captured for the longest
+// context) still spreads each row over all the splits.
+__device__ __forceinline__ int split_tiles(int ntiles, int kv_splits) {
+  return max(4, (ntiles + kv_splits - 1) / kv_splits);
+}
 
 // kSplit: a split-KV launch (a separate instance, so that the one-kernel instances keep their code).
 template <int D, int kPages, int kWaves, bool kSplit>
@@ -158,8 +166,9 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   const int reach = shift + last_tok + 1;  // <= kv_len
   const int ntiles = reach > 0 ? (reach + kTileP - 1) / kTileP : 0;
   // This workgroup's key tiles: all of them, or its split's share.
-  const int it_begin = kSplit ? split * a.split_tiles : 0;
-  const int it_end = !kSplit || split == a.kv_splits - 1 ? ntiles : min(ntiles, it_begin + a.split_tiles);
+  const int per_split = kSplit ? split_tiles(ntiles, a.kv_splits) : 0;
+  const int it_begin = kSplit ? split * per_split : 0;
+  const int it_end = !kSplit || split == a.kv_splits - 1 ? ntiles : min(ntiles, it_begin + per_split);
   if (kSplit && it_begin >= it_end) {  // an empty split (uniform): the merge skips it
     if (len_bad && tid == 0 && blockIdx.x == 0 && tile_idx == 0 && split == 0) report(a.err, MAS_ERRBIT_POSITION);
     return;
@@ -502,7 +511,8 @@ __global__ __launch_bounds__(64) void context_combine(ContextArgs a, int tokens_
   const int tile_tok = t / tokens_per_wg * tokens_per_wg;
   const int reach = kv_len - q_len + min(tile_tok + tokens_per_wg, q_len);
   const int ntiles = reach > 0 ? (reach + kTileP - 1) / kTileP : 0;
-  const int nsplit = min(a.kv_splits, (ntiles + a.split_tiles - 1) / a.split_tiles);  // <= kMaxCtxSplits
+  const int per_split = split_tiles(ntiles, a.kv_splits);
+  const int nsplit = min(a.kv_splits, (ntiles + per_split - 1) / per_split);  // <= kMaxCtxSplits
   const int64_t base = ((static_cast<int64_t>(row) * a.row_tokens + t) * a.hq + h) * a.kv_splits;
   float acc[DPL], l = 0.f;
 #pragma unroll
@@ -673,9 +683,9 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
 
   // Split-KV for grids of fewer workgroups than CUs (few new tokens after a long cached prefix):
   // each token tile's key range is split over up to kMaxCtxSplits workgroups of at least 4 key
-  // tiles each, when the workspace holds the partials (workspace_bytes 0: no split). The splits
-  // divide max_kv_len (if positive, else the block table's reach) evenly; a longer row's last
-  // split takes the rest, so the hint sizes the work and never bounds it. The split count
+  // tiles each, when the workspace holds the partials (workspace_bytes 0: no split). Each token
+  // tile divides its own key tiles among the splits (split_tiles); max_kv_len (if positive, else
+  // the block table's reach) only sizes the estimate that picks the split count. The split count
   // minimises an estimate in microseconds fitted on MI355X: (tiles per split + 4.8, a workgroup's
   // fixed cost) x 1.8 us with at most one workgroup per CU, else x 2.1 us per round of resident
   // workgroups, plus, when split, the merge (a launch, then its bytes at 5 TB/s or 0.6 ns per
@@ -689,7 +699,7 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   auto partial_bytes = [&](int64_t splits) {
     return context_partial_bytes(num_rows, row_tokens, num_q_heads, head_dim, splits);
   };
-  int64_t kv_splits = 1, split_tiles = 1;
+  int64_t kv_splits = 1;
   const int64_t base_wgs = gx * gy * num_rows;
   if (workspace != nullptr && workspace_bytes > 0 && (reinterpret_cast<uintptr_t>(workspace) & 15u) == 0) {
     int cus = 0;
@@ -716,7 +726,6 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
         if (const double c = cost(k, tiles); c < best) {
           best = c;
           kv_splits = k;
-          split_tiles = tiles;
         }
       }
     }
@@ -753,7 +762,6 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   a.quant_scale_host = out_scale_host;
   a.err = err;
   a.kv_splits = static_cast<int>(kv_splits);
-  a.split_tiles = static_cast<int>(split_tiles);
   a.row_tokens = static_cast<int>(row_tokens);
   a.part_o = static_cast<float*>(workspace);
   a.part_ml = kv_splits > 1 ? a.part_o + num_rows * row_tokens * num_q_heads * kv_splits * head_dim : nullptr;

@@ -390,3 +390,20 @@ def test_context_attention_peaked_scores(mas, dev, ws_bytes):
     out = _run(mas, dev, q, kc, vc, tables, seq, cu, 1.0, ws_bytes=ws_bytes, max_kv=1500)
     want = ops.paged_context_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), cu.numpy(), 1.0)
     _check(bits(out), want, min_exact=0.5)
+
+
+@pytest.mark.parametrize("reach", [32768, 131072])
+def test_context_attention_block_table_wider_than_rows(mas, dev, reach):
+    """The reference passes max_kv_len = the block table's reach (devstral2.py:296), which in a graph
+    captured for the longest context far exceeds the rows: each token tile still divides its own
+    positions among the splits; results match the oracle and no padding column is read as a page."""
+    q_lens, kv_lens, hq, hk, dim, ps = [128, 20], [4224, 900], 32, 8, 128, 16
+    q, kc, vc, tables, seq, cu = _case(53, q_lens, kv_lens, hq, hk, dim, ps)
+    wide = torch.full((len(q_lens), reach // ps), -7, dtype=torch.int32)   # out-of-range page ids
+    wide[:, : tables.shape[1]] = tables
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = _run(mas, dev, q, kc, vc, wide, seq, cu, dim ** -0.5, flags=flags, ws_bytes=SPLIT_WS, max_kv=reach)
+    assert int(flags.item()) == 0
+    want = ops.paged_context_attention(bits(q), bits(kc), bits(vc), wide.numpy(), seq.numpy(), cu.numpy(),
+                                       dim ** -0.5)
+    _check(bits(out), want, min_exact=0.5)
