@@ -49,8 +49,10 @@ struct ContextArgs {
   // Split-KV (kv_splits > 1, for grids of fewer workgroups than CUs): split s of a token tile walks
   // key tiles [s * t, (s + 1) * t), t = split_tiles(its key tiles, kv_splits) (the last split: to
   // the end), and writes its (max, sum, unnormalised O) per (token, head) to part_ml / part_o,
-  // indexed by (row * row_tokens + token, head, split); context_combine merges them.
-  int kv_splits, row_tokens;
+  // indexed by (row * row_tokens + token, head, split); context_combine merges them. Token tiles
+  // reaching fewer than split_from key tiles are not split: split 0 computes them whole and writes
+  // their output.
+  int kv_splits, row_tokens, split_from;
   float* part_o;
   float* part_ml;
   float scale_log2;
@@ -166,10 +168,13 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   const int reach = shift + last_tok + 1;  // <= kv_len
   const int ntiles = reach > 0 ? (reach + kTileP - 1) / kTileP : 0;
   // This workgroup's key tiles: all of them, or its split's share.
-  const int per_split = kSplit ? split_tiles(ntiles, a.kv_splits) : 0;
+  const bool split_tile = kSplit && ntiles >= a.split_from;
+  const int per_split = split_tile ? split_tiles(ntiles, a.kv_splits) : ntiles;
   const int it_begin = kSplit ? split * per_split : 0;
-  const int it_end = !kSplit || split == a.kv_splits - 1 ? ntiles : min(ntiles, it_begin + per_split);
-  if (kSplit && it_begin >= it_end) {  // an empty split (uniform): the merge skips it
+  const int it_end = !split_tile || split == a.kv_splits - 1 ? ntiles : min(ntiles, it_begin + per_split);
+  // an empty split (uniform), which the merge skips; split 0 of a tile that is not split goes on,
+  // to write its output (zeros for a tile that reaches no key)
+  if (kSplit && it_begin >= it_end && (split_tile || split > 0)) {
     if (len_bad && tid == 0 && blockIdx.x == 0 && tile_idx == 0 && split == 0) report(a.err, MAS_ERRBIT_POSITION);
     return;
   }
@@ -449,7 +454,7 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   if (!wave_live) return;
   const int t = tok + n;
   if (t >= q_len) return;
-  if constexpr (kSplit) {
+  if (split_tile) {
     // ---- this split's partial: O row (lane half hf holds columns 32 db + 8 q + 4 hf .. + 3) and
     // (max, sum), both halves holding the same (max, sum)
     const int64_t pi = ((static_cast<int64_t>(row) * a.row_tokens + t) * a.hq + h) * a.kv_splits + split;
@@ -511,6 +516,7 @@ __global__ __launch_bounds__(64) void context_combine(ContextArgs a, int tokens_
   const int tile_tok = t / tokens_per_wg * tokens_per_wg;
   const int reach = kv_len - q_len + min(tile_tok + tokens_per_wg, q_len);
   const int ntiles = reach > 0 ? (reach + kTileP - 1) / kTileP : 0;
+  if (ntiles < a.split_from) return;  // not split: the split kernel wrote this token's output
   const int per_split = split_tiles(ntiles, a.kv_splits);
   const int nsplit = min(a.kv_splits, (ntiles + per_split - 1) / per_split);  // <= kMaxCtxSplits
   const int64_t base = ((static_cast<int64_t>(row) * a.row_tokens + t) * a.hq + h) * a.kv_splits;
@@ -699,7 +705,7 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   auto partial_bytes = [&](int64_t splits) {
     return context_partial_bytes(num_rows, row_tokens, num_q_heads, head_dim, splits);
   };
-  int64_t kv_splits = 1;
+  int64_t kv_splits = 1, split_from = INT32_MAX;
   const int64_t base_wgs = gx * gy * num_rows;
   if (workspace != nullptr && workspace_bytes > 0 && (reinterpret_cast<uintptr_t>(workspace) & 15u) == 0) {
     int cus = 0;
@@ -708,7 +714,6 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
     const int64_t max_tiles = cdiv(cap, kTileP);
     const int64_t hint_tiles = max_kv_len > 0 ? std::min(max_tiles, cdiv(max_kv_len, kTileP)) : max_tiles;
     if (base_wgs < cus && num_rows * row_tokens * num_q_heads <= INT32_MAX) {
-      const int64_t most = std::min<int64_t>({kMaxCtxSplits, hint_tiles / 4, 65535 / num_rows});
       const double merges = static_cast<double>(num_rows * row_tokens * num_q_heads);
       auto cost = [&](int64_t k, int64_t tiles) {  // microseconds
         const int64_t wgs = base_wgs * k;
@@ -717,16 +722,36 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
         if (k > 1) t += 2.0 + std::max(static_cast<double>(partial_bytes(k)) / 5.0e6, merges * 6.0e-4);
         return t;
       };
-      double best = 0.8 * cost(1, hint_tiles);
-      for (int64_t k = 2; k <= most; ++k) {
-        const int64_t tiles = cdiv(hint_tiles, k);
-        const int64_t used = cdiv(hint_tiles, tiles);  // splits that get tiles at the hint's length
-        if (used != k) continue;                       // the same split as a smaller count
-        if (partial_bytes(k) > workspace_bytes) break;
-        if (const double c = cost(k, tiles); c < best) {
-          best = c;
-          kv_splits = k;
+      // The best split count for token tiles that all reach `reach` key tiles (1: no split).
+      // at most two rounds of resident workgroups: a split grid whose rows turn out shorter than
+      // the hint (tiles below split_from are not split) pays for its empty workgroups
+      const int64_t grid_most = std::max<int64_t>(1, 2 * resident / base_wgs);
+      auto best_splits = [&](int64_t reach) {
+        const int64_t most = std::min<int64_t>({kMaxCtxSplits, reach / 4, 65535 / num_rows, grid_most});
+        double best = 0.8 * cost(1, reach);
+        int64_t k_best = 1;
+        for (int64_t k = 2; k <= most; ++k) {
+          const int64_t tiles = cdiv(reach, k);
+          if (cdiv(reach, tiles) != k) continue;  // the same split as a smaller count
+          if (partial_bytes(k) > workspace_bytes) break;
+          if (const double c = cost(k, tiles); c < best) {
+            best = c;
+            k_best = k;
+          }
         }
+        return k_best;
+      };
+      kv_splits = best_splits(hint_tiles);
+      if (kv_splits > 1) {
+        // The shortest reach (in powers of two) worth splitting: tiles of rows shorter than the
+        // hint (a graph's table far wider than its rows) are computed whole when splitting them
+        // would cost more than it saves.
+        split_from = hint_tiles;
+        for (int64_t reach = 4; reach < hint_tiles; reach *= 2)
+          if (best_splits(reach) > 1) {
+            split_from = reach;
+            break;
+          }
       }
     }
   }
@@ -763,6 +788,7 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   a.err = err;
   a.kv_splits = static_cast<int>(kv_splits);
   a.row_tokens = static_cast<int>(row_tokens);
+  a.split_from = static_cast<int>(split_from);
   a.part_o = static_cast<float*>(workspace);
   a.part_ml = kv_splits > 1 ? a.part_o + num_rows * row_tokens * num_q_heads * kv_splits * head_dim : nullptr;
   const dim3 grid(static_cast<uint32_t>(gx), static_cast<uint32_t>(gy), static_cast<uint32_t>(num_rows * kv_splits));
