@@ -264,7 +264,8 @@ def test_decode_attention_fp8_output_argument_checks(mas, dev):
 
 def _random_config(seed):
     """A seeded mix: 1-40 rows of 0-3000 positions, group sizes 1-16, head_dim 64 / 128 / 256, pages
-    of 4-512 slots, the reference's workspace or a small one (longer splits)."""
+    of 4-512 slots, the reference's workspace or a small one (longer splits), block tables as wide
+    as the rows or 4-32 times wider."""
     rng = np.random.default_rng(seed)
     batch = int(rng.choice([1, 2, 5, 16, 40]))
     lens = [int(rng.integers(0, 3001)) for _ in range(batch)]
@@ -272,13 +273,18 @@ def _random_config(seed):
     group = int(rng.choice([1, 2, 3, 4, 6, 8, 12, 16]))
     dim = int(rng.choice([64, 128, 256]))
     ps = int(rng.choice([4, 16, 64, 256, 512]))
-    return batch, hk * group, hk, dim, ps, lens
+    widen = int(rng.choice([1, 1, 4, 32]))  # a block table 4 or 32 times wider than the rows need
+    return batch, hk * group, hk, dim, ps, lens, widen
 
 
 @pytest.mark.parametrize("seed", range(30))
 def test_decode_attention_random_configs(mas, dev, seed):
-    batch, hq, hk, dim, ps, lens = _random_config(seed)
+    batch, hq, hk, dim, ps, lens, widen = _random_config(seed)
     q, kc, vc, tables, seq = _case(200 + seed, batch, hq, hk, dim, ps, lens)
+    if widen > 1:   # padding columns hold out-of-range page ids
+        wide = torch.full((tables.shape[0], tables.shape[1] * widen), -7, dtype=torch.int32)
+        wide[:, : tables.shape[1]] = tables
+        tables = wide
     flags = torch.zeros(1, dtype=torch.int32, device=dev)
     full = mas.attention.decode_workspace_bytes(batch, hq, dim, tables.shape[1], ps, 1)
     ws = full if seed % 3 else max(16, full // 4)

@@ -343,7 +343,7 @@ def test_context_attention_split_kv_fp8_output(mas, dev, dim, hq, hk):
 def _random_config(seed):
     """A seeded mix: 1-3 rows of 1-96 new tokens after 0-2900 cached positions (some rows without
     new tokens), group sizes 1-12, head_dim 64 / 128, pages of 8-256 slots, with and without a
-    split-KV workspace and max_kv_len."""
+    split-KV workspace and max_kv_len, block tables as wide as the rows or 4-32 times wider."""
     rng = np.random.default_rng(seed)
     rows = int(rng.integers(1, 4))
     q_lens = [int(rng.integers(0 if r else 1, 97)) for r in range(rows)]
@@ -354,13 +354,19 @@ def _random_config(seed):
     ps = int(rng.choice([8, 16, 64, 256]))
     ws = int(rng.choice([16, SPLIT_WS]))
     max_kv = int(rng.choice([0, max(kv_lens)]))
-    return q_lens, kv_lens, hk * group, hk, dim, ps, ws, max_kv
+    widen = int(rng.choice([1, 1, 4, 32]))  # a block table 4 or 32 times wider than the rows need
+    return q_lens, kv_lens, hk * group, hk, dim, ps, ws, max_kv, widen
 
 
 @pytest.mark.parametrize("seed", range(40))
 def test_context_attention_random_configs(mas, dev, seed):
-    q_lens, kv_lens, hq, hk, dim, ps, ws, max_kv = _random_config(seed)
+    q_lens, kv_lens, hq, hk, dim, ps, ws, max_kv, widen = _random_config(seed)
     q, kc, vc, tables, seq, cu = _case(100 + seed, q_lens, kv_lens, hq, hk, dim, ps)
+    if widen > 1:   # padding columns hold out-of-range page ids; max_kv_len then is the table's reach
+        wide = torch.full((tables.shape[0], tables.shape[1] * widen), -7, dtype=torch.int32)
+        wide[:, : tables.shape[1]] = tables
+        tables = wide
+        max_kv = tables.shape[1] * ps if max_kv else 0
     flags = torch.zeros(1, dtype=torch.int32, device=dev)
     out = _run(mas, dev, q, kc, vc, tables, seq, cu, dim ** -0.5, flags=flags, ws_bytes=ws, max_kv=max_kv)
     assert int(flags.item()) == 0
