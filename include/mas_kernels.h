@@ -232,7 +232,9 @@ int mas_embedding_fill_placeholders_bf16(void* out, int64_t out_stride, const vo
  * partials fit (mas_paged_decode_attention_workspace_bytes), with at most 64 splits per row and
  * batch * num_kv_heads * splits within 16384 work items (longer splits past those). Grids of fewer
  * such items than the GPU has SIMDs split rows into 128 or 64 positions instead (at most 128 splits
- * per row), when the workspace holds those partials. A page id
+ * per row), when the workspace holds those partials. These lengths bound a row's splits; each row
+ * picks its own on the device from its length (256 positions, or 128 / 64 when the rows x kv heads
+ * leave 4+ SIMDs per row), so a block table far wider than the rows does not lengthen them. A page id
  * outside [0, num_pages) skips its position (MAS_ERRBIT_PAGE); a seq_len outside
  * [0, max_blocks * page_size] is clamped (MAS_ERRBIT_POSITION); a row with no position gets zeros.
  * With out_fp8, `out` receives e4m3fn codes (strides in elements, as for bf16): the output is
