@@ -768,8 +768,8 @@ def context_main(mas, args, shape, dev) -> int:
 
     def call():
         mas.attention.trtllm_batch_context_with_kv_cache(inp.q, (inp.k_cache, inp.v_cache), ws, inp.block_tables,
-                                                         inp.seq_lens, shape.q_len, shape.q_len + shape.cached,
-                                                         scale, 1.0, shape.rows, inp.cu_seqlens_q, None, out=out)
+                                                         inp.seq_lens, inp.max_q_len, inp.max_kv_len, scale, 1.0,
+                                                         inp.cu_seqlens_q.numel() - 1, inp.cu_seqlens_q, None, out=out)
 
     if args.pmc_probe:
         # 5 calls of the op and nothing else: a counter pass then sees only its dispatches
@@ -802,7 +802,9 @@ def context_main(mas, args, shape, dev) -> int:
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": shape.name, "rows": shape.rows, "q_len": shape.q_len, "cached": shape.cached,
                    "q_heads": shape.q_heads, "kv_heads": shape.kv_heads, "head_dim": shape.head_dim,
-                   "page_size": shape.page_size, "flops": flops, "launch": "hip-graph"},
+                   "page_size": shape.page_size, "flops": flops, "launch": "hip-graph",
+                   **({"graph_rows": shape.graph_rows, "max_q_len": inp.max_q_len, "max_kv_len": inp.max_kv_len}
+                      if shape.graph_rows else {})},
         "us_per_call": round(ms_per_step * 1e3, 3), "graph_us_per_call": round(timing["graph_s"] / steps * 1e6, 3),
         "host_us_per_call": round(timing["host_s"] / steps * 1e6, 3),
         "ops": {"paged_context_attention": {"us": round(call_us, 3), "TFLOP/s": round(kernel_tflops, 1),

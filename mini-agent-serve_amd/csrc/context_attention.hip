@@ -35,6 +35,23 @@ constexpr int kRowsPerWave = 32;  // query rows (tokens of one head) per wavefro
 constexpr int kMaxCtxSplits = 32;  // split-KV: key-range splits per token tile, at most
 constexpr float kNegInf = -__builtin_huge_valf();
 
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// How a launch maps workgroups to work:
+//   kWorkGrid  - one workgroup per (kv head block, token tile, row) of the host's grid;
+//   kWorkSplit - the same grid with each row's token tiles split over kv_splits key ranges (the
+//                split count picked on the host, from the grid's size);
+//   kWorkPlan  - one workgroup per item of a plan that context_plan wrote from the real lengths on
+//                the device (a graph captured with padded rows and token counts: the host only knows
+//                bounds, so the split decision waits for the lengths).
+constexpr int kWorkGrid = 0, kWorkSplit = 1, kWorkPlan = 2;
+
+// The planner: one workgroup; rows and (row, token tile) units it handles, at most.
+constexpr int kPlanThreads = 256;
+constexpr int kPlanMaxRows = 512;
+constexpr int kPlanMaxUnits = 2048;
+constexpr int kPlanMaxTokens = 1024;  // planned launches: the grid's token tiles cover at most this many tokens
+
 struct ContextArgs {
   const uint16_t* q;
   int64_t q_stride, q_head_stride;
@@ -55,6 +72,15 @@ struct ContextArgs {
   int kv_splits, row_tokens, split_from;
   float* part_o;
   float* part_ml;
+  // Planned launches (kWorkPlan): the plan's counts (items, split units, splits), its items (two
+  // i32x4 each: {q0, q_len, kv_len, row | split << 16 | splits << 24}, {tile | head block << 16,
+  // first key tile, end key tile, partial slot or -1}) and its split units ({q0, q_len, kv_len, row},
+  // {first token, splits used, splits, first partial slot}). Partials of slot s: (token of the
+  // tile, head of the block, split) entries at ((s * tokens + token) * heads + head) * splits + split.
+  const int* plan_hdr;
+  const i32x4* plan_items;
+  const i32x4* plan_units;
+  int plan_rows, plan_gy;  // the rows and token tiles per row of the unsplit grid
   float scale_log2;
   float out_scale;
   void* out;                // bf16, or fp8 e4m3fn codes when out_fp8
@@ -96,13 +122,72 @@ constexpr int kPagesLane = 0, kPagesStep = 1, kPagesTile = 2, kPagesStep1 = 3;
 // them evenly, at least 4 each (fewer splits then hold them all). From the tile's own reach, not
 // the block table's, so that a table much wider than the rows (a graph captured for the longest
 // context) still spreads each row over all the splits.
-__device__ __forceinline__ int split_tiles(int ntiles, int kv_splits) {
+__host__ __device__ __forceinline__ int split_tiles(int ntiles, int kv_splits) {
   return max(4, (ntiles + kv_splits - 1) / kv_splits);
 }
 
-// kSplit: a split-KV launch (a separate instance, so that the one-kernel instances keep their code).
-template <int D, int kPages, int kWaves, bool kSplit>
+// The split count's estimate, in microseconds fitted on MI355X, for a grid of `base` workgroups
+// whose token tiles each reach `tiles` key tiles, split k ways: (tiles per split + 4.8, a
+// workgroup's fixed cost) x 1.8 us with at most one workgroup per CU, else x 2.1 us per round of
+// resident workgroups, plus, when split, the merge (a launch, then its bytes at 5 TB/s or 0.6 ns
+// per (token, head), whichever is longer). The host evaluates it for its grid, the planner for the
+// real lengths.
+struct SplitModel {
+  int64_t base;               // workgroups of the unsplit grid
+  int64_t cus, resident;      // CUs, and workgroups resident at once
+  double merges;              // (token, head) pairs the merge visits
+  int64_t partial_per_split;  // bytes of partials per split
+  int64_t capacity;           // bytes of partials the workspace holds
+  int64_t max_splits;         // splits the launch can express
+};
+
+__host__ __device__ inline double split_cost(const SplitModel& m, int64_t k, int64_t tiles) {
+  const int64_t wgs = m.base * k;
+  const double per_wg = static_cast<double>(tiles) + 4.8;
+  double t = wgs <= m.cus ? per_wg * 1.8 : static_cast<double>((wgs + m.resident - 1) / m.resident) * per_wg * 2.1;
+  if (k > 1) t += 2.0 + fmax(static_cast<double>(m.partial_per_split * k) / 5.0e6, m.merges * 6.0e-4);
+  return t;
+}
+
+// The best split count for token tiles that all reach `reach` key tiles (1: no split): at most
+// kMaxCtxSplits of at least 4 tiles, at most two rounds of resident workgroups (a split grid whose
+// rows turn out shorter than the estimate assumed pays for its empty workgroups), partials within
+// the workspace, and 20% better than one kernel.
+__host__ __device__ inline int64_t best_splits(const SplitModel& m, int64_t reach) {
+  const int64_t grid_most = m.base > 0 ? (2 * m.resident / m.base > 1 ? 2 * m.resident / m.base : 1) : 1;
+  int64_t most = reach / 4;
+  if (most > kMaxCtxSplits) most = kMaxCtxSplits;
+  if (most > m.max_splits) most = m.max_splits;
+  if (most > grid_most) most = grid_most;
+  double best = 0.8 * split_cost(m, 1, reach);
+  int64_t k_best = 1;
+  for (int64_t k = 2; k <= most; ++k) {
+    const int64_t tiles = (reach + k - 1) / k;
+    if ((reach + tiles - 1) / tiles != k) continue;  // the same split as a smaller count
+    if (m.partial_per_split * k > m.capacity) break;
+    if (const double c = split_cost(m, k, tiles); c < best) {
+      best = c;
+      k_best = k;
+    }
+  }
+  return k_best;
+}
+
+// The shortest reach (in powers of two from 4) worth splitting, for a split count picked at
+// `hint` key tiles: token tiles reaching fewer (rows shorter than the hint, as under a graph's
+// table far wider than its rows) are computed whole.
+__host__ __device__ inline int64_t split_from_reach(const SplitModel& m, int64_t hint) {
+  for (int64_t reach = 4; reach < hint; reach *= 2)
+    if (best_splits(m, reach) > 1) return reach;
+  return hint;
+}
+
+// kWork: how workgroups map to work (each a separate instance, so that the one-kernel instances
+// keep their code).
+template <int D, int kPages, int kWaves, int kWork>
 __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextArgs a) {
+  constexpr bool kSplit = kWork == kWorkSplit;
+  constexpr bool kPlan = kWork == kWorkPlan;
   constexpr int kCtxWaves = kWaves;
   constexpr int kCtxThreads = 64 * kWaves;
   constexpr int KS = D / 16;            // MFMA k-steps over the head dim (S^T)
@@ -120,24 +205,55 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id_uniform();
   const int n = lane & 31, hf = lane >> 5;  // this lane's query row (token) and lane half
   const int hgroups = (a.group + a.heads_per_wg - 1) / a.heads_per_wg;
-  const int kvh = blockIdx.x / hgroups, hg = blockIdx.x - kvh * hgroups;
-  const int row = kSplit ? blockIdx.z / a.kv_splits : blockIdx.z;
-  const int split = kSplit ? blockIdx.z - row * a.kv_splits : 0;
-  const int q0 = a.cu_seqlens_q[row], q_len = a.cu_seqlens_q[row + 1] - q0;
+  // A planned launch's item. Unsplit plans are the grid launch's workgroups in its order, taken from
+  // the workgroup id: their lengths are loaded in the same round trip as the plan's counts (row
+  // clamped to the last), as the grid launch loads them, and no item is read. Split plans' items
+  // are read from the plan; workgroups past the plan's count exit (the item array holds one slot
+  // per workgroup of the grid, so the load stays inside it).
+  i32x4 d0{}, d1{};
+  if constexpr (kPlan) {
+    const int n_items = a.plan_hdr[0], plan_splits = a.plan_hdr[2];
+    const unsigned per_row = static_cast<unsigned>(a.plan_gy) * (a.hk * hgroups);
+    const unsigned grid_row = blockIdx.x / per_row, rem = blockIdx.x - grid_row * per_row;
+    const int row_ld = static_cast<int>(min(grid_row, static_cast<unsigned>(a.plan_rows - 1)));
+    const int cu0 = a.cu_seqlens_q[row_ld], cu1 = a.cu_seqlens_q[row_ld + 1], len = a.seq_lens[row_ld];
+    if (static_cast<int>(blockIdx.x) >= n_items) return;
+    if (plan_splits == 1) {
+      const unsigned y = rem / (a.hk * hgroups), block = rem - y * (a.hk * hgroups);
+      const int tile = a.plan_gy - 1 - static_cast<int>(y);
+      d0 = i32x4{cu0, cu1 - cu0, len, row_ld | (1 << 24)};
+      d1 = i32x4{tile | static_cast<int>(block << 16), 0, INT32_MAX, -1};
+    } else {
+      d0 = a.plan_items[2 * blockIdx.x];
+      d1 = a.plan_items[2 * blockIdx.x + 1];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        d0[e] = __builtin_amdgcn_readfirstlane(d0[e]);
+        d1[e] = __builtin_amdgcn_readfirstlane(d1[e]);
+      }
+    }
+  }
+  const unsigned head_block = kPlan ? static_cast<unsigned>(d1[0]) >> 16 : blockIdx.x;
+  const int kvh = head_block / hgroups, hg = head_block - kvh * hgroups;
+  const int row = kPlan ? d0[3] & 0xffff : (kSplit ? blockIdx.z / a.kv_splits : blockIdx.z);
+  const int split = kPlan ? (d0[3] >> 16) & 0xff : (kSplit ? blockIdx.z - row * a.kv_splits : 0);
+  const int q0 = kPlan ? d0[0] : a.cu_seqlens_q[row];
+  const int q_len = kPlan ? d0[1] : a.cu_seqlens_q[row + 1] - q0;
   const int tokens_per_wg = kRowsPerWave * (kCtxWaves / a.heads_per_wg);
   // Token tiles in reverse launch order: the last tiles reach the most positions, so they start first.
-  const int tile_idx = static_cast<int>(gridDim.y - 1 - blockIdx.y);
+  const int tile_idx = kPlan ? d1[0] & 0xffff : static_cast<int>(gridDim.y - 1 - blockIdx.y);
   const int tile_tok = tile_idx * tokens_per_wg;
   if (tile_tok >= q_len) return;  // uniform over the workgroup
   // kv_len clamped to the block table's reach; a kv_len below q_len leaves the first tokens with
   // negative positions: they see no key and get zeros.
   const int64_t cap = a.max_blocks << a.log2_page;
-  const int64_t raw_len = a.seq_lens[row];
+  const int64_t raw_len = kPlan ? d0[2] : a.seq_lens[row];
   // Error bits are reported at the end: a global atomic before the tile loop would keep the
   // compiler from reading the block table through the scalar cache.
   // also flagged: a row with more query tokens than the grid covers (max_q_len too small); the
-  // tokens past the grid are left unwritten
-  const bool len_bad = raw_len < q_len || raw_len > cap || q_len > static_cast<int>(gridDim.y) * tokens_per_wg;
+  // tokens past the grid are left unwritten. The planner reports these for planned launches.
+  const bool len_bad =
+      !kPlan && (raw_len < q_len || raw_len > cap || q_len > static_cast<int>(gridDim.y) * tokens_per_wg);
   const int kv_len = static_cast<int>(raw_len < 0 ? 0 : (raw_len > cap ? cap : raw_len));
   const int shift = kv_len - q_len;  // position of query token i = shift + i
 
@@ -167,11 +283,12 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   const int last_tok = min(tile_tok + tokens_per_wg, q_len) - 1;
   const int reach = shift + last_tok + 1;  // <= kv_len
   const int ntiles = reach > 0 ? (reach + kTileP - 1) / kTileP : 0;
-  // This workgroup's key tiles: all of them, or its split's share.
-  const bool split_tile = kSplit && ntiles >= a.split_from;
-  const int per_split = split_tile ? split_tiles(ntiles, a.kv_splits) : ntiles;
-  const int it_begin = kSplit ? split * per_split : 0;
-  const int it_end = !split_tile || split == a.kv_splits - 1 ? ntiles : min(ntiles, it_begin + per_split);
+  // This workgroup's key tiles: all of them, or its split's share (a planned item carries its range).
+  const bool split_tile = kPlan ? d1[3] >= 0 : kSplit && ntiles >= a.split_from;
+  const int per_split = split_tile && !kPlan ? split_tiles(ntiles, a.kv_splits) : ntiles;
+  const int it_begin = kPlan ? max(d1[1], 0) : (kSplit ? split * per_split : 0);
+  const int it_end = kPlan ? min(d1[2], ntiles)
+                           : (!split_tile || split == a.kv_splits - 1 ? ntiles : min(ntiles, it_begin + per_split));
   // an empty split (uniform), which the merge skips; split 0 of a tile that is not split goes on,
   // to write its output (zeros for a tile that reaches no key)
   if (kSplit && it_begin >= it_end && (split_tile || split > 0)) {
@@ -414,20 +531,21 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   TileRegs tr;
   // Software pipeline over tiles: tile it + 1's scores (MFMA, keys from the other LDS buffer) are
   // computed in the same block as tile it's softmax (VALU), so the two overlap; then tile it's P.V.
-  // Buffer it & 1 holds tile it, buffer (it + 1) & 1 tile it + 1 (staged after the barrier that
-  // ends every read of tile it - 1, which used that buffer).
+  // Buffer (it - it_begin) & 1 holds tile it, the other one tile it + 1 (staged after the barrier
+  // that ends every read of tile it - 1, which used that buffer). The parity is counted from the
+  // workgroup's first tile, so that it is a constant at each call of step even where the first tile
+  // is not known at compile time (split ranges): LDS addresses then fold into the instructions.
   f32x16 s_a[2], s_b[2];
   if (it_begin < it_end) {
     issue_tile(tr, it_begin * kTileP);
-    stage(tr, it_begin & 1);
+    stage(tr, 0);
     __syncthreads();
     if (it_begin + 1 < it_end) issue_tile(tr, (it_begin + 1) * kTileP);
-    if (wave_live) scores(it_begin & 1, s_a);
+    if (wave_live) scores(0, s_a);
   }
-  // One tile; `cur` holds its scores, `nxt` receives the next tile's. Called with the two score
-  // arrays in turn (no copy between them).
-  auto step = [&](int it, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
-    const int buf = it & 1;
+  // One tile in buffer `buf`; `cur` holds its scores, `nxt` receives the next tile's. Called with
+  // the two score arrays in turn (no copy between them).
+  auto step = [&](int it, int buf, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
     __syncthreads();  // tile it - 1's reads (of buffer buf ^ 1) are done
     if (it + 1 < it_end) stage(tr, buf ^ 1);
     __syncthreads();
@@ -443,10 +561,10 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   };
   int it = it_begin;
   for (; it + 1 < it_end; it += 2) {
-    step(it, s_a, s_b);
-    step(it + 1, s_b, s_a);
+    step(it, 0, s_a, s_b);
+    step(it + 1, 1, s_b, s_a);
   }
-  if (it < it_end) step(it, s_a, s_b);
+  if (it < it_end) step(it, 0, s_a, s_b);
   if (__builtin_amdgcn_ballot_w64(page_bad) != 0 && lane == 0) report(a.err, MAS_ERRBIT_PAGE);
   // reported by the workgroup of token tile 0, which every row with a query token has
   if (len_bad && tid == 0 && blockIdx.x == 0 && tile_idx == 0) report(a.err, MAS_ERRBIT_POSITION);
@@ -457,7 +575,10 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   if (split_tile) {
     // ---- this split's partial: O row (lane half hf holds columns 32 db + 8 q + 4 hf .. + 3) and
     // (max, sum), both halves holding the same (max, sum)
-    const int64_t pi = ((static_cast<int64_t>(row) * a.row_tokens + t) * a.hq + h) * a.kv_splits + split;
+    const int64_t pi =
+        kPlan ? ((static_cast<int64_t>(d1[3]) * tokens_per_wg + (t - tile_tok)) * a.heads_per_wg + hsub) *
+                        ((d0[3] >> 24) & 0xff) + split
+              : ((static_cast<int64_t>(row) * a.row_tokens + t) * a.hq + h) * a.kv_splits + split;
     float* po = a.part_o + pi * D + 4 * hf;
 #pragma unroll
     for (int db = 0; db < DB; ++db)
@@ -494,32 +615,16 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   }
 }
 
-// One wavefront per (row, token, query head) of a split-KV launch: merges the token's non-empty
-// splits with weights 2^(c (m_s - max m)) (c = bmm1_scale * log2 e, maxima in raw score units as
-// the split kernel keeps them) and writes O / l * bmm2_scale as bf16, or its fp8 quantize. Every
-// load is issued in one round trip: lane s reads split s's (max, sum) and 16 (32 past 16 splits)
-// partial O rows are loaded (indices past the last split clamped to it, weighted 0) before the
-// max is known. A token that sees no position (all maxima -inf) gets zeros.
+// Merges one (token, query head)'s nsplit partials, stored from index `base` on, with weights
+// 2^(c (m_s - max m)) (c = bmm1_scale * log2 e, maxima in raw score units as the split kernel keeps
+// them) and writes O / l * bmm2_scale as bf16, or its fp8 quantize, to output token `token`, head
+// `h`. Every load is issued in one round trip: lane s reads split s's (max, sum) and 16 (32 past 16
+// splits) partial O rows are loaded (indices past the last split clamped to it, weighted 0) before
+// the max is known. A token that sees no position (all maxima -inf) gets zeros.
 template <int D>
-__global__ __launch_bounds__(64) void context_combine(ContextArgs a, int tokens_per_wg) {
+__device__ __forceinline__ void merge_partials(const ContextArgs& a, int64_t base, int nsplit, int64_t token, int h,
+                                               int lane) {
   constexpr int DPL = D / 64;  // head-dim elements per lane
-  const int lane = threadIdx.x;
-  const int id = static_cast<int>(blockIdx.x);  // < rows * row_tokens * hq <= 2^31 - 1 (host-checked)
-  const int rt = id / a.hq, h = id - rt * a.hq;
-  const int row = rt / a.row_tokens, t = rt - row * a.row_tokens;
-  const int q0 = a.cu_seqlens_q[row], q_len = a.cu_seqlens_q[row + 1] - q0;
-  if (t >= q_len) return;
-  // the token tile's key tiles, as the split kernel counts them
-  const int64_t cap = a.max_blocks << a.log2_page;
-  const int64_t raw_len = a.seq_lens[row];
-  const int kv_len = static_cast<int>(raw_len < 0 ? 0 : (raw_len > cap ? cap : raw_len));
-  const int tile_tok = t / tokens_per_wg * tokens_per_wg;
-  const int reach = kv_len - q_len + min(tile_tok + tokens_per_wg, q_len);
-  const int ntiles = reach > 0 ? (reach + kTileP - 1) / kTileP : 0;
-  if (ntiles < a.split_from) return;  // not split: the split kernel wrote this token's output
-  const int per_split = split_tiles(ntiles, a.kv_splits);
-  const int nsplit = min(a.kv_splits, (ntiles + per_split - 1) / per_split);  // <= kMaxCtxSplits
-  const int64_t base = ((static_cast<int64_t>(row) * a.row_tokens + t) * a.hq + h) * a.kv_splits;
   float acc[DPL], l = 0.f;
 #pragma unroll
   for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
@@ -569,7 +674,7 @@ __global__ __launch_bounds__(64) void context_combine(ContextArgs a, int tokens_
     }
   }
   const float sc = l > 0.f ? a.out_scale / l : 0.f;
-  const int64_t at = static_cast<int64_t>(q0 + t) * a.out_stride + h * a.out_head_stride + DPL * lane;
+  const int64_t at = token * a.out_stride + h * a.out_head_stride + DPL * lane;
   uint32_t y[(DPL + 1) / 2];
   if constexpr (DPL == 1) {
     y[0] = pack_bf16x2(acc[0] * sc, 0.f);
@@ -604,14 +709,319 @@ __global__ __launch_bounds__(64) void context_combine(ContextArgs a, int tokens_
   }
 }
 
-template <int D, int kWaves, bool kSplit>
+// One wavefront per (row, token, query head) of a split-KV launch: merges the token's non-empty
+// splits (merge_partials).
+template <int D>
+__global__ __launch_bounds__(64) void context_combine(ContextArgs a, int tokens_per_wg) {
+  const int lane = threadIdx.x;
+  const int id = static_cast<int>(blockIdx.x);  // < rows * row_tokens * hq <= 2^31 - 1 (host-checked)
+  const int rt = id / a.hq, h = id - rt * a.hq;
+  const int row = rt / a.row_tokens, t = rt - row * a.row_tokens;
+  const int q0 = a.cu_seqlens_q[row], q_len = a.cu_seqlens_q[row + 1] - q0;
+  if (t >= q_len) return;
+  // the token tile's key tiles, as the split kernel counts them
+  const int64_t cap = a.max_blocks << a.log2_page;
+  const int64_t raw_len = a.seq_lens[row];
+  const int kv_len = static_cast<int>(raw_len < 0 ? 0 : (raw_len > cap ? cap : raw_len));
+  const int tile_tok = t / tokens_per_wg * tokens_per_wg;
+  const int reach = kv_len - q_len + min(tile_tok + tokens_per_wg, q_len);
+  const int ntiles = reach > 0 ? (reach + kTileP - 1) / kTileP : 0;
+  if (ntiles < a.split_from) return;  // not split: the split kernel wrote this token's output
+  const int per_split = split_tiles(ntiles, a.kv_splits);
+  const int nsplit = min(a.kv_splits, (ntiles + per_split - 1) / per_split);  // <= kMaxCtxSplits
+  const int64_t base = ((static_cast<int64_t>(row) * a.row_tokens + t) * a.hq + h) * a.kv_splits;
+  merge_partials<D>(a, base, nsplit, q0 + t, h, lane);
+}
+
+// The merge of a planned launch: its split units' (token, query head) pairs, one per wavefront in
+// turn (a fixed grid: the plan's size is known only on the device).
+constexpr int kMergeWaves = 8;  // wavefronts per workgroup of the planned merge
+
+template <int D>
+__global__ __launch_bounds__(64 * kMergeWaves) void context_combine_plan(ContextArgs a, int tokens_per_wg) {
+  const int lane = threadIdx.x & 63;
+  const int n_units = a.plan_hdr[1];
+  const int per_unit = tokens_per_wg * a.hq;  // pairs per split unit; n_units * per_unit <= 2^31 - 1 (host-checked)
+  const int total = n_units * per_unit;
+  const int hgroups = (a.group + a.heads_per_wg - 1) / a.heads_per_wg;
+  const int waves = static_cast<int>(gridDim.x) * kMergeWaves;
+  for (int m = static_cast<int>(blockIdx.x) * kMergeWaves + wave_id_uniform(); m < total; m += waves) {
+    const int su = m / per_unit, r = m - su * per_unit;
+    const int j = r / a.hq, h = r - j * a.hq;  // token of the unit's tile, query head
+    const i32x4 u0 = a.plan_units[2 * su], u1 = a.plan_units[2 * su + 1];
+    const int q0 = __builtin_amdgcn_readfirstlane(u0[0]), q_len = __builtin_amdgcn_readfirstlane(u0[1]);
+    const int t = __builtin_amdgcn_readfirstlane(u1[0]) + j;
+    if (t >= q_len) continue;
+    const int nsplit = __builtin_amdgcn_readfirstlane(u1[1]), splits = __builtin_amdgcn_readfirstlane(u1[2]);
+    const int kvh = h / a.group, g = h - kvh * a.group, hg = g / a.heads_per_wg, hs = g - hg * a.heads_per_wg;
+    const int slot = __builtin_amdgcn_readfirstlane(u1[3]) + kvh * hgroups + hg;
+    const int64_t base = ((static_cast<int64_t>(slot) * tokens_per_wg + j) * a.heads_per_wg + hs) * splits;
+    merge_partials<D>(a, base, nsplit, q0 + t, h, lane);
+  }
+}
+
+// ---- the planner of planned launches ----------------------------------------------------------
+
+struct PlanArgs {
+  const int32_t* cu_seqlens_q;
+  const int32_t* seq_lens;
+  int rows, gy, tokens_per_wg, heads_per_wg, head_blocks, hq, head_dim;
+  int64_t cap;         // positions the block table reaches
+  int64_t cus, resident;
+  int64_t item_cap;    // items the main grid has workgroups for
+  int64_t entry_cap;   // partial entries ((token, head, split)) the workspace holds
+  int* hdr;
+  i32x4* items;
+  i32x4* units;
+  uint32_t* err;
+};
+
+// Exclusive prefix sum of v[0..n) in place, v[n] = the total, which every thread gets back.
+__device__ int plan_scan(int* v, int n, int* slots) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __syncthreads();  // v written, slots free
+  const int per = (n + kPlanThreads - 1) / kPlanThreads;
+  const int lo = min(n, tid * per), hi = min(n, lo + per);
+  int sum = 0;
+  for (int i = lo; i < hi; ++i) sum += v[i];
+  int x = sum;  // inclusive scan over the wavefront
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(x, d);
+    if (lane >= d) x += y;
+  }
+  if (lane == 63) slots[wave] = x;
+  __syncthreads();
+  int run = x - sum, total = 0;
+#pragma unroll
+  for (int w = 0; w < kPlanThreads / 64; ++w) {
+    if (w < wave) run += slots[w];
+    total += slots[w];
+  }
+  for (int i = lo; i < hi; ++i) {
+    const int c = v[i];
+    v[i] = run;
+    run += c;
+  }
+  if (tid == 0) v[n] = total;
+  __syncthreads();
+  return total;
+}
+
+__device__ int plan_max(int x, int* slots) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) x = max(x, __shfl_xor(x, d));
+  __syncthreads();
+  if ((tid & 63) == 0) slots[tid >> 6] = x;
+  __syncthreads();
+  int m = slots[0];
+#pragma unroll
+  for (int w = 1; w < kPlanThreads / 64; ++w) m = max(m, slots[w]);
+  return m;
+}
+
+// The split estimate of SplitModel in fp32 for the planner, one split count per lane.
+struct PlanModel {
+  int base, cus, resident;
+  float merges;  // (token, head) pairs the merge visits
+  float pps_us;  // microseconds to move one split's partials at 5 TB/s
+  int most_k;    // splits whose partials the workspace holds
+};
+
+__device__ float plan_cost(const PlanModel& m, int k, int tiles) {
+  const int wgs = m.base * k;
+  const float per_wg = static_cast<float>(tiles) + 4.8f;
+  float t = wgs <= m.cus ? per_wg * 1.8f : static_cast<float>((wgs + m.resident - 1) / m.resident) * per_wg * 2.1f;
+  if (k > 1) t += 2.0f + fmaxf(m.pps_us * static_cast<float>(k), m.merges * 6.0e-4f);
+  return t;
+}
+
+// The estimate for k splits of a reach (infinite where best_splits does not weigh k: past its
+// limits, or the same split as a smaller count).
+__device__ float plan_split_cost(const PlanModel& m, int reach, int k) {
+  const int grid_most = max(1, 2 * m.resident / m.base);
+  const int most = min(min(reach / 4, kMaxCtxSplits), min(grid_most, m.most_k));
+  if (k > most) return __builtin_huge_valf();
+  const int tiles = (reach + k - 1) / k;
+  return (reach + tiles - 1) / tiles == k ? plan_cost(m, k, tiles) : __builtin_huge_valf();
+}
+
+// Whether k splits of the reach beat one kernel by 20% (best_splits > 1 iff some k does).
+__device__ bool plan_splits_pay(const PlanModel& m, int reach, int k) {
+  return plan_split_cost(m, reach, k) < 0.8f * plan_cost(m, 1, reach);
+}
+
+// best_splits for a wavefront-uniform reach, lane l weighing l + 2 splits: the smallest count of
+// least cost, if it beats one kernel by 20% (else 1).
+__device__ int plan_best_splits(const PlanModel& m, int reach, int lane) {
+  const float c = plan_split_cost(m, reach, lane + 2);
+  float low = c;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) low = fminf(low, __shfl_xor(low, d));
+  if (!(low < 0.8f * plan_cost(m, 1, reach))) return 1;
+  return __builtin_ctzll(__ballot(c == low)) + 2;
+}
+
+// Lays out a planned launch from the real lengths (one workgroup). Units are a row's token tiles,
+// longest reach first; the split count comes from the same estimate the host uses for its grids
+// (SplitModel), evaluated for the units there are and the longest reach among them; a unit whose
+// tile reaches at least split_from key tiles is split into its non-empty key ranges
+// (split_tiles), each range an item per head block, and its partials get a slot per head block;
+// every other unit is one item per head block that writes its output. Rows' length errors are
+// reported here, as the grid launch reports them (a row with query tokens: kv_len below q_len or
+// past the block table, or more tokens than the grid's token tiles cover, which are left
+// unwritten).
+__global__ __launch_bounds__(kPlanThreads) void context_plan(PlanArgs p) {
+  __shared__ int r_q0[kPlanMaxRows], r_qlen[kPlanMaxRows], r_kv[kPlanMaxRows], r_unit[kPlanMaxRows + 1];
+  __shared__ int u_row[kPlanMaxUnits], u_tile[kPlanMaxUnits], u_nt[kPlanMaxUnits];
+  __shared__ int u_item[kPlanMaxUnits + 1], u_slot[kPlanMaxUnits + 1];
+  __shared__ int slots[kPlanThreads / 64];
+  __shared__ int params[1];
+  __shared__ int found[kPlanThreads / 32];
+  const int tid = threadIdx.x;
+
+  // rows: lengths and token tiles
+  bool bad = false;
+  for (int r = tid; r < p.rows; r += kPlanThreads) {
+    const int q0 = p.cu_seqlens_q[r];
+    const int64_t q_len = static_cast<int64_t>(p.cu_seqlens_q[r + 1]) - q0;
+    const int64_t raw = p.seq_lens[r];
+    int tiles = 0;
+    if (q_len > 0) {
+      const int64_t covered = static_cast<int64_t>(p.gy) * p.tokens_per_wg;
+      tiles = static_cast<int>((min(q_len, covered) + p.tokens_per_wg - 1) / p.tokens_per_wg);
+      bad = bad || raw < q_len || raw > p.cap || q_len > covered;
+    }
+    r_q0[r] = q0;
+    r_qlen[r] = q_len > 0 ? static_cast<int>(q_len) : 0;
+    r_kv[r] = static_cast<int>(raw < 0 ? 0 : (raw > p.cap ? p.cap : raw));
+    r_unit[r] = tiles;
+  }
+  if (__syncthreads_or(bad) && tid == 0) report(p.err, MAS_ERRBIT_POSITION);
+  const int units = plan_scan(r_unit, p.rows, slots);  // <= rows * gy <= kPlanMaxUnits (host-checked)
+
+  // units: each row's token tiles, the last (longest reach) first
+  int longest = 0;
+  for (int r = tid; r < p.rows; r += kPlanThreads) {
+    const int first = r_unit[r], tiles = r_unit[r + 1] - first;
+    const int q_len = r_qlen[r], shift = r_kv[r] - q_len;
+    for (int i = 0; i < tiles; ++i) {
+      const int tile = tiles - 1 - i;
+      const int reach = shift + min((tile + 1) * p.tokens_per_wg, q_len);
+      const int nt = reach > 0 ? (reach + kTileP - 1) / kTileP : 0;
+      u_row[first + i] = r;
+      u_tile[first + i] = tile;
+      u_nt[first + i] = nt;
+      longest = max(longest, nt);
+    }
+  }
+  longest = plan_max(longest, slots);
+
+  // the split count at the longest reach (wavefront 0, a split count per lane), then the shortest
+  // reach worth splitting (all threads: 8 reaches x 32 split counts per pass)
+  PlanModel m{};
+  const int base = units * p.head_blocks;
+  const bool may_split = units > 0 && base < p.cus;
+  if (may_split) {
+    const float entry_bytes = (p.head_dim + 2) * 4.f;
+    m.base = base;
+    m.cus = static_cast<int>(p.cus);
+    m.resident = static_cast<int>(p.resident);
+    m.merges = static_cast<float>(units) * p.tokens_per_wg * p.hq;
+    m.pps_us = static_cast<float>(base) * p.tokens_per_wg * p.heads_per_wg * entry_bytes / 5.0e6f;
+    m.most_k = static_cast<int>(min(static_cast<int64_t>(kMaxCtxSplits),
+                                    p.entry_cap / (static_cast<int64_t>(base) * p.tokens_per_wg * p.heads_per_wg)));
+  }
+  if (tid < 64) {
+    const int best = may_split ? plan_best_splits(m, longest, tid) : 1;
+    if (tid == 0) params[0] = best;
+  }
+  __syncthreads();
+  int splits = params[0];
+  int from = INT32_MAX;
+  if (splits > 1) {
+    from = longest;
+    for (int pass = 0; pass < 3 && from == longest; ++pass) {  // the same trip count in every thread
+      const int ri = (tid >> 5) + 8 * pass;
+      const int reach = ri < 24 ? 4 << ri : INT32_MAX;
+      const bool ok = reach < longest && plan_splits_pay(m, reach, (tid & 31) + 2);
+      const uint64_t hits = __ballot(ok);
+      if ((tid & 31) == 0) found[tid >> 5] = ((tid & 32) ? hits >> 32 : hits & 0xffffffffu) != 0;
+      __syncthreads();
+#pragma unroll
+      for (int i = 7; i >= 0; --i)
+        if (found[i]) from = 4 << (i + 8 * pass);
+      __syncthreads();
+    }
+  }
+
+  // items and partial slots per unit; no split if the grid or the workspace would not hold them
+  int items = 0, split_units = 0;
+  if (splits > 1) {
+    for (int u = tid; u < units; u += kPlanThreads) {
+      const int nt = u_nt[u];
+      int used = 1;
+      if (nt >= from) {
+        const int per = split_tiles(nt, splits);
+        used = (nt + per - 1) / per;
+      }
+      u_item[u] = used * p.head_blocks;
+      u_slot[u] = used > 1 ? 1 : 0;
+    }
+    items = plan_scan(u_item, units, slots);
+    split_units = plan_scan(u_slot, units, slots);
+    const bool fits = items <= p.item_cap &&
+                      static_cast<int64_t>(split_units) * p.head_blocks * p.tokens_per_wg * p.heads_per_wg * splits <=
+                          p.entry_cap;
+    if (!fits) splits = 1;  // the same totals in every thread
+  }
+
+  if (splits == 1) {
+    // No split: the launch is the grid launch, each workgroup finding its (head block, token tile,
+    // row) from its id and loading its row's lengths itself; no items are written.
+    split_units = 0;
+    items = p.rows * p.gy * p.head_blocks;  // <= item_cap (host-checked)
+  } else {
+    // items in unit order: unit u's items are its key ranges x head blocks (head block fastest),
+    // from u_item[u] on; one thread per (unit, head block) writes that block's ranges
+    for (int j = tid; j < units * p.head_blocks; j += kPlanThreads) {
+      const int u = j / p.head_blocks, block = j - u * p.head_blocks;
+      const int used = (u_item[u + 1] - u_item[u]) / p.head_blocks;
+      const int r = u_row[u], nt = u_nt[u];
+      const int per = used > 1 ? split_tiles(nt, splits) : nt;
+      const int slot = used > 1 ? u_slot[u] * p.head_blocks + block : -1;
+      for (int range = 0; range < used; ++range) {
+        const int i = u_item[u] + range * p.head_blocks + block, first = range * per;
+        p.items[2 * i] = i32x4{r_q0[r], r_qlen[r], r_kv[r], r | (range << 16) | (splits << 24)};
+        p.items[2 * i + 1] = i32x4{u_tile[u] | (block << 16), first, min(nt, first + per), slot};
+      }
+    }
+  }
+  // split units, for the merge
+  for (int u = tid; u < units && split_units > 0; u += kPlanThreads) {
+    const int used = (u_item[u + 1] - u_item[u]) / p.head_blocks;
+    if (used > 1) {
+      const int su = u_slot[u], r = u_row[u];
+      p.units[2 * su] = i32x4{r_q0[r], r_qlen[r], r_kv[r], r};
+      p.units[2 * su + 1] = i32x4{u_tile[u] * p.tokens_per_wg, used, splits, su * p.head_blocks};
+    }
+  }
+  if (tid == 0) {
+    p.hdr[0] = items;
+    p.hdr[1] = split_units;
+    p.hdr[2] = splits;
+  }
+}
+
+template <int D, int kWaves, int kWork>
 void launch_context_mode(int mode, dim3 grid, dim3 block, hipStream_t stream, const ContextArgs& a) {
-  if (mode == kPagesTile) hipLaunchKernelGGL((context_attn<D, kPagesTile, kWaves, kSplit>), grid, block, 0, stream, a);
+  if (mode == kPagesTile) hipLaunchKernelGGL((context_attn<D, kPagesTile, kWaves, kWork>), grid, block, 0, stream, a);
   else if (mode == kPagesStep1)
-    hipLaunchKernelGGL((context_attn<D, kPagesStep1, kWaves, kSplit>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((context_attn<D, kPagesStep1, kWaves, kWork>), grid, block, 0, stream, a);
   else if (mode == kPagesStep)
-    hipLaunchKernelGGL((context_attn<D, kPagesStep, kWaves, kSplit>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((context_attn<D, kPagesLane, kWaves, kSplit>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((context_attn<D, kPagesStep, kWaves, kWork>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((context_attn<D, kPagesLane, kWaves, kWork>), grid, block, 0, stream, a);
 }
 
 // Workgroup shape for a query-head group: heads per workgroup, wavefronts, and query tokens per
@@ -634,16 +1044,29 @@ int64_t context_partial_bytes(int64_t rows, int64_t row_tokens, int64_t num_q_he
   return rows * row_tokens * num_q_heads * splits * (head_dim + 2) * 4;
 }
 
-template <bool kSplit>
+template <int kWork>
 void launch_context(int64_t head_dim, int waves, int mode, dim3 grid, dim3 block, hipStream_t stream,
                     const ContextArgs& a) {
   if (head_dim == 64) {
-    if (waves == 8) launch_context_mode<64, 8, kSplit>(mode, grid, block, stream, a);
-    else launch_context_mode<64, 4, kSplit>(mode, grid, block, stream, a);
+    if (waves == 8) launch_context_mode<64, 8, kWork>(mode, grid, block, stream, a);
+    else launch_context_mode<64, 4, kWork>(mode, grid, block, stream, a);
   } else {
-    if (waves == 8) launch_context_mode<128, 8, kSplit>(mode, grid, block, stream, a);
-    else launch_context_mode<128, 4, kSplit>(mode, grid, block, stream, a);
+    if (waves == 8) launch_context_mode<128, 8, kWork>(mode, grid, block, stream, a);
+    else launch_context_mode<128, 4, kWork>(mode, grid, block, stream, a);
   }
+}
+
+// The workspace of a planned launch: the plan's counts (256 bytes), its items (32 bytes per
+// workgroup of the grid), its split units (32 bytes per unit), then the partials.
+struct PlanLayout {
+  int64_t item_cap, units_bound, partial_off;
+};
+
+PlanLayout plan_layout(int64_t units_bound, int64_t head_blocks, int64_t resident) {
+  // items: at most one per (unit, head block) unsplit; split, the estimate keeps the grid within
+  // two rounds of resident workgroups (best_splits)
+  const int64_t item_cap = std::max(units_bound * head_blocks, 2 * resident);
+  return {item_cap, units_bound, 256 + 32 * item_cap + 32 * units_bound};
 }
 
 }  // namespace
@@ -691,67 +1114,59 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   // each token tile's key range is split over up to kMaxCtxSplits workgroups of at least 4 key
   // tiles each, when the workspace holds the partials (workspace_bytes 0: no split). Each token
   // tile divides its own key tiles among the splits (split_tiles); max_kv_len (if positive, else
-  // the block table's reach) only sizes the estimate that picks the split count. The split count
-  // minimises an estimate in microseconds fitted on MI355X: (tiles per split + 4.8, a workgroup's
-  // fixed cost) x 1.8 us with at most one workgroup per CU, else x 2.1 us per round of resident
-  // workgroups, plus, when split, the merge (a launch, then its bytes at 5 TB/s or 0.6 ns per
-  // (token, head), whichever is longer); a split must beat the one-kernel estimate by 20%. Whole
-  // rounds matter: one row of 256 new tokens after 2048 (64 workgroups) took 39 us in 8 splits
-  // (512 workgroups, one round of two per CU) and 49 us in 9. The merge's per-(token, head) cost
-  // decides for many short rows: 24 rows of 32 new tokens after 512 took 26.6 us unsplit and
+  // the block table's reach) only sizes the estimate that picks the split count (SplitModel).
+  // Whole rounds matter: one row of 256 new tokens after 2048 (64 workgroups) took 39 us in 8
+  // splits (512 workgroups, one round of two per CU) and 49 us in 9. The merge's per-(token, head)
+  // cost decides for many short rows: 24 rows of 32 new tokens after 512 took 26.6 us unsplit and
   // 44.9 in 2 splits. A grid with a workgroup on every CU gains nothing (4 rows of 256 after
   // 8192: 256 workgroups, 237 us either way) and is not split.
+  //
+  // Planned: a grid sized for several rows of up to kPlanMaxTokens query tokens that holds a
+  // workgroup per CU or more may still be mostly empty (a graph captured with padded prompt rows
+  // and the step's whole token count as max_q_len; the rows' real lengths are on the device). When
+  // the smallest grid it could hold (one token tile) would split at the hint's reach, context_plan
+  // lays the launch out from the real lengths first: the same estimate on the real grid, one
+  // workgroup per item, and a merge over the split tiles only.
   const int64_t row_tokens = gy * tokens_per_wg;
-  auto partial_bytes = [&](int64_t splits) {
-    return context_partial_bytes(num_rows, row_tokens, num_q_heads, head_dim, splits);
-  };
+  const int64_t entry_bytes = (head_dim + 2) * 4;
+  const int64_t units_bound = num_rows * gy;
   int64_t kv_splits = 1, split_from = INT32_MAX;
   const int64_t base_wgs = gx * gy * num_rows;
+  bool planned = false;
+  PlanLayout plan{};
+  int64_t plan_entries = 0;
+  int cus = 0;
+  int64_t resident = 0;
   if (workspace != nullptr && workspace_bytes > 0 && (reinterpret_cast<uintptr_t>(workspace) & 15u) == 0) {
-    int cus = 0;
     if (const int st = device_cu_count(&cus); st != MAS_OK) return st;
-    const int64_t resident = static_cast<int64_t>(cus) * (8 / waves);
+    resident = static_cast<int64_t>(cus) * (8 / waves);
     const int64_t max_tiles = cdiv(cap, kTileP);
     const int64_t hint_tiles = max_kv_len > 0 ? std::min(max_tiles, cdiv(max_kv_len, kTileP)) : max_tiles;
     if (base_wgs < cus && num_rows * row_tokens * num_q_heads <= INT32_MAX) {
-      const double merges = static_cast<double>(num_rows * row_tokens * num_q_heads);
-      auto cost = [&](int64_t k, int64_t tiles) {  // microseconds
-        const int64_t wgs = base_wgs * k;
-        const double per_wg = static_cast<double>(tiles) + 4.8;
-        double t = wgs <= cus ? per_wg * 1.8 : static_cast<double>(cdiv(wgs, resident)) * per_wg * 2.1;
-        if (k > 1) t += 2.0 + std::max(static_cast<double>(partial_bytes(k)) / 5.0e6, merges * 6.0e-4);
-        return t;
-      };
-      // The best split count for token tiles that all reach `reach` key tiles (1: no split).
-      // at most two rounds of resident workgroups: a split grid whose rows turn out shorter than
-      // the hint (tiles below split_from are not split) pays for its empty workgroups
-      const int64_t grid_most = std::max<int64_t>(1, 2 * resident / base_wgs);
-      auto best_splits = [&](int64_t reach) {
-        const int64_t most = std::min<int64_t>({kMaxCtxSplits, reach / 4, 65535 / num_rows, grid_most});
-        double best = 0.8 * cost(1, reach);
-        int64_t k_best = 1;
-        for (int64_t k = 2; k <= most; ++k) {
-          const int64_t tiles = cdiv(reach, k);
-          if (cdiv(reach, tiles) != k) continue;  // the same split as a smaller count
-          if (partial_bytes(k) > workspace_bytes) break;
-          if (const double c = cost(k, tiles); c < best) {
-            best = c;
-            k_best = k;
-          }
-        }
-        return k_best;
-      };
-      kv_splits = best_splits(hint_tiles);
-      if (kv_splits > 1) {
-        // The shortest reach (in powers of two) worth splitting: tiles of rows shorter than the
-        // hint (a graph's table far wider than its rows) are computed whole when splitting them
-        // would cost more than it saves.
-        split_from = hint_tiles;
-        for (int64_t reach = 4; reach < hint_tiles; reach *= 2)
-          if (best_splits(reach) > 1) {
-            split_from = reach;
-            break;
-          }
+      SplitModel m{};
+      m.base = base_wgs;
+      m.cus = cus;
+      m.resident = resident;
+      m.merges = static_cast<double>(num_rows * row_tokens * num_q_heads);
+      m.partial_per_split = context_partial_bytes(num_rows, row_tokens, num_q_heads, head_dim, 1);
+      m.capacity = workspace_bytes;
+      m.max_splits = 65535 / num_rows;
+      kv_splits = best_splits(m, hint_tiles);
+      if (kv_splits > 1) split_from = split_from_reach(m, hint_tiles);
+    } else if (base_wgs >= cus && num_rows > 1 && num_rows <= kPlanMaxRows && units_bound <= kPlanMaxUnits &&
+               row_tokens <= kPlanMaxTokens && gx <= 32767 && units_bound * tokens_per_wg * num_q_heads <= INT32_MAX) {
+      plan = plan_layout(units_bound, gx, resident);
+      if (workspace_bytes > plan.partial_off) {
+        plan_entries = (workspace_bytes - plan.partial_off) / entry_bytes;
+        SplitModel m{};
+        m.base = gx;
+        m.cus = cus;
+        m.resident = resident;
+        m.merges = static_cast<double>(tokens_per_wg * num_q_heads);
+        m.partial_per_split = gx * tokens_per_wg * heads_per_wg * entry_bytes;
+        m.capacity = plan_entries * entry_bytes;
+        m.max_splits = kMaxCtxSplits;
+        planned = best_splits(m, hint_tiles) > 1;
       }
     }
   }
@@ -791,7 +1206,6 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   a.split_from = static_cast<int>(split_from);
   a.part_o = static_cast<float*>(workspace);
   a.part_ml = kv_splits > 1 ? a.part_o + num_rows * row_tokens * num_q_heads * kv_splits * head_dim : nullptr;
-  const dim3 grid(static_cast<uint32_t>(gx), static_cast<uint32_t>(gy), static_cast<uint32_t>(num_rows * kv_splits));
   // Page mode: a tile within one page, a thread-row step within one or two pages, or per lane.
   const int64_t pos_step = 64 * waves / (head_dim / 8);
   const int mode = page_size >= kTileP     ? kPagesTile
@@ -799,8 +1213,52 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
                    : 2 * page_size >= pos_step ? kPagesStep
                                                : kPagesLane;
   const dim3 block(static_cast<uint32_t>(64 * waves));
-  if (kv_splits > 1) launch_context<true>(head_dim, waves, mode, grid, block, stream, a);
-  else launch_context<false>(head_dim, waves, mode, grid, block, stream, a);
+  if (planned) {
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    PlanArgs pa{};
+    pa.cu_seqlens_q = cu_seqlens_q;
+    pa.seq_lens = seq_lens;
+    pa.rows = static_cast<int>(num_rows);
+    pa.gy = static_cast<int>(gy);
+    pa.tokens_per_wg = static_cast<int>(tokens_per_wg);
+    pa.heads_per_wg = heads_per_wg;
+    pa.head_blocks = static_cast<int>(gx);
+    pa.hq = static_cast<int>(num_q_heads);
+    pa.head_dim = static_cast<int>(head_dim);
+    pa.cap = cap;
+    pa.cus = cus;
+    pa.resident = resident;
+    pa.item_cap = plan.item_cap;
+    pa.entry_cap = plan_entries;
+    pa.hdr = reinterpret_cast<int*>(ws);
+    pa.items = reinterpret_cast<i32x4*>(ws + 256);
+    pa.units = reinterpret_cast<i32x4*>(ws + 256 + 32 * plan.item_cap);
+    pa.err = err;
+    a.plan_hdr = pa.hdr;
+    a.plan_items = pa.items;
+    a.plan_units = pa.units;
+    a.plan_rows = pa.rows;
+    a.plan_gy = pa.gy;
+    a.part_o = reinterpret_cast<float*>(ws + plan.partial_off);
+    a.part_ml = a.part_o + plan_entries * head_dim;
+    hipLaunchKernelGGL(context_plan, dim3(1), dim3(kPlanThreads), 0, stream, pa);
+    if (const int st = launch_status(); st != MAS_OK) return st;
+    launch_context<kWorkPlan>(head_dim, waves, mode, dim3(static_cast<uint32_t>(plan.item_cap)), block, stream, a);
+    if (const int st = launch_status(); st != MAS_OK) return st;
+    // each wavefront takes (token, head) pairs of the split units in turn; 16 per CU
+    const int64_t pairs = units_bound * tokens_per_wg * num_q_heads;
+    const dim3 merge_grid(
+        static_cast<uint32_t>(std::min<int64_t>(cdiv(pairs, kMergeWaves), 16 * static_cast<int64_t>(cus) / kMergeWaves)));
+    const dim3 merge_block(64 * kMergeWaves);
+    if (head_dim == 64)
+      hipLaunchKernelGGL(context_combine_plan<64>, merge_grid, merge_block, 0, stream, a, static_cast<int>(tokens_per_wg));
+    else
+      hipLaunchKernelGGL(context_combine_plan<128>, merge_grid, merge_block, 0, stream, a, static_cast<int>(tokens_per_wg));
+    return launch_status();
+  }
+  const dim3 grid(static_cast<uint32_t>(gx), static_cast<uint32_t>(gy), static_cast<uint32_t>(num_rows * kv_splits));
+  if (kv_splits > 1) launch_context<kWorkSplit>(head_dim, waves, mode, grid, block, stream, a);
+  else launch_context<kWorkGrid>(head_dim, waves, mode, grid, block, stream, a);
   if (const int st = launch_status(); st != MAS_OK || kv_splits == 1) return st;
   const int64_t merges = num_rows * row_tokens * num_q_heads;  // <= INT32_MAX when split
   if (head_dim == 64)

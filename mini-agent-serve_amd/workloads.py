@@ -285,6 +285,14 @@ class ContextShape:
     kv_heads: int
     head_dim: int
     page_size: int
+    # The layout of the reference's captured graphs (model_runner.py:155-221) when graph_rows > 0:
+    # graph_rows prompt rows, the real ones first, then one padding row holding the padding tokens
+    # (the step's token count rounded up to 64; their kv_len = their count, every block-table entry
+    # the sink page) and empty rows (seq_len 1); max_q_len = the step's tokens, padding included
+    # (devstral2.py:295), and the block table reach positions wide (the graphs' max_blocks), passed
+    # as max_kv_len (devstral2.py:296).
+    graph_rows: int = 0
+    reach: int = 0
 
 
 CONTEXT_SHAPES: dict[str, ContextShape] = {s.name: s for s in [
@@ -299,6 +307,12 @@ CONTEXT_SHAPES: dict[str, ContextShape] = {s.name: s for s in [
     ContextShape("context_attn_1x128_after4096_24b", 1, 128, 4096, 32, 8, 128, 16),
     ContextShape("context_attn_4x256_after8192_24b", 4, 256, 8192, 32, 8, 128, 16),
     ContextShape("context_attn_1x128_after4096_123b", 1, 128, 4096, 96, 8, 128, 16),
+    # the same kind of turn inside the reference's graphs (17 prompt rows, 128 tokens, an 8192-position
+    # table: its engine's defaults, serving_engine.py:23-27): split-KV decided on the device
+    ContextShape("context_attn_graph_1x100_after4000_24b", 1, 100, 4000, 32, 8, 128, 16, graph_rows=17, reach=8192),
+    ContextShape("context_attn_graph_1x100_after4000_123b", 1, 100, 4000, 96, 8, 128, 16, graph_rows=17,
+                 reach=8192),
+    ContextShape("context_attn_graph_3x100_after2000_24b", 3, 100, 2000, 32, 8, 128, 16, graph_rows=17, reach=8192),
 ]}
 
 
@@ -308,9 +322,11 @@ class ContextInputs:
     q: torch.Tensor             # [rows * q_len, Hq, D]
     k_cache: torch.Tensor
     v_cache: torch.Tensor
-    block_tables: torch.Tensor  # [rows, pages per row] int32
+    block_tables: torch.Tensor  # [rows, pages per row] int32 (the real rows first)
     seq_lens: torch.Tensor      # [rows] int32 (kv_len)
     cu_seqlens_q: torch.Tensor  # [rows + 1] int32
+    max_q_len: int
+    max_kv_len: int
 
 
 def make_context_inputs(shape: ContextShape | str, device="cpu", seed: int = 0) -> ContextInputs:
@@ -319,23 +335,40 @@ def make_context_inputs(shape: ContextShape | str, device="cpu", seed: int = 0) 
     device = torch.device(device)
     kv_len = shape.cached + shape.q_len
     width = -(-kv_len // shape.page_size)
-    pages = shape.rows * width + 1
+    pages = shape.rows * width + 1   # the last page: the graphs' sink for padding rows
     g = torch.Generator().manual_seed(seed)
-    tables = torch.randperm(pages, generator=g)[: shape.rows * width].reshape(shape.rows, width).to(torch.int32)
+    perm = torch.randperm(pages - 1 if shape.graph_rows else pages, generator=g)
+    real = perm[: shape.rows * width].reshape(shape.rows, width).to(torch.int32)
+    lens = [kv_len] * shape.rows
+    cu = [r * shape.q_len for r in range(shape.rows + 1)]
+    tokens, max_q, max_kv = shape.rows * shape.q_len, shape.q_len, kv_len
+    tables = real
+    if shape.graph_rows:
+        total = -(-tokens // 64) * 64
+        pad = total - tokens
+        tables = torch.full((shape.graph_rows, max(shape.reach // shape.page_size, width)), pages - 1,
+                            dtype=torch.int32)
+        tables[: shape.rows, :width] = real
+        tables[: shape.rows, width:] = -1   # past seq_lens: never read
+        lens += [max(pad, 1)] + [1] * (shape.graph_rows - shape.rows - 1)
+        cu += [total] * (shape.graph_rows - shape.rows)
+        tokens, max_q, max_kv = total, total, tables.shape[1] * shape.page_size
     dg = torch.Generator(device=device).manual_seed(seed)
     kv = (pages, shape.page_size, shape.kv_heads, shape.head_dim)
     return ContextInputs(
         shape=shape,
-        q=torch.randn(shape.rows * shape.q_len, shape.q_heads, shape.head_dim, generator=dg, device=device).bfloat16(),
+        q=torch.randn(tokens, shape.q_heads, shape.head_dim, generator=dg, device=device).bfloat16(),
         k_cache=torch.randn(kv, generator=dg, device=device).bfloat16(),
         v_cache=torch.randn(kv, generator=dg, device=device).bfloat16(),
         block_tables=tables.to(device),
-        seq_lens=torch.full((shape.rows,), kv_len, dtype=torch.int32, device=device),
-        cu_seqlens_q=(torch.arange(shape.rows + 1, dtype=torch.int32) * shape.q_len).to(device))
+        seq_lens=torch.tensor(lens, dtype=torch.int32, device=device),
+        cu_seqlens_q=torch.tensor(cu, dtype=torch.int32, device=device),
+        max_q_len=max_q, max_kv_len=max_kv)
 
 
 def context_flops(shape: ContextShape) -> int:
     """Algorithmic flops of causal attention: each (query token, head) scores and weighs the
-    positions up to its own, 2 * D flops each for Q.K and for P.V."""
+    positions up to its own, 2 * D flops each for Q.K and for P.V (the real rows only, not a graph's
+    padding)."""
     positions = sum(shape.cached + i + 1 for i in range(shape.q_len))
     return shape.rows * positions * shape.q_heads * shape.head_dim * 4
