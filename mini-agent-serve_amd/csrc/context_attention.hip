@@ -821,64 +821,77 @@ __device__ int plan_max(int x, int* slots) {
   return m;
 }
 
-// The split estimate of SplitModel in fp32 for the planner, one split count per lane.
+// The planner's estimate (SplitModel's terms, with the real lengths): split k ways, the longest
+// unit is cut into ranges of per = max(4, ceil(longest / k)) key tiles and so is every unit longer
+// than per; the rest stay whole. Its time is that of a workgroup of per tiles, (per + 4.8) x 1.8 us
+// with at most one workgroup per CU, else x 2.1 us per round of resident workgroups, plus, split,
+// 5 us (the merge's launch and the planner's item writes, 3 us more than an unsplit plan's on
+// MI355X) and the merge: the partials' bytes at 5 TB/s or 0.9 ns per (token, head) pair of the
+// split units, whichever is longer (the planned merge takes its pairs in turn on a fixed grid:
+// 12,288-13,312 pairs in 11-13 us, against 0.6 ns per pair for the grid launch's merge, which has a
+// wavefront per pair).
 struct PlanModel {
-  int base, cus, resident;
-  float merges;  // (token, head) pairs the merge visits
-  float pps_us;  // microseconds to move one split's partials at 5 TB/s
-  int most_k;    // splits whose partials the workspace holds
+  int units, head_blocks, longest;
+  int cus, resident;
+  int item_cap;           // workgroups of the main grid
+  int64_t entry_cap;      // partial entries the workspace holds
+  int entries_per_unit;   // partial entries of a split unit per split (head blocks x tokens x heads)
+  float pair_us;          // merge microseconds per split unit (its (token, head) pairs)
+  float entry_us;         // microseconds per partial entry moved at 5 TB/s
 };
 
-__device__ float plan_cost(const PlanModel& m, int k, int tiles) {
-  const int wgs = m.base * k;
-  const float per_wg = static_cast<float>(tiles) + 4.8f;
-  float t = wgs <= m.cus ? per_wg * 1.8f : static_cast<float>((wgs + m.resident - 1) / m.resident) * per_wg * 2.1f;
-  if (k > 1) t += 2.0f + fmaxf(m.pps_us * static_cast<float>(k), m.merges * 6.0e-4f);
-  return t;
+__device__ float plan_time(const PlanModel& m, int wgs, int per) {
+  const float per_wg = static_cast<float>(per) + 4.8f;
+  return wgs <= m.cus ? per_wg * 1.8f : static_cast<float>((wgs + m.resident - 1) / m.resident) * per_wg * 2.1f;
 }
 
-// The estimate for k splits of a reach (infinite where best_splits does not weigh k: past its
-// limits, or the same split as a smaller count).
-__device__ float plan_split_cost(const PlanModel& m, int reach, int k) {
-  const int grid_most = max(1, 2 * m.resident / m.base);
-  const int most = min(min(reach / 4, kMaxCtxSplits), min(grid_most, m.most_k));
-  if (k > most) return __builtin_huge_valf();
-  const int tiles = (reach + k - 1) / k;
-  return (reach + tiles - 1) / tiles == k ? plan_cost(m, k, tiles) : __builtin_huge_valf();
+// The split length for k splits, or 0 where k is not weighed (the same split as a smaller count,
+// or more splits than kMaxCtxSplits).
+__device__ int plan_per(const PlanModel& m, int k) {
+  if (k > kMaxCtxSplits) return 0;
+  const int tiles = (m.longest + k - 1) / k;
+  if ((m.longest + tiles - 1) / tiles != k) return 0;
+  return max(4, tiles);
 }
 
-// Whether k splits of the reach beat one kernel by 20% (best_splits > 1 iff some k does).
-__device__ bool plan_splits_pay(const PlanModel& m, int reach, int k) {
-  return plan_split_cost(m, reach, k) < 0.8f * plan_cost(m, 1, reach);
+// The estimate for k > 1 splits (infinite if the grid or the workspace would not hold them); the
+// unit lengths are read from LDS, the same address in every lane.
+__device__ float plan_split_cost(const PlanModel& m, const int* u_nt, int k) {
+  const int per = plan_per(m, k);
+  if (per == 0 || per >= m.longest) return __builtin_huge_valf();
+  int split = 0;  // units longer than per
+  for (int u = 0; u < m.units; ++u) split += u_nt[u] > per ? 1 : 0;
+  const int64_t wgs = static_cast<int64_t>(m.units + split * (k - 1)) * m.head_blocks;  // at most
+  const int64_t entries = static_cast<int64_t>(split) * m.entries_per_unit * k;
+  if (wgs > m.item_cap || entries > m.entry_cap) return __builtin_huge_valf();
+  return plan_time(m, static_cast<int>(wgs), per) + 5.0f +
+         fmaxf(static_cast<float>(entries) * m.entry_us, static_cast<float>(split) * m.pair_us);
 }
 
-// best_splits for a wavefront-uniform reach, lane l weighing l + 2 splits: the smallest count of
-// least cost, if it beats one kernel by 20% (else 1).
-__device__ int plan_best_splits(const PlanModel& m, int reach, int lane) {
-  const float c = plan_split_cost(m, reach, lane + 2);
+// The split count, lane l weighing l + 2 splits: the smallest count of least estimate if it beats
+// one kernel by 20%, else 1.
+__device__ int plan_best_splits(const PlanModel& m, const int* u_nt, int lane) {
+  const float c = plan_split_cost(m, u_nt, lane + 2);
   float low = c;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) low = fminf(low, __shfl_xor(low, d));
-  if (!(low < 0.8f * plan_cost(m, 1, reach))) return 1;
+  if (!(low < 0.8f * plan_time(m, m.units * m.head_blocks, m.longest))) return 1;
   return __builtin_ctzll(__ballot(c == low)) + 2;
 }
 
 // Lays out a planned launch from the real lengths (one workgroup). Units are a row's token tiles,
-// longest reach first; the split count comes from the same estimate the host uses for its grids
-// (SplitModel), evaluated for the units there are and the longest reach among them; a unit whose
-// tile reaches at least split_from key tiles is split into its non-empty key ranges
-// (split_tiles), each range an item per head block, and its partials get a slot per head block;
-// every other unit is one item per head block that writes its output. Rows' length errors are
-// reported here, as the grid launch reports them (a row with query tokens: kv_len below q_len or
-// past the block table, or more tokens than the grid's token tiles cover, which are left
-// unwritten).
+// longest reach first. The split count comes from PlanModel's estimate; a unit longer than the
+// split length is cut into ranges of that length, each range an item per head block, and its
+// partials get a slot per head block; every other unit is one item per head block that writes its
+// output. Rows' length errors are reported here, as the grid launch reports them (a row with query
+// tokens: kv_len below q_len or past the block table, or more tokens than the grid's token tiles
+// cover, which are left unwritten).
 __global__ __launch_bounds__(kPlanThreads) void context_plan(PlanArgs p) {
   __shared__ int r_q0[kPlanMaxRows], r_qlen[kPlanMaxRows], r_kv[kPlanMaxRows], r_unit[kPlanMaxRows + 1];
   __shared__ int u_row[kPlanMaxUnits], u_tile[kPlanMaxUnits], u_nt[kPlanMaxUnits];
   __shared__ int u_item[kPlanMaxUnits + 1], u_slot[kPlanMaxUnits + 1];
   __shared__ int slots[kPlanThreads / 64];
   __shared__ int params[1];
-  __shared__ int found[kPlanThreads / 32];
   const int tid = threadIdx.x;
 
   // rows: lengths and token tiles
@@ -918,54 +931,35 @@ __global__ __launch_bounds__(kPlanThreads) void context_plan(PlanArgs p) {
   }
   longest = plan_max(longest, slots);
 
-  // the split count at the longest reach (wavefront 0, a split count per lane), then the shortest
-  // reach worth splitting (all threads: 8 reaches x 32 split counts per pass)
-  PlanModel m{};
-  const int base = units * p.head_blocks;
-  const bool may_split = units > 0 && base < p.cus;
-  if (may_split) {
-    const float entry_bytes = (p.head_dim + 2) * 4.f;
-    m.base = base;
-    m.cus = static_cast<int>(p.cus);
-    m.resident = static_cast<int>(p.resident);
-    m.merges = static_cast<float>(units) * p.tokens_per_wg * p.hq;
-    m.pps_us = static_cast<float>(base) * p.tokens_per_wg * p.heads_per_wg * entry_bytes / 5.0e6f;
-    m.most_k = static_cast<int>(min(static_cast<int64_t>(kMaxCtxSplits),
-                                    p.entry_cap / (static_cast<int64_t>(base) * p.tokens_per_wg * p.heads_per_wg)));
-  }
+  // the split count (wavefront 0, a split count per lane) and its split length
   if (tid < 64) {
-    const int best = may_split ? plan_best_splits(m, longest, tid) : 1;
+    int best = 1;
+    if (units > 0 && units * p.head_blocks < p.cus) {
+      PlanModel m{};
+      m.units = units;
+      m.head_blocks = p.head_blocks;
+      m.longest = longest;
+      m.cus = static_cast<int>(p.cus);
+      m.resident = static_cast<int>(p.resident);
+      m.item_cap = static_cast<int>(p.item_cap);
+      m.entry_cap = p.entry_cap;
+      m.entries_per_unit = p.head_blocks * p.tokens_per_wg * p.heads_per_wg;
+      m.pair_us = static_cast<float>(p.tokens_per_wg) * p.hq * 9.0e-4f;
+      m.entry_us = (p.head_dim + 2) * 4.f / 5.0e6f;
+      best = plan_best_splits(m, u_nt, tid);
+    }
     if (tid == 0) params[0] = best;
   }
   __syncthreads();
   int splits = params[0];
-  int from = INT32_MAX;
-  if (splits > 1) {
-    from = longest;
-    for (int pass = 0; pass < 3 && from == longest; ++pass) {  // the same trip count in every thread
-      const int ri = (tid >> 5) + 8 * pass;
-      const int reach = ri < 24 ? 4 << ri : INT32_MAX;
-      const bool ok = reach < longest && plan_splits_pay(m, reach, (tid & 31) + 2);
-      const uint64_t hits = __ballot(ok);
-      if ((tid & 31) == 0) found[tid >> 5] = ((tid & 32) ? hits >> 32 : hits & 0xffffffffu) != 0;
-      __syncthreads();
-#pragma unroll
-      for (int i = 7; i >= 0; --i)
-        if (found[i]) from = 4 << (i + 8 * pass);
-      __syncthreads();
-    }
-  }
+  const int per = splits > 1 ? max(4, (longest + splits - 1) / splits) : 0;  // units longer than per split
 
   // items and partial slots per unit; no split if the grid or the workspace would not hold them
   int items = 0, split_units = 0;
   if (splits > 1) {
     for (int u = tid; u < units; u += kPlanThreads) {
       const int nt = u_nt[u];
-      int used = 1;
-      if (nt >= from) {
-        const int per = split_tiles(nt, splits);
-        used = (nt + per - 1) / per;
-      }
+      const int used = nt > per ? (nt + per - 1) / per : 1;  // <= splits
       u_item[u] = used * p.head_blocks;
       u_slot[u] = used > 1 ? 1 : 0;
     }
@@ -989,12 +983,12 @@ __global__ __launch_bounds__(kPlanThreads) void context_plan(PlanArgs p) {
       const int u = j / p.head_blocks, block = j - u * p.head_blocks;
       const int used = (u_item[u + 1] - u_item[u]) / p.head_blocks;
       const int r = u_row[u], nt = u_nt[u];
-      const int per = used > 1 ? split_tiles(nt, splits) : nt;
+      const int len = used > 1 ? per : nt;
       const int slot = used > 1 ? u_slot[u] * p.head_blocks + block : -1;
       for (int range = 0; range < used; ++range) {
-        const int i = u_item[u] + range * p.head_blocks + block, first = range * per;
+        const int i = u_item[u] + range * p.head_blocks + block, first = range * len;
         p.items[2 * i] = i32x4{r_q0[r], r_qlen[r], r_kv[r], r | (range << 16) | (splits << 24)};
-        p.items[2 * i + 1] = i32x4{u_tile[u] | (block << 16), first, min(nt, first + per), slot};
+        p.items[2 * i + 1] = i32x4{u_tile[u] | (block << 16), first, min(nt, first + len), slot};
       }
     }
   }
