@@ -273,7 +273,13 @@ int mas_paged_decode_attention_bf16(void* out, int64_t out_stride, int64_t out_h
  * * 4 bytes, tile = 32 tokens x (workgroup wavefronts / heads per workgroup) - and a second kernel
  * merges them; with less workspace, fewer splits or none. Each token tile divides its own key
  * range among the splits; max_kv_len (<= 0: none; else the block table's reach) is a hint that
- * only sizes the choice of the split count.
+ * only sizes the choice of the split count. A grid of several rows and at most 1024 tokens per
+ * row that has a workgroup per CU or more (a captured graph's padded prompt rows, max_q_len the
+ * step's tokens) is planned on the device when the workspace holds the plan: a first kernel reads
+ * cu_seqlens_q / seq_lens, picks the split count for the real lengths and writes the work items
+ * to the workspace (its counts, 32 bytes per workgroup of the grid, 32 per (row, token tile), then
+ * the partials), and the merge runs over the split tiles only. Calls sharing a workspace must not
+ * overlap.
  * Replaces flashinfer.prefill.trtllm_batch_context_with_kv_cache at
  * miniagentserve/models/devstral2/devstral2.py:198-213 (kv_layout "NHD", no sliding window).
  */
