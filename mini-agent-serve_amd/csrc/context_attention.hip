@@ -828,7 +828,7 @@ __device__ int plan_max(int x, int* slots) {
 // 5 us (the merge's launch and the planner's item writes, 3 us more than an unsplit plan's on
 // MI355X) and the merge: the partials' bytes at 5 TB/s or 0.9 ns per (token, head) pair of the
 // split units, whichever is longer (the planned merge takes its pairs in turn on a fixed grid:
-// 12,288-13,312 pairs in 11-13 us, against 0.6 ns per pair for the grid launch's merge, which has a
+// 12,288 pairs in 9.6-11 us, against 0.6 ns per pair for the grid launch's merge, which has a
 // wavefront per pair).
 struct PlanModel {
   int units, head_blocks, longest;
@@ -1239,10 +1239,11 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
     if (const int st = launch_status(); st != MAS_OK) return st;
     launch_context<kWorkPlan>(head_dim, waves, mode, dim3(static_cast<uint32_t>(plan.item_cap)), block, stream, a);
     if (const int st = launch_status(); st != MAS_OK) return st;
-    // each wavefront takes (token, head) pairs of the split units in turn; 16 per CU
+    // each wavefront takes (token, head) pairs of the split units in turn; 24 per CU (6 per SIMD,
+    // as many as the merge's registers allow: 12,288 pairs merged in 9.6 us against 11.1 with 16)
     const int64_t pairs = units_bound * tokens_per_wg * num_q_heads;
     const dim3 merge_grid(
-        static_cast<uint32_t>(std::min<int64_t>(cdiv(pairs, kMergeWaves), 16 * static_cast<int64_t>(cus) / kMergeWaves)));
+        static_cast<uint32_t>(std::min<int64_t>(cdiv(pairs, kMergeWaves), 24 * static_cast<int64_t>(cus) / kMergeWaves)));
     const dim3 merge_block(64 * kMergeWaves);
     if (head_dim == 64)
       hipLaunchKernelGGL(context_combine_plan<64>, merge_grid, merge_block, 0, stream, a, static_cast<int>(tokens_per_wg));
