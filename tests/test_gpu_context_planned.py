@@ -255,3 +255,61 @@ def test_planned_context_attention_graph_replays_new_lengths(mas, dev):
                 want = ops.paged_context_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(),
                                                    cu.numpy(), dim ** -0.5)
                 _check(bits(out), want, min_exact=0.0)
+
+
+def test_planned_context_attention_compiled_and_captured(mas, dev):
+    """The way the reference runs its graph steps (model_runner.py:98-119): the call compiled with
+    torch.compile(dynamic=True, fullgraph=True), max_q_len taken from the query's shape
+    (devstral2.py:295), warmed up three times on a side stream and captured in a CUDA graph; replays
+    over steps of different prompts equal the eager call bit for bit, and the long-prefix step splits
+    (its result differs from the one-kernel launch's)."""
+    hq, hk, dim, ps, reach, t = 32, 8, 128, 16, 8192, 128
+    steps = [[(100, 4000)], [(60, 2000), (40, 10)], [(128, 0)]]
+    cases = [_graph_case(110 + i, p, t - sum(n for n, _ in p), hq, hk, dim, ps, reach=reach) for i, p in enumerate(steps)]
+    pages = max(c[1].shape[0] for c in cases)
+    kc = torch.randn(pages, ps, hk, dim, generator=torch.Generator().manual_seed(7)).bfloat16().to(dev)
+    vc = torch.randn(pages, ps, hk, dim, generator=torch.Generator().manual_seed(8)).bfloat16().to(dev)
+    qb = torch.zeros(t, hq, dim, dtype=torch.bfloat16, device=dev)
+    tb = torch.zeros(PREFILL_ROWS, reach // ps, dtype=torch.int32, device=dev)
+    sb = torch.zeros(PREFILL_ROWS, dtype=torch.int32, device=dev)
+    cb = torch.zeros(PREFILL_ROWS + 1, dtype=torch.int32, device=dev)
+    ws = _workspace(dev, WS)
+    att = mas.attention
+
+    def f(q, tables, seq, cu):
+        return att.trtllm_batch_context_with_kv_cache(q, (kc, vc), ws, tables, seq, q.shape[0], tables.shape[1] * ps,
+                                                      dim ** -0.5, 1.0, cu.shape[0] - 1, cu)
+
+    def load(case):
+        q, _, _, tables, seq, cu, _ = case
+        tables = tables.clone()
+        tables[tables == case[1].shape[0] - 1] = pages - 1
+        qb.copy_(q)
+        tb.copy_(tables)
+        sb.copy_(seq)
+        cb.copy_(cu)
+
+    compiled = torch.compile(f, dynamic=True, fullgraph=True)
+    load(cases[0])
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            compiled(qb, tb, sb, cb)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = compiled(qb, tb, sb, cb)
+    for i, case in enumerate(cases):
+        load(case)
+        want = f(qb, tb, sb, cb)
+        torch.cuda.synchronize()
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"step {i}"
+        if i == 0:
+            one_kernel = att.trtllm_batch_context_with_kv_cache(qb, (kc, vc), _workspace(dev, 16), tb, sb, t, reach,
+                                                                dim ** -0.5, 1.0, PREFILL_ROWS, cb)
+            assert not torch.equal(out, one_kernel)
