@@ -845,6 +845,13 @@ __device__ float plan_time(const PlanModel& m, int wgs, int per) {
   return wgs <= m.cus ? per_wg * 1.8f : static_cast<float>((wgs + m.resident - 1) / m.resident) * per_wg * 2.1f;
 }
 
+// Whether no split can pay for units reaching at most `longest` key tiles: the unsplit estimate,
+// at most one workgroup per CU (else no split is weighed), against the least any split costs (a
+// split length of 4 tiles in one round, plus the fixed 5 us).
+__device__ bool plan_never_splits(int longest) {
+  return 0.8f * ((static_cast<float>(longest) + 4.8f) * 1.8f) <= (4.f + 4.8f) * 1.8f + 5.0f;
+}
+
 // The split length for k splits, or 0 where k is not weighed (the same split as a smaller count,
 // or more splits than kMaxCtxSplits).
 __device__ int plan_per(const PlanModel& m, int k) {
@@ -896,6 +903,7 @@ __global__ __launch_bounds__(kPlanThreads) void context_plan(PlanArgs p) {
 
   // rows: lengths and token tiles
   bool bad = false;
+  int reach_bound = 0;  // key tiles of the longest row: no unit reaches more
   for (int r = tid; r < p.rows; r += kPlanThreads) {
     const int q0 = p.cu_seqlens_q[r];
     const int64_t q_len = static_cast<int64_t>(p.cu_seqlens_q[r + 1]) - q0;
@@ -910,8 +918,18 @@ __global__ __launch_bounds__(kPlanThreads) void context_plan(PlanArgs p) {
     r_qlen[r] = q_len > 0 ? static_cast<int>(q_len) : 0;
     r_kv[r] = static_cast<int>(raw < 0 ? 0 : (raw > p.cap ? p.cap : raw));
     r_unit[r] = tiles;
+    if (tiles > 0) reach_bound = max(reach_bound, (r_kv[r] + kTileP - 1) / kTileP);
   }
   if (__syncthreads_or(bad) && tid == 0) report(p.err, MAS_ERRBIT_POSITION);
+  // short rows: an unsplit plan without laying out the units
+  if (plan_never_splits(plan_max(reach_bound, slots))) {
+    if (tid == 0) {
+      p.hdr[0] = p.rows * p.gy * p.head_blocks;
+      p.hdr[1] = 0;
+      p.hdr[2] = 1;
+    }
+    return;
+  }
   const int units = plan_scan(r_unit, p.rows, slots);  // <= rows * gy <= kPlanMaxUnits (host-checked)
 
   // units: each row's token tiles, the last (longest reach) first
