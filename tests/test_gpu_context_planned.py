@@ -313,3 +313,26 @@ def test_planned_context_attention_compiled_and_captured(mas, dev):
             one_kernel = att.trtllm_batch_context_with_kv_cache(qb, (kc, vc), _workspace(dev, 16), tb, sb, t, reach,
                                                                 dim ** -0.5, 1.0, PREFILL_ROWS, cb)
             assert not torch.equal(out, one_kernel)
+
+
+@pytest.mark.parametrize("rows,prompts,hq,hk,dim", [
+    (300, [(40, 3000), (5, 900), (2, 0)], 32, 8, 128),   # 300 prompt rows (the planner's row loop wraps)
+    (17, [(70, 2600), (9, 40)], 12, 2, 128),               # 6 query heads per kv head: a half-empty head block
+    (17, [(90, 3000), (150, 10)], 16, 2, 64),              # head_dim 64, 8 query heads per kv head (8 wavefronts)
+])
+def test_planned_context_attention_more_shapes(mas, dev, rows, prompts, hq, hk, dim):
+    """Planned launches beyond the graph-step defaults: a step of hundreds of prompt rows, a head
+    group that leaves part of a workgroup's heads empty, head_dim 64 with eight wavefronts; split
+    (the result differs from the one-kernel launch's) and within the oracle's tolerance."""
+    t = -(-sum(n for n, _ in prompts) // 64) * 64
+    q, kc, vc, tables, seq, cu, max_q = _graph_case(rows + hq + dim, prompts, t - sum(n for n, _ in prompts), hq, hk,
+                                                    dim, 16, rows=rows)
+    reach = tables.shape[1] * 16
+    scale = dim ** -0.5
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = _call(mas, dev, q, kc, vc, tables, seq, cu, max_q, reach, scale, flags=flags)
+    assert int(flags.item()) == 0
+    want = ops.paged_context_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), cu.numpy(), scale)
+    one_kernel = _call(mas, dev, q, kc, vc, tables, seq, cu, max_q, reach, scale, ws_bytes=16)
+    assert not torch.equal(out, one_kernel)
+    _check(bits(out), want, min_exact=0.5)
