@@ -336,3 +336,36 @@ def test_planned_context_attention_more_shapes(mas, dev, rows, prompts, hq, hk, 
     one_kernel = _call(mas, dev, q, kc, vc, tables, seq, cu, max_q, reach, scale, ws_bytes=16)
     assert not torch.equal(out, one_kernel)
     _check(bits(out), want, min_exact=0.5)
+
+
+def test_planned_context_attention_degenerate_steps(mas, dev):
+    """Planned launches of degenerate steps give what the grid launch gives: a step whose rows have
+    no query tokens writes nothing and flags nothing; a row whose seq_len is 0 gets zeros and the
+    position bit; a row whose cum_seq_lens_q entries decrease (a negative count) is skipped."""
+    hq, hk, dim, ps, t = 32, 8, 128, 16, 128
+    q, kc, vc, tables, seq, cu, _ = _graph_case(131, [(100, 4000)], 28, hq, hk, dim, ps)
+    reach = tables.shape[1] * ps
+    # no query tokens in any row
+    empty_cu = torch.zeros_like(cu)
+    out = torch.full(q.shape, 7.0, dtype=torch.bfloat16, device=dev)
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    mas.attention.trtllm_batch_context_with_kv_cache(
+        q.to(dev), (kc.to(dev), vc.to(dev)), _workspace(dev, WS), tables.to(dev), seq.to(dev), t, reach, 0.1, 1.0,
+        PREFILL_ROWS, empty_cu.to(dev), None, out=out, error_flags=flags)
+    assert int(flags.item()) == 0 and torch.all(out == 7.0)
+    # seq_len 0 for the long row; a decreasing entry for the padding row
+    seq_bad = seq.clone()
+    seq_bad[0] = 0
+    cu_bad = cu.clone()
+    cu_bad[2] = 90  # row 1 (padding) now has 90 - 100 < 0 tokens; row 2 starts at 90
+    results = []
+    for ws_bytes in (WS, 16):
+        out = torch.full(q.shape, 7.0, dtype=torch.bfloat16, device=dev)
+        flags = torch.zeros(1, dtype=torch.int32, device=dev)
+        mas.attention.trtllm_batch_context_with_kv_cache(
+            q.to(dev), (kc.to(dev), vc.to(dev)), _workspace(dev, ws_bytes), tables.to(dev), seq_bad.to(dev), t, reach,
+            0.1, 1.0, PREFILL_ROWS, cu_bad.to(dev), None, out=out, error_flags=flags)
+        results.append((int(flags.item()), out))
+    assert results[0][0] == results[1][0] == 2
+    assert torch.equal(results[0][1], results[1][1])
+    assert not results[0][1][:100].any()
