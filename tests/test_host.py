@@ -250,3 +250,24 @@ def test_golden_fixtures_reproduce():
     assert set(stored.files) == set(fresh)
     for key in stored.files:
         assert np.array_equal(stored[key], fresh[key]), key
+
+
+def test_graph_context_workload_layout(mas):
+    """The bench's graph-step context workloads follow the reference runner's layout
+    (model_runner.py:155-221): 17 prompt rows, the real prompts first, then one padding row holding
+    the padding tokens (the step's token count rounded up to 64; its kv_len their count, every
+    block-table entry the sink page) and empty rows (seq_len 1, the sink in column 0); max_q_len the
+    padded token count, max_kv_len the table's reach."""
+    inp = mas.workloads.make_context_inputs("context_attn_graph_3x100_after2000_24b")
+    s = inp.shape
+    cu, seq, tables = inp.cu_seqlens_q.tolist(), inp.seq_lens.tolist(), inp.block_tables
+    assert len(seq) == 17 and len(cu) == 18 and tables.shape == (17, 8192 // 16)
+    assert cu[:4] == [0, 100, 200, 300] and cu[4:] == [320] * 14
+    assert seq[:3] == [2100] * 3 and seq[3] == 20 and seq[4:] == [1] * 13
+    assert (inp.max_q_len, inp.max_kv_len) == (320, 8192) and inp.q.shape == (320, s.q_heads, s.head_dim)
+    sink = inp.k_cache.shape[0] - 1
+    width = -(-2100 // 16)
+    real = tables[:3, :width]
+    assert int(real.min()) >= 0 and int(real.max()) < sink and real.unique().numel() == real.numel()
+    assert torch.all(tables[3] == sink) and torch.all(tables[4:, 0] == sink)
+    assert mas.workloads.context_flops(s) == 3 * sum(2000 + i + 1 for i in range(100)) * 32 * 128 * 4
