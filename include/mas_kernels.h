@@ -273,7 +273,7 @@ int mas_paged_decode_attention_bf16(void* out, int64_t out_stride, int64_t out_h
  * * 4 bytes, tile = 32 tokens x (workgroup wavefronts / heads per workgroup) - and a second kernel
  * merges them; with less workspace, fewer splits or none. Each token tile divides its own key
  * range among the splits; max_kv_len (<= 0: none; else the block table's reach) is a hint that
- * only sizes the choice of the split count. A grid of several rows and at most 1024 tokens per
+ * only sizes the choice of the split count. A grid of 8 or more rows and at most 1024 tokens per
  * row that has a workgroup per CU or more (a captured graph's padded prompt rows, max_q_len the
  * step's tokens) is planned on the device when the workspace holds the plan: a first kernel reads
  * cu_seqlens_q / seq_lens, picks the split count for the real lengths and writes the work items

@@ -51,6 +51,10 @@ constexpr int kPlanThreads = 256;
 constexpr int kPlanMaxRows = 512;
 constexpr int kPlanMaxUnits = 2048;
 constexpr int kPlanMaxTokens = 1024;  // planned launches: the grid's token tiles cover at most this many tokens
+// Planned launches: at least this many rows. The runner's graph steps have 17 prompt rows, nearly
+// all padding; a grid of a few rows that fills the GPU is more likely full than padded (4 rows of
+// 256 new tokens after 8192: planning it cost 5-14 us of 231).
+constexpr int kPlanMinRows = 8;
 
 struct ContextArgs {
   const uint16_t* q;
@@ -1133,9 +1137,9 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   // 44.9 in 2 splits. A grid with a workgroup on every CU gains nothing (4 rows of 256 after
   // 8192: 256 workgroups, 237 us either way) and is not split.
   //
-  // Planned: a grid sized for several rows of up to kPlanMaxTokens query tokens that holds a
-  // workgroup per CU or more may still be mostly empty (a graph captured with padded prompt rows
-  // and the step's whole token count as max_q_len; the rows' real lengths are on the device). When
+  // Planned: a grid sized for kPlanMinRows or more rows of up to kPlanMaxTokens query tokens that
+  // holds a workgroup per CU or more may still be mostly empty (a graph captured with padded prompt
+  // rows and the step's whole token count as max_q_len; the rows' real lengths are on the device). When
   // the smallest grid it could hold (one token tile) would split at the hint's reach, context_plan
   // lays the launch out from the real lengths first: the same estimate on the real grid, one
   // workgroup per item, and a merge over the split tiles only.
@@ -1165,7 +1169,7 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
       m.max_splits = 65535 / num_rows;
       kv_splits = best_splits(m, hint_tiles);
       if (kv_splits > 1) split_from = split_from_reach(m, hint_tiles);
-    } else if (base_wgs >= cus && num_rows > 1 && num_rows <= kPlanMaxRows && units_bound <= kPlanMaxUnits &&
+    } else if (base_wgs >= cus && num_rows >= kPlanMinRows && num_rows <= kPlanMaxRows && units_bound <= kPlanMaxUnits &&
                row_tokens <= kPlanMaxTokens && gx <= 32767 && units_bound * tokens_per_wg * num_q_heads <= INT32_MAX) {
       plan = plan_layout(units_bound, gx, resident);
       if (workspace_bytes > plan.partial_off) {
