@@ -369,3 +369,31 @@ def test_planned_context_attention_degenerate_steps(mas, dev):
     assert results[0][0] == results[1][0] == 2
     assert torch.equal(results[0][1], results[1][1])
     assert not results[0][1][:100].any()
+
+
+def _random_graph_step(seed):
+    """A seeded graph step: 1-5 prompts of 1-120 new tokens after 0-9000 cached positions (the step's
+    tokens rounded up to 64, at most 512, the rest a padding row), group sizes 1-12, head_dim 64 /
+    128, pages of 8-256 slots, a table reach of 16384 positions."""
+    rng = np.random.default_rng(seed)
+    n = int(rng.integers(1, 6))
+    prompts = [(int(rng.integers(1, 121)), int(rng.choice([0, rng.integers(1, 9001)]))) for _ in range(n)]
+    hk = int(rng.choice([2, 8]))
+    group = int(rng.choice([1, 2, 3, 4, 6, 8, 12]))
+    dim = int(rng.choice([64, 128]))
+    ps = int(rng.choice([8, 16, 64, 256]))
+    return prompts, hk * group, hk, dim, ps
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_planned_context_attention_random_steps(mas, dev, seed):
+    prompts, hq, hk, dim, ps = _random_graph_step(seed)
+    used = sum(n for n, _ in prompts)
+    t = -(-used // 64) * 64
+    q, kc, vc, tables, seq, cu, max_q = _graph_case(1000 + seed, prompts, t - used, hq, hk, dim, ps, reach=16384)
+    scale = dim ** -0.5
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = _call(mas, dev, q, kc, vc, tables, seq, cu, max_q, 16384, scale, flags=flags)
+    assert int(flags.item()) == 0
+    want = ops.paged_context_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), cu.numpy(), scale)
+    _check(bits(out), want, min_exact=0.5)
