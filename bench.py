@@ -52,23 +52,109 @@ METRIC = "HBM GB/s & % of peak for layer kernels; µs/layer at 64-token decode"
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 COLD_BYTES = 768 << 20         # working set cycled by the cold protocol (3x the Infinity Cache)
-# HBM bytes per launch of a workload's dominant kernel, from two rocprofv3 counter passes
-# (FETCH_SIZE, then WRITE_SIZE) over `bench.py --pmc-probe`, each calibrated by the same counter on
-# a 256 MiB device copy (fetch factor 1.9997, write factor 1.0000). Re-measure when the kernel changes.
-MEASURED_TRAFFIC = {("decode64_24b", "silu_and_mul"): 12_611_644,
-                    ("prefill8192_24b", "silu_and_mul"): 1_610_374_077,
-                    ("prefill16384_123b", "silu_and_mul"): 2_818_327_781,
-                    ("decode_attn_64x8192_24b", "paged_decode_attention"): 1_115_001_551,
-                    ("decode_attn_64x8192_123b", "paged_decode_attention"): 1_188_456_517}
-# Average per-dispatch duration (µs) of a workload's dominant kernel in a committed rocprofv3 kernel
-# trace (profiles/), beside the bench's own HIP-event figure: the tracer lengthens decode-sized
-# dispatches (~15%); at prefill sizes the two agree within 2%. Re-trace when the kernel changes.
-TRACED_LAUNCH_US = {("decode64_24b", "silu_and_mul"): (4.170, "profiles/layer_decode64_kernel_trace.md"),
-                    ("prefill8192_24b", "silu_and_mul"): (242.570, "profiles/layer_prefill8192_kernel_trace.md"),
-                    ("decode_attn_64x8192_24b", "paged_decode_attention"):
-                        (205.223 + 7.225, "profiles/decode_attention_64x8192_kernel_trace.md"),
-                    ("decode_attn_64x8192_123b", "paged_decode_attention"):
-                        (225.285 + 13.855, "profiles/decode_attention_64x8192_kernel_trace.md")}
+# Figures taken from committed rocprofv3 profiles (profiles/), each with the git blob hashes
+# (`git hash-object <file>`) of the kernel sources it was measured on. `stale_sources` reports a
+# figure whose sources have changed since: the bench line then carries it with "stale": true and
+# takes its roofline from the live HIP-event timing instead.
+KERNEL_SOURCES = {
+    "silu_and_mul": ("csrc/silu_and_mul.hip", "csrc/device.h"),
+    "fused_add_rmsnorm": ("csrc/rmsnorm.hip", "csrc/device.h"),
+    "paged_decode_attention": ("csrc/attention.hip", "csrc/device.h"),
+    "paged_context_attention": ("csrc/context_attention.hip", "csrc/device.h"),
+}
+# Git blob hashes of the kernel sources the profiled figures below were measured on.
+_SILU_SOURCES = {"csrc/silu_and_mul.hip": "bad18b16d062f19d55aead1bf7b7d74e2f49874a",
+                 "csrc/device.h": "4a649fbd27cb9b4a8503ee1b497b4df962d5650e"}
+_NORM_SOURCES = {"csrc/rmsnorm.hip": "089cb088624451ba8a83f3bc292864153fe93b0d",
+                 "csrc/device.h": "4a649fbd27cb9b4a8503ee1b497b4df962d5650e"}
+_DECODE_ATTN_SOURCES = {"csrc/attention.hip": "dda44b23e3291378ddd77bff11e72877ea72ea47",
+                        "csrc/device.h": "4a649fbd27cb9b4a8503ee1b497b4df962d5650e"}
+# HBM bytes per launch of a workload's dominant kernel: two rocprofv3 counter passes (FETCH_SIZE,
+# then WRITE_SIZE) over `bench.py --pmc-probe`, each calibrated by the same counter on a 256 MiB
+# device copy.
+MEASURED_TRAFFIC = {
+    ("decode64_24b", "silu_and_mul"): {
+        "bytes": 12_610_966, "profile": "profiles/silu_and_mul_decode64_hbm_traffic.md", "sources": _SILU_SOURCES},
+    ("rmsnorm_256x5120", "fused_add_rmsnorm"): {
+        "bytes": 10_607_023, "profile": "profiles/rmsnorm_256x5120_kernel_trace.md", "sources": _NORM_SOURCES},
+    ("decode_pass_256x40", "silu_and_mul"): {
+        "bytes": 50_359_743, "profile": "profiles/decode_pass_256x40_kernel_trace.md", "sources": _SILU_SOURCES},
+    ("prefill8192_24b", "silu_and_mul"): {
+        "bytes": 1_610_476_668, "profile": "profiles/silu_and_mul_prefill_hbm_traffic.md", "sources": _SILU_SOURCES},
+    ("decode_attn_64x8192_24b", "paged_decode_attention"): {
+        "bytes": 1_115_129_174, "profile": "profiles/decode_attention_64x8192_kernel_trace.md",
+        "sources": _DECODE_ATTN_SOURCES},
+    ("decode_attn_64x8192_123b", "paged_decode_attention"): {
+        "bytes": 1_188_602_784, "profile": "profiles/decode_attention_64x8192_kernel_trace.md",
+        "sources": _DECODE_ATTN_SOURCES},
+}
+# Average per-dispatch duration (µs) of a workload's dominant kernel in a committed kernel trace of
+# `bench.py --trace-probe ops` (the same graph of back-to-back launches the bench times with HIP
+# events, and nothing else). The roofline's `achieved` and `frac` use this duration.
+TRACED_LAUNCH_US = {
+    ("decode64_24b", "silu_and_mul"): {
+        "us": 4.565, "profile": "profiles/layer_decode64_kernel_trace.md", "sources": _SILU_SOURCES},
+    ("rmsnorm_256x5120", "fused_add_rmsnorm"): {
+        "us": 4.751, "profile": "profiles/rmsnorm_256x5120_kernel_trace.md", "sources": _NORM_SOURCES},
+    ("decode_pass_256x40", "silu_and_mul"): {
+        "us": 9.680, "profile": "profiles/decode_pass_256x40_kernel_trace.md", "sources": _SILU_SOURCES},
+    ("prefill8192_24b", "silu_and_mul"): {
+        "us": 245.177, "profile": "profiles/layer_prefill8192_kernel_trace.md", "sources": _SILU_SOURCES},
+    ("decode_attn_64x8192_24b", "paged_decode_attention"): {     # split + combine
+        "us": 207.618 + 7.071, "profile": "profiles/decode_attention_64x8192_kernel_trace.md",
+        "sources": _DECODE_ATTN_SOURCES},
+    ("decode_attn_64x8192_123b", "paged_decode_attention"): {
+        "us": 226.207 + 13.955, "profile": "profiles/decode_attention_64x8192_kernel_trace.md",
+        "sources": _DECODE_ATTN_SOURCES},
+}
+
+
+def source_blob(rel: str) -> str:
+    """Git blob hash of a package source file (what `git hash-object` prints), computed without git:
+    sha1 of b"blob <size>\\0" followed by the file's bytes."""
+    import hashlib
+    data = (ROOT / "mini-agent-serve_amd" / rel).read_bytes()
+    return hashlib.sha1(b"blob %d\0" % len(data) + data).hexdigest()
+
+
+def stale_sources(entry: dict, kernel: str) -> list[str]:
+    """Sources of ``kernel`` whose blob hash differs from the one ``entry`` (a profiled figure) was
+    measured on; every source when the entry records none."""
+    recorded = entry.get("sources", {})
+    return [rel for rel in KERNEL_SOURCES.get(kernel, ()) if recorded.get(rel) != source_blob(rel)]
+
+
+def roofline_entry(shape_name: str, kernel: str, amount: int, event_us: float, bound: str = "hbm") -> dict:
+    """The `roofline` object of a line: `amount` is the kernel's algorithmic bytes (bound "hbm") or
+    flops (bound "mfma") per launch. Achieved rate and frac come from the committed trace's
+    per-dispatch duration when one exists for this kernel and workload and its sources are unchanged,
+    else from the live HIP-event duration; both figures are carried."""
+    key = (shape_name, kernel)
+    hbm = bound == "hbm"
+    peak, unit, scale = (PEAK_HBM_GBS, "GB/s", 1e3) if hbm else (PEAK_BF16_TFLOPS, "TFLOP/s", 1e6)
+    out = {"bound": bound, "kernel": kernel}
+    traced = TRACED_LAUNCH_US.get(key)
+    traced_stale = stale_sources(traced, kernel) if traced else []
+    use_trace = traced is not None and not traced_stale
+    us = traced["us"] if use_trace else event_us
+    rate = amount / us / scale
+    out.update({"achieved": round(rate, 1), "peak": peak, "unit": unit, "frac": round(rate / peak, 4)})
+    traffic = MEASURED_TRAFFIC.get(key)
+    traffic_stale = stale_sources(traffic, kernel) if traffic else []
+    out["traffic"] = traffic["bytes"] if traffic and not traffic_stale else None
+    out["bytes_per_launch" if hbm else "flops_per_launch"] = amount
+    out["avg_launch_us"] = round(us, 3)
+    out["timing"] = f"rocprofv3 kernel trace, {traced['profile']}" if use_trace else "hip-events (live)"
+    out["event_avg_launch_us"] = round(event_us, 3)
+    out["frac_event"] = round(amount / event_us / scale / peak, 4)
+    if traced is not None:
+        out["traced_avg_launch_us"] = round(traced["us"], 3)
+        out["traced_in"] = traced["profile"]
+        out["trace_stale"] = bool(traced_stale)
+    if traffic is not None:
+        out["traffic_in"] = traffic["profile"]
+        out["traffic_stale"] = bool(traffic_stale)
+    return out
 
 
 def parse_args():
@@ -88,9 +174,19 @@ def parse_args():
                         "on the cold layer sets, then a 256 MiB device copy (the calibration reference for "
                         "FETCH_SIZE / WRITE_SIZE); decode attention workloads: 5 calls, then the copies; context "
                         "attention workloads: 5 calls")
+    p.add_argument("--trace-probe", choices=("ops", "steps"), default=None,
+                   help="short run for rocprofv3 --kernel-trace: 'ops' launches only the per-kernel graphs of "
+                        "back-to-back launches (and memory skeletons) the bench times with HIP events; 'steps' only "
+                        "the stamped step graphs; prints the same run's HIP-event figures")
     p.add_argument("--pmc-op", default=None,
                    help="kernel for --pmc-probe: fused_add_rmsnorm, rope, append_paged_kv_cache, silu_and_mul, "
                         "rope_append, fused_add_rmsnorm_quant or silu_and_mul_quant")
+    p.add_argument("--sets", type=int, default=None,
+                   help="number of layer sets the cold protocol cycles (default: enough that one step's buffers "
+                        "exceed 768 MB)")
+    p.add_argument("--table-per-set", action="store_true",
+                   help="give every cold layer set its own cos/sin table, so RoPE's table rows come from HBM as in a "
+                        "forward pass whose weight traffic evicts the table between layers")
     p.add_argument("--separate-rope-kv", action="store_true",
                    help="run RoPE and the KV append as the reference's two calls (default: one fused kernel, "
                         "same results, one launch fewer per layer); the other form is timed alongside")
@@ -112,8 +208,9 @@ def step_ops(shape, fp8: bool) -> tuple[str, ...]:
     return (norm, "rope", "append_paged_kv_cache", "silu_and_mul_quant" if fp8 else "silu_and_mul", "rope_append")
 
 
-SKELETON_OPS = ("fused_add_rmsnorm", "rope", "append_paged_kv_cache", "silu_and_mul")
+SKELETON_OPS = ("fused_add_rmsnorm", "rope", "append_paged_kv_cache", "silu_and_mul", "rope_append")
 _skeleton_fn = None
+_rope_append_skeleton_fn = None
 _stamp_fn = None
 _clock_khz = 0
 
@@ -121,7 +218,7 @@ _clock_khz = 0
 def load_skeletons(mas) -> None:
     """Loads the benchmark's library (libmas_bench.so, built beside the kernel library): the memory
     skeletons and the wall-clock stamp kernel that brackets timed steps inside a graph."""
-    global _skeleton_fn, _stamp_fn, _clock_khz
+    global _skeleton_fn, _rope_append_skeleton_fn, _stamp_fn, _clock_khz
     path = Path(mas.__file__).resolve().parent / "libmas_bench.so"
     if not path.exists():
         raise RuntimeError(f"{path.name} is not built; run __graft_entry__.build()")
@@ -130,6 +227,11 @@ def load_skeletons(mas) -> None:
     fn.restype = ctypes.c_int
     fn.argtypes = [ctypes.c_void_p, ctypes.c_int64] * 4 + [ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p]
     _skeleton_fn = fn
+    fn = lib.mas_bench_rope_append_skeleton
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p] + [ctypes.c_int64] * 3 + [ctypes.c_void_p] * 2 + [ctypes.c_int64] * 2 + \
+        [ctypes.c_void_p]
+    _rope_append_skeleton_fn = fn
     _stamp_fn = lib.mas_bench_timestamp
     _stamp_fn.restype = ctypes.c_int
     _stamp_fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
@@ -211,6 +313,16 @@ def skeleton_launcher(b, op):
     elif op == "append_paged_kv_cache":
         k, v, row = li.k, li.v, s.kv_heads * s.head_dim
         args = (k, k.stride(0), v, v.stride(0), li.k_cache, row, li.v_cache, row, n, row)
+    elif op == "rope_append":
+        qkv, row = li.qkv, s.kv_heads * s.head_dim
+        ptrs = (qkv.data_ptr(), qkv.stride(0), (s.q_heads + s.kv_heads) * s.head_dim, row, li.k_cache.data_ptr(),
+                li.v_cache.data_ptr(), row, n)
+
+        def launch_fused():
+            st = _rope_append_skeleton_fn(*ptrs, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            if st != 0:
+                raise RuntimeError(f"memory skeleton of {op} failed with status {st}")
+        return launch_fused
     else:
         raise ValueError(op)
     ptrs = [a.data_ptr() if isinstance(a, torch.Tensor) else a for a in args]
@@ -625,13 +737,53 @@ class EmbeddingBench:
         return entry, steps
 
 
-def run_layer_workload(mas, args, shape, dev) -> dict:
+def layer_sets(mas, args, shape, dev) -> list:
+    """The layer buffer sets a one-layer workload cycles: enough distinct sets (each with its own KV
+    cache) that no step finds its data in the Infinity Cache (cold), or one (hot)."""
     wl, lp = mas.workloads, mas.layer_pass
     n_sets = 1 if args.protocol == "hot" else max(2, math.ceil(COLD_BYTES / footprint_bytes(shape)))
+    if args.sets is not None and args.protocol != "hot":
+        n_sets = args.sets
     table = mas.rope.cos_sin_cache(shape.max_position, shape.head_dim, shape.theta).to(dev)
-    sets = [lp.LayerBuffers(wl.make_layer_inputs(shape, dev, seed=i, fill_on_device=True, table=table,
-                                                     zero_cache=False),
+    return [lp.LayerBuffers(wl.make_layer_inputs(shape, dev, seed=i, fill_on_device=True,
+                                                 table=table.clone() if args.table_per_set else table,
+                                                 zero_cache=False),
                             fp8=args.fp8, fuse_rope_kv=not args.separate_rope_kv) for i in range(n_sets)]
+
+
+def op_launches(shape, n_sets: int) -> int:
+    """Launches per graph when each kernel is timed alone (decode: at least 100 back to back)."""
+    if shape.layers > 1:
+        return shape.layers
+    return max(2 * n_sets, 100) if shape.decode else 4 * n_sets
+
+
+def timed_kernels(shape, fp8: bool) -> tuple[str, ...]:
+    """The step's kernels followed by the memory skeletons of those that have one."""
+    kernels = step_ops(shape, fp8)
+    skeletons = tuple(f"skeleton:{op}" for op in kernels if op in SKELETON_OPS and shape.tokens <= 65535) \
+        if _skeleton_fn is not None else ()
+    return kernels + skeletons
+
+
+def op_table(mas, shape, kernels: tuple[str, ...], op_us: dict) -> dict:
+    """Per-kernel µs, credited GB/s and fraction of peak, with the memory skeleton's µs and
+    `of_skeleton` (skeleton µs / kernel µs) where the skeleton was timed."""
+    cb = mas.workloads.credited_bytes(shape)
+    ops = {op: {"us": round(op_us[op], 3), "GB/s": round(cb[op] / op_us[op] / 1e3, 1),
+                "frac": round(cb[op] / op_us[op] / 1e3 / PEAK_HBM_GBS, 4)} for op in kernels}
+    for op in kernels:
+        if f"skeleton:{op}" in op_us:
+            sk = op_us[f"skeleton:{op}"]
+            ops[op]["skeleton_us"] = round(sk, 3)
+            ops[op]["of_skeleton"] = round(sk / op_us[op], 3)
+    return ops
+
+
+def run_layer_workload(mas, args, shape, dev) -> dict:
+    wl, lp = mas.workloads, mas.layer_pass
+    sets = layer_sets(mas, args, shape, dev)
+    n_sets = len(sets)
     fused = not args.separate_rope_kv
     per_step = wl.layer_credited_bytes(shape, fused, args.fp8)
     steps = args.steps if args.steps is not None else (2000 if shape.decode else 40)
@@ -664,20 +816,11 @@ def run_layer_workload(mas, args, shape, dev) -> dict:
     torch.cuda.synchronize()
     stream_us = (time.perf_counter() - s0) / stream_steps * 1e6
 
-    launches = max(2 * n_sets, 100) if shape.decode else 4 * n_sets
     kernels = step_ops(shape, args.fp8)
     eager = eager_host_us(mas, sets, kernels) if shape.decode else None
-    skeletons = tuple(f"skeleton:{op}" for op in kernels if op in SKELETON_OPS and shape.tokens <= 65535) \
-        if _skeleton_fn is not None else ()
-    op_us = time_ops(mas, sets, launches, kernels + skeletons)
+    op_us = time_ops(mas, sets, op_launches(shape, n_sets), timed_kernels(shape, args.fp8))
+    ops = op_table(mas, shape, kernels, op_us)
     cb = wl.credited_bytes(shape)
-    ops = {op: {"us": round(op_us[op], 3), "GB/s": round(cb[op] / op_us[op] / 1e3, 1),
-                "frac": round(cb[op] / op_us[op] / 1e3 / PEAK_HBM_GBS, 4)} for op in kernels}
-    for op in kernels:
-        if f"skeleton:{op}" in op_us:
-            sk = op_us[f"skeleton:{op}"]
-            ops[op]["skeleton_us"] = round(sk, 3)
-            ops[op]["of_skeleton"] = round(sk / op_us[op], 3)
     step_inputs = None
     if shape.decode and not shape.norm_only:
         ops["embedding"], step_inputs = EmbeddingBench(mas, shape, dev).report()
@@ -702,10 +845,9 @@ def run_pass_workload(mas, args, shape, dev) -> dict:
     timing = time_steps(lambda lo, hi: [passes[0].run() for _ in range(lo, hi)], steps, warmup, lead=1, per_graph=10)
     elapsed = timing["device_s"]
     ops_timed = step_ops(shape, args.fp8)
-    op_us = time_ops(mas, passes[0].layers, shape.layers, ops_timed)
+    op_us = time_ops(mas, passes[0].layers, op_launches(shape, 1), timed_kernels(shape, args.fp8))
+    ops = op_table(mas, shape, ops_timed, op_us)
     cb = wl.credited_bytes(shape)
-    ops = {op: {"us": round(us, 3), "GB/s": round(cb[op] / us / 1e3, 1),
-                "frac": round(cb[op] / us / 1e3 / PEAK_HBM_GBS, 4)} for op, us in op_us.items()}
     ops["embedding"], step_inputs = EmbeddingBench(mas, shape, dev).report()
     ms_per_step = elapsed / steps * 1e3
     dominant = ops_timed[3]
@@ -714,6 +856,20 @@ def run_pass_workload(mas, args, shape, dev) -> dict:
             "dominant_bytes": cb[dominant], "dominant_us": op_us[dominant],
             "us_per_layer": ms_per_step * 1e3 / shape.layers, "graph_us_per_step": timing["graph_s"] / steps * 1e6,
             "host_us_per_step": timing["host_s"] / steps * 1e6, "step_inputs": step_inputs}
+
+
+def graph_call_us(call, calls: int) -> float:
+    """Per-call µs of an attention call: HIP events around a graph of ``calls`` back-to-back calls,
+    replayed once untimed, then the median of five timed replays."""
+    gb = capture(lambda: [call() for _ in range(calls)])
+    gb.replay()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(5)]
+    for start, stop in events:
+        start.record()
+        gb.replay()
+        stop.record()
+    torch.cuda.synchronize()
+    return 1000.0 * sorted(a.elapsed_time(b) for a, b in events)[2] / calls
 
 
 def run_attention_workload(mas, args, shape, dev) -> dict:
@@ -733,17 +889,7 @@ def run_attention_workload(mas, args, shape, dev) -> dict:
     call()
     timing = time_steps(lambda lo, hi: [call() for _ in range(lo, hi)], steps, warmup, lead=4, per_graph=10)
     elapsed = timing["device_s"]
-    # per-call duration: HIP events around graphs of back-to-back calls, median of five replays
-    graph_calls = 10
-    gb = capture(lambda: [call() for _ in range(graph_calls)])
-    gb.replay()
-    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(5)]
-    for start, stop in events:
-        start.record()
-        gb.replay()
-        stop.record()
-    torch.cuda.synchronize()
-    call_us = 1000.0 * sorted(a.elapsed_time(b) for a, b in events)[2] / graph_calls
+    call_us = graph_call_us(call, 10)
     ms_per_step = elapsed / steps * 1e3
     lens = inp.seq_lens.cpu()
     return {"steps": steps, "warmup": warmup, "ms_per_step": ms_per_step, "per_step_bytes": per_step,
@@ -779,20 +925,17 @@ def context_main(mas, args, shape, dev) -> int:
         print(json.dumps({"pmc_probe": "paged_context_attention", "launches": 5, "flops_per_launch": flops}),
               flush=True)
         return 0
+    if args.trace_probe:
+        call()
+        print(json.dumps({"trace_probe": "ops", "workload": shape.name, "calls_per_graph": 4,
+                          "event_us_per_call": round(graph_call_us(call, 4), 3)}), flush=True)
+        return 0
     steps = args.steps if args.steps is not None else 20
     warmup = args.warmup if args.warmup is not None else 3
     call()
     timing = time_steps(lambda lo, hi: [call() for _ in range(lo, hi)], steps, warmup, lead=1, per_graph=4)
     elapsed = timing["device_s"]
-    gb = capture(lambda: [call() for _ in range(4)])
-    gb.replay()
-    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(5)]
-    for start, stop in events:
-        start.record()
-        gb.replay()
-        stop.record()
-    torch.cuda.synchronize()
-    call_us = 1000.0 * sorted(x.elapsed_time(y) for x, y in events)[2] / 4
+    call_us = graph_call_us(call, 4)
     ms_per_step = elapsed / steps * 1e3
     tflops = flops / (ms_per_step * 1e-3) / 1e12
     kernel_tflops = flops / (call_us * 1e-6) / 1e12
@@ -809,9 +952,7 @@ def context_main(mas, args, shape, dev) -> int:
         "host_us_per_call": round(timing["host_s"] / steps * 1e6, 3),
         "ops": {"paged_context_attention": {"us": round(call_us, 3), "TFLOP/s": round(kernel_tflops, 1),
                                             "frac": round(kernel_tflops / PEAK_BF16_TFLOPS, 4)}},
-        "roofline": {"bound": "mfma", "kernel": "paged_context_attention", "achieved": round(kernel_tflops, 1),
-                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(kernel_tflops / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None, "flops_per_launch": flops, "avg_launch_us": round(call_us, 3)},
+        "roofline": roofline_entry(shape.name, "paged_context_attention", flops, call_us, bound="mfma"),
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_torch_context(inp, args.cpu_seconds)
@@ -968,6 +1109,38 @@ def pmc_probe(mas, args, shape, dev) -> None:
                       "calibration_copy_bytes": 256 << 20}), flush=True)
 
 
+def trace_probe(mas, args, shape, dev) -> None:
+    """Launches only what a kernel trace of the bench's own timing needs, so the trace's per-dispatch
+    durations come from the same graphs the line's HIP-event figures do: ``ops`` - each kernel's
+    graph of back-to-back launches (and its memory skeleton's), replayed once untimed and five
+    times timed; ``steps`` - the stamped step graphs alone. Prints the HIP-event figures."""
+    if shape.layers > 1:
+        p = mas.layer_pass.DecodePass(shape, dev, seed=0, fp8=args.fp8, fuse_rope_kv=not args.separate_rope_kv)
+        sets = p.layers
+
+        def run_range(lo, hi):
+            for _ in range(lo, hi):
+                p.run()
+        steps, warmup, lead, per_graph = args.steps or 20, args.warmup or 3, 1, 10
+    else:
+        sets = layer_sets(mas, args, shape, dev)
+
+        def run_range(lo, hi):
+            for i in range(lo, hi):
+                mas.layer_pass.run_layer(sets[i % len(sets)])
+        per_graph = len(sets) * max(1, math.ceil(50 / len(sets)))
+        steps, warmup, lead = args.steps or (200 if shape.decode else 20), args.warmup or len(sets), per_graph
+    out = {"trace_probe": args.trace_probe, "workload": shape.name, "layer_sets": len(sets)}
+    if args.trace_probe == "ops":
+        launches = op_launches(shape, len(sets))
+        op_us = time_ops(mas, sets, launches, timed_kernels(shape, args.fp8))
+        out.update({"launches_per_graph": launches, "replays": 6, "event_us": {k: round(v, 3) for k, v in op_us.items()}})
+    else:
+        timing = time_steps(run_range, steps, warmup, lead=lead, per_graph=per_graph)
+        out.update({"steps": steps, "us_per_step": round(timing["device_s"] / steps * 1e6, 3)})
+    print(json.dumps(out), flush=True)
+
+
 def main() -> int:
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -992,12 +1165,14 @@ def main() -> int:
     if args.pmc_probe:
         pmc_probe(mas, args, shape, dev)
         return 0
+    if args.trace_probe:
+        trace_probe(mas, args, shape, dev)
+        return 0
     if shape.layers > 1:
         res = run_pass_workload(mas, args, shape, dev)
     else:
         res = run_layer_workload(mas, args, shape, dev)
 
-    dom_gbs = res["dominant_bytes"] / res["dominant_us"] / 1e3
     line = {
         "metric": METRIC,
         "value": round(res["value"], 2),
@@ -1020,15 +1195,8 @@ def main() -> int:
         "us_per_layer": round(res.get("us_per_layer", res["ms_per_step"] * 1e3), 3),
         "frac_of_peak": round(res["value"] / PEAK_HBM_GBS, 4),
         "ops": res["ops"],
-        "roofline": {"bound": "hbm", "kernel": res["dominant"], "achieved": round(dom_gbs, 1),
-                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(dom_gbs / PEAK_HBM_GBS, 4),
-                     "traffic": MEASURED_TRAFFIC.get((shape.name, res["dominant"])),
-                     "bytes_per_launch": res["dominant_bytes"],
-                     "avg_launch_us": round(res["dominant_us"], 3)},
+        "roofline": roofline_entry(shape.name, res["dominant"], res["dominant_bytes"], res["dominant_us"]),
     }
-    traced = TRACED_LAUNCH_US.get((shape.name, res["dominant"]))
-    if traced is not None:
-        line["roofline"]["traced_avg_launch_us"], line["roofline"]["traced_in"] = traced
     dom = res["ops"].get(res["dominant"], {})
     if "skeleton_us" in dom:
         # the same bytes, buffers and launch shape moved by a kernel with no arithmetic, same run
@@ -1072,8 +1240,20 @@ def attention_main(mas, args, shape, dev) -> int:
                           "bytes_per_launch": wl.attention_credited_bytes(inp),
                           "calibration_copy_bytes": 256 << 20}), flush=True)
         return 0
+    if args.trace_probe:
+        wl = mas.workloads
+        inp = wl.make_attention_inputs(shape, dev, seed=0)
+        out = torch.empty_like(inp.q)
+
+        def call():
+            mas.attention.trtllm_batch_decode_with_kv_cache(inp.q, (inp.k_cache, inp.v_cache), inp.workspace,
+                                                            inp.block_tables, inp.seq_lens, 0,
+                                                            shape.head_dim ** -0.5, 1.0, out=out)
+        call()
+        print(json.dumps({"trace_probe": "ops", "workload": shape.name, "calls_per_graph": 10,
+                          "event_us_per_call": round(graph_call_us(call, 10), 3)}), flush=True)
+        return 0
     res = run_attention_workload(mas, args, shape, dev)
-    dom_gbs = res["dominant_bytes"] / res["dominant_us"] / 1e3
     line = {
         "metric": METRIC, "value": round(res["value"], 2), "unit": "GB/s", "n_gpus": 1, "steps": res["steps"],
         "warmup": res["warmup"], "ms_per_step": round(res["ms_per_step"], 6), "higher_is_better": True,
@@ -1085,15 +1265,9 @@ def attention_main(mas, args, shape, dev) -> int:
         "graph_us_per_call": round(res["graph_us_per_step"], 3), "host_us_per_call": round(res["host_us_per_step"], 3),
         "frac_of_peak": round(res["value"] / PEAK_HBM_GBS, 4),
         "ops": res["ops"],
-        "roofline": {"bound": "hbm", "kernel": res["dominant"], "achieved": round(dom_gbs, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(dom_gbs / PEAK_HBM_GBS, 4),
-                     "traffic": MEASURED_TRAFFIC.get((shape.name, res["dominant"])),
-                     "bytes_per_launch": res["dominant_bytes"], "avg_launch_us": round(res["dominant_us"], 3)},
+        "roofline": roofline_entry(shape.name, res["dominant"], res["dominant_bytes"], res["dominant_us"]),
         "copy_ceiling_GBps": round(copy_ceiling_gbs(dev), 1),
     }
-    traced = TRACED_LAUNCH_US.get((shape.name, res["dominant"]))
-    if traced is not None:
-        line["roofline"]["traced_avg_launch_us"], line["roofline"]["traced_in"] = traced
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_torch_attention(res["inputs"], args.cpu_seconds)
         line["cpu_oracle"] = cpu_oracle_attention(res["inputs"], args.cpu_seconds / 2)

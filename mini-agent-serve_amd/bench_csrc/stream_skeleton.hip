@@ -37,6 +37,26 @@ __global__ __launch_bounds__(256) void stream_skeleton(SkeletonStreams s, int64_
   }
 }
 
+// The fused RoPE + KV append kernel's streams: each token's qkv row is read once; its q and k
+// vectors are written back in place, k also to a key-cache row and v to a value-cache row (cache
+// rows consecutive per token, as the KV skeleton writes them). The in-place write-back goes through
+// `qkv_out`, the same address passed as a second pointer: a store of a just-loaded value through
+// the pointer it was loaded from would be removed by the compiler, with its load.
+__global__ __launch_bounds__(256) void rope_append_skeleton(const uint16_t* qkv, uint16_t* qkv_out, int64_t qkv_stride,
+                                                            int64_t qk_vecs, int64_t kv_vecs, uint16_t* k_cache,
+                                                            uint16_t* v_cache, int64_t cache_stride) {
+  const int64_t v = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t row = blockIdx.y;
+  if (v >= qk_vecs + kv_vecs) return;
+  const u32x4 x = load_stream(qkv + row * qkv_stride + 8 * v);
+  if (v < qk_vecs) {
+    store_stream(qkv_out + row * qkv_stride + 8 * v, x);
+    if (v >= qk_vecs - kv_vecs) store_stream(k_cache + row * cache_stride + 8 * (v - (qk_vecs - kv_vecs)), x);
+  } else {
+    store_stream(v_cache + row * cache_stride + 8 * (v - qk_vecs), x);
+  }
+}
+
 }  // namespace
 }  // namespace mas
 
@@ -68,5 +88,28 @@ extern "C" int mas_bench_stream_skeleton(const void* src0, int64_t src0_stride, 
     hipLaunchKernelGGL((stream_skeleton<2, 2>), grid, dim3(block), 0, stream, s, row_vecs);
   else
     hipLaunchKernelGGL((stream_skeleton<2, 1>), grid, dim3(block), 0, stream, s, row_vecs);
+  return launch_status();
+}
+
+// The fused RoPE + KV append's memory skeleton: rows of [q | k | v] (qk_elems + kv_elems elements
+// each, the last kv_elems of the q|k part being k) read once; q|k written back in place, k to
+// k_cache and v to v_cache rows of cache_stride elements. Rows up to 65535; every size a multiple
+// of 8 and every pointer and stride 16-byte aligned.
+extern "C" int mas_bench_rope_append_skeleton(void* qkv, int64_t qkv_stride, int64_t qk_elems, int64_t kv_elems,
+                                              void* k_cache, void* v_cache, int64_t cache_stride, int64_t rows,
+                                              hipStream_t stream) {
+  using namespace mas;
+  if (rows < 0 || rows > 65535 || qk_elems < kv_elems || kv_elems < 0) return MAS_ERR_INVALID_VALUE;
+  if (rows == 0 || qk_elems == 0) return MAS_OK;
+  if (qkv == nullptr || k_cache == nullptr || v_cache == nullptr) return MAS_ERR_INVALID_VALUE;
+  if (qk_elems % 8 != 0 || kv_elems % 8 != 0 || qkv_stride % 8 != 0 || cache_stride % 8 != 0 ||
+      qkv_stride < qk_elems + kv_elems || cache_stride < kv_elems || !aligned16(qkv) || !aligned16(k_cache) ||
+      !aligned16(v_cache))
+    return MAS_ERR_INVALID_VALUE;
+  const int64_t vecs = (qk_elems + kv_elems) / 8;
+  const dim3 grid(static_cast<uint32_t>(cdiv(vecs, 256)), static_cast<uint32_t>(rows));
+  hipLaunchKernelGGL(rope_append_skeleton, grid, dim3(256), 0, stream, static_cast<const uint16_t*>(qkv),
+                     static_cast<uint16_t*>(qkv), qkv_stride, qk_elems / 8, kv_elems / 8,
+                     static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), cache_stride);
   return launch_status();
 }

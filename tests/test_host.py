@@ -271,3 +271,55 @@ def test_graph_context_workload_layout(mas):
     assert int(real.min()) >= 0 and int(real.max()) < sink and real.unique().numel() == real.numel()
     assert torch.all(tables[3] == sink) and torch.all(tables[4:, 0] == sink)
     assert mas.workloads.context_flops(s) == 3 * sum(2000 + i + 1 for i in range(100)) * 32 * 128 * 4
+
+
+# ---- the bench line's profiled figures --------------------------------------------------------------
+
+def _bench():
+    import sys
+    sys.path.insert(0, str(ROOT))
+    import bench
+    return bench
+
+
+def test_source_blob_is_git_hash_object():
+    """The staleness check hashes a source as `git hash-object` does: sha1 of "blob <size>\\0" + bytes."""
+    import hashlib
+    bench = _bench()
+    rel = "csrc/silu_and_mul.hip"
+    data = (ROOT / "mini-agent-serve_amd" / rel).read_bytes()
+    want = hashlib.sha1(b"blob " + str(len(data)).encode() + b"\0" + data).hexdigest()
+    assert bench.source_blob(rel) == want
+
+
+def test_roofline_follows_a_fresh_trace_and_flags_a_stale_one(monkeypatch):
+    """With its sources unchanged, the roofline's rate and frac come from the committed trace; with
+    a source hash that no longer matches, from the live HIP-event time, flagged stale."""
+    bench = _bench()
+    key = ("decode64_24b", "silu_and_mul")
+    traced = bench.TRACED_LAUNCH_US[key]
+    fresh = dict(traced, sources={rel: bench.source_blob(rel) for rel in bench.KERNEL_SOURCES["silu_and_mul"]})
+    monkeypatch.setitem(bench.TRACED_LAUNCH_US, key, fresh)
+    e = bench.roofline_entry(*key, 12_582_912, 3.5)
+    assert e["avg_launch_us"] == round(fresh["us"], 3) and not e["trace_stale"]
+    assert e["frac"] == round(12_582_912 / fresh["us"] / 1e3 / 8000.0, 4)
+    assert e["frac_event"] == round(12_582_912 / 3.5 / 1e3 / 8000.0, 4)
+    stale = dict(fresh, sources={**fresh["sources"], "csrc/silu_and_mul.hip": "0" * 40})
+    monkeypatch.setitem(bench.TRACED_LAUNCH_US, key, stale)
+    e = bench.roofline_entry(*key, 12_582_912, 3.5)
+    assert e["trace_stale"] and e["avg_launch_us"] == 3.5 and e["timing"] == "hip-events (live)"
+    # flops-bound lines use the same rule
+    m = bench.roofline_entry("no_such_workload", "paged_context_attention", 1e12, 500.0, bound="mfma")
+    assert m["unit"] == "TFLOP/s" and m["frac"] == round(1e12 / 500.0 / 1e6 / 2500.0, 4)
+
+
+def test_profiled_figures_name_existing_profiles_that_hold_them():
+    """Every profiled figure cites a committed profile that states it, and records the hash of every
+    source its kernel is built from."""
+    bench = _bench()
+    for table, field, fmt in ((bench.TRACED_LAUNCH_US, "us", None), (bench.MEASURED_TRAFFIC, "bytes", "{:,}")):
+        for (workload, kernel), entry in table.items():
+            text = (ROOT / entry["profile"]).read_text()
+            assert set(entry["sources"]) == set(bench.KERNEL_SOURCES[kernel]), (workload, kernel)
+            if fmt is not None:
+                assert fmt.format(entry[field]) in text, (workload, kernel, entry[field])
