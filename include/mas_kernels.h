@@ -44,6 +44,8 @@ extern "C" {
 #define MAS_ERR_DEVICE (-4)        /* hipGetDevice / device-attribute query failed        */
 #define MAS_ERR_SCRATCH (-5)       /* the call needs more scratch than the no-allocation
                                       entry point's static buffer holds                    */
+#define MAS_ERR_NOT_READY (-6)     /* the no-allocation entry point's first call on a device
+                                      came under graph capture: make one call outside it   */
 
 #define MAS_ERRBIT_TOKEN_ID 1u  /* embedding: id < 0 or id >= vocab                       */
 #define MAS_ERRBIT_POSITION 2u  /* rope: position < 0 or >= table rows; kv: position < 0;
@@ -297,9 +299,14 @@ int mas_paged_context_attention_bf16(void* out, int64_t out_stride, int64_t out_
 /*
  * mas_paged_decode_attention_bf16 without a workspace argument: the same kernels and results, with
  * the split partials in a scratch array the library keeps in device memory, one per GPU it runs on,
- * MAS_DECODE_ATTENTION_SCRATCH_BYTES long, held until the process ends. No allocation happens in the
+ * MAS_DECODE_ATTENTION_SCRATCH_BYTES long, held until the process ends. The array is part of the
+ * library's code object: every process that loads the library holds it on each GPU where the library's
+ * kernels are loaded, whether or not it calls this entry point. No allocation happens in the
  * call: the array's address is looked up once per device, on the first call there (the caller's
- * current device is left as it was). Splits are made as long as needed for the partials to fit the
+ * current device is left as it was). That first call must not be made while `stream` is being
+ * captured into a graph (the lookup may load the code object): it then returns MAS_ERR_NOT_READY and
+ * enqueues nothing; one call outside capture per device sets the lookup up, after which captured
+ * calls work. Splits are made as long as needed for the partials to fit the
  * array; a call that does not fit even with one split per row (batch * num_q_heads * (head_dim + 2)
  * * 4 bytes over the limit) returns MAS_ERR_SCRATCH and enqueues nothing. Every call on one GPU
  * uses that GPU's one array: calls that overlap in time on one GPU (on different streams) race and

@@ -733,13 +733,18 @@ std::atomic<void*> g_scratch_ptr[kMaxDevices];
 std::mutex g_scratch_mutex;
 
 // The scratch array's address on the stream's device, looked up once per device with that device
-// current (and the caller's current device restored).
+// current (and the caller's current device restored). The lookup may load the code object that
+// holds the array, so it is not made while `stream` is being captured into a graph: such a first
+// call returns MAS_ERR_NOT_READY, and one call outside capture on the device sets it up.
 int scratch_address(hipStream_t stream, void** ptr) {
   int dev = 0;
   if (hipStreamGetDevice(stream, &dev) != hipSuccess) return MAS_ERR_DEVICE;
   if (dev < 0 || dev >= kMaxDevices) return MAS_ERR_UNSUPPORTED;
   void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
   if (p == nullptr) {
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &capture) != hipSuccess) return MAS_ERR_DEVICE;
+    if (capture != hipStreamCaptureStatusNone) return MAS_ERR_NOT_READY;
     std::lock_guard<std::mutex> lock(g_scratch_mutex);
     p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
     if (p == nullptr) {

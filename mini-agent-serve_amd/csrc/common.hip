@@ -35,6 +35,9 @@ extern "C" const char* mas_status_string(int status) {
     case MAS_ERR_MISALIGNED: return "pointer or stride breaks the kernel's 16-byte alignment";
     case MAS_ERR_DEVICE: return "device query failed";
     case MAS_ERR_SCRATCH: return "the call needs more scratch than the no-allocation entry point holds";
+    case MAS_ERR_NOT_READY:
+      return "the no-allocation entry point's first call on a device came under graph capture; make one call outside "
+             "capture first";
     default: break;
   }
   if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));

@@ -15,6 +15,7 @@ pytestmark = pytest.mark.gpu
 
 SCRATCH_BYTES = 64 << 20          # MAS_DECODE_ATTENTION_SCRATCH_BYTES
 MAS_ERR_SCRATCH = -5
+MAS_ERR_NOT_READY = -6
 
 
 def _inputs(dev, batch, hq, hk, d, page_size, max_len, seed):
@@ -88,3 +89,61 @@ def test_noalloc_through_the_wrapper_and_a_graph(mas, dev):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, want)
+
+
+_FIRST_CALL_UNDER_CAPTURE = r"""
+import json, sys
+import torch
+sys.path.insert(0, sys.argv[1])
+sys.path.insert(0, sys.argv[1] + "/tests")
+import __graft_entry__
+from test_zz_no_alloc import _call, _inputs
+mas = __graft_entry__.load_package()
+lib = mas._lib.load()
+dev = torch.device("cuda:0")
+q, kc, vc, tables, lens = _inputs(dev, 8, 32, 8, 128, 256, 2000, seed=7)
+want = torch.empty_like(q)
+ws = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+assert _call(lib, False, q, kc, vc, tables, lens, want, ws) == 0
+out = torch.zeros_like(q)
+torch.cuda.synchronize()
+codes = []
+g0 = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g0):           # the entry point's first call in this process, under capture
+    codes.append(_call(lib, True, q, kc, vc, tables, lens, out))
+torch.cuda.synchronize()
+untouched = not out.any().item()
+codes.append(_call(lib, True, q, kc, vc, tables, lens, out))      # outside capture: sets up the scratch
+torch.cuda.synchronize()
+eager_ok = torch.equal(out, want)
+out.zero_()
+g1 = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g1):
+    codes.append(_call(lib, True, q, kc, vc, tables, lens, out))
+replays_ok = []
+for _ in range(2):
+    out.zero_()
+    torch.cuda.synchronize()
+    g1.replay()
+    torch.cuda.synchronize()
+    replays_ok.append(torch.equal(out, want))
+print(json.dumps({"codes": codes, "untouched": untouched, "eager_ok": eager_ok, "replays_ok": replays_ok,
+                  "text": lib.mas_status_string(codes[0]).decode()}))
+"""
+
+
+def test_noalloc_first_call_under_capture_in_a_fresh_process(mas, dev):
+    """In a process that has not called the entry point yet, a first call under graph capture is
+    rejected with MAS_ERR_NOT_READY and enqueues nothing; one eager call sets the scratch up, after
+    which a captured call works and its replays match the workspace entry point."""
+    import json
+    import subprocess
+    import sys
+    from conftest import ROOT
+    proc = subprocess.run([sys.executable, "-c", _FIRST_CALL_UNDER_CAPTURE, str(ROOT)], capture_output=True,
+                          text=True, timeout=300)
+    assert proc.returncode == 0, proc.stderr[-2000:]
+    res = json.loads(proc.stdout.strip().splitlines()[-1])
+    assert res["codes"] == [MAS_ERR_NOT_READY, 0, 0], res
+    assert res["untouched"] and res["eager_ok"] and all(res["replays_ok"]), res
+    assert "outside capture" in res["text"]
