@@ -43,8 +43,11 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 //                split count picked on the host, from the grid's size);
 //   kWorkPlan  - one workgroup per item of a plan that context_plan wrote from the real lengths on
 //                the device (a graph captured with padded rows and token counts: the host only knows
-//                bounds, so the split decision waits for the lengths).
-constexpr int kWorkGrid = 0, kWorkSplit = 1, kWorkPlan = 2;
+//                bounds, so the split decision waits for the lengths);
+//   kWorkSelfPlan - the same plan, laid out by each workgroup itself from the rows' lengths (at most
+//                64 rows: one per lane), with no planner launch.
+constexpr int kWorkGrid = 0, kWorkSplit = 1, kWorkPlan = 2, kWorkSelfPlan = 3;
+constexpr int kSelfPlanMaxRows = 64;
 
 // The planner: one workgroup; rows and (row, token tile) units it handles, at most.
 constexpr int kPlanThreads = 256;
@@ -85,6 +88,10 @@ struct ContextArgs {
   const i32x4* plan_items;
   const i32x4* plan_units;
   int plan_rows, plan_gy;  // the rows and token tiles per row of the unsplit grid
+  // kWorkSelfPlan: what the plan's estimate needs (CUs, resident workgroups, the grid's workgroups,
+  // the partial entries the workspace holds) and the block table's reach
+  int plan_cus, plan_resident;
+  int64_t plan_item_cap, plan_entry_cap, plan_cap;
   float scale_log2;
   float out_scale;
   void* out;                // bf16, or fp8 e4m3fn codes when out_fp8
@@ -186,12 +193,262 @@ __host__ __device__ inline int64_t split_from_reach(const SplitModel& m, int64_t
   return hint;
 }
 
+// The planner's estimate (SplitModel's terms, with the real lengths): split k ways, the longest
+// unit is cut into ranges of per = max(4, ceil(longest / k)) key tiles and so is every unit longer
+// than per; the rest stay whole. Its time is that of a workgroup of per tiles, (per + 4.8) x 1.8 us
+// with at most one workgroup per CU, else x 2.1 us per round of resident workgroups, plus, split,
+// 5 us (the merge's launch and the planner's item writes, 3 us more than an unsplit plan's on
+// MI355X) and the merge: the partials' bytes at 5 TB/s or 0.9 ns per (token, head) pair of the
+// split units, whichever is longer (the planned merge takes its pairs in turn on a fixed grid:
+// 12,288 pairs in 9.6-11 us, against 0.6 ns per pair for the grid launch's merge, which has a
+// wavefront per pair).
+struct PlanModel {
+  int units, head_blocks, longest;
+  int cus, resident;
+  int item_cap;           // workgroups of the main grid
+  int64_t entry_cap;      // partial entries the workspace holds
+  int entries_per_unit;   // partial entries of a split unit per split (head blocks x tokens x heads)
+  float pair_us;          // merge microseconds per split unit (its (token, head) pairs)
+  float entry_us;         // microseconds per partial entry moved at 5 TB/s
+};
+
+__device__ float plan_time(const PlanModel& m, int wgs, int per) {
+  const float per_wg = static_cast<float>(per) + 4.8f;
+  return wgs <= m.cus ? per_wg * 1.8f : static_cast<float>((wgs + m.resident - 1) / m.resident) * per_wg * 2.1f;
+}
+
+// Whether no split can pay for units reaching at most `longest` key tiles: the unsplit estimate,
+// at most one workgroup per CU (else no split is weighed), against the least any split costs (a
+// split length of 4 tiles in one round, plus the fixed 5 us).
+__device__ bool plan_never_splits(int longest) {
+  return 0.8f * ((static_cast<float>(longest) + 4.8f) * 1.8f) <= (4.f + 4.8f) * 1.8f + 5.0f;
+}
+
+// The split length for k splits, or 0 where k is not weighed (the same split as a smaller count,
+// or more splits than kMaxCtxSplits).
+__device__ int plan_per(const PlanModel& m, int k) {
+  if (k > kMaxCtxSplits) return 0;
+  const int tiles = (m.longest + k - 1) / k;
+  if ((m.longest + tiles - 1) / tiles != k) return 0;
+  return max(4, tiles);
+}
+
+// ---- planned launches planned in the kernels --------------------------------------------------
+// With at most 64 rows (the runner's graph steps have 17), every workgroup of the attention kernel
+// and of its merge lays the plan out itself from the rows' real lengths, one row per lane, instead
+// of reading it from a planner launch: the same units, split count, items and partial slots as
+// context_plan writes, so the same results, with one launch fewer.
+
+// Key tiles that token tile t of a row reaches (shift = kv_len - q_len; tokens per tile 2^lt).
+__device__ __forceinline__ int tile_key_tiles(int shift, int q_len, int lt, int t) {
+  const int reach = shift + min((t + 1) << lt, q_len);
+  return reach > 0 ? (reach + kTileP - 1) / kTileP : 0;
+}
+
+// A row as the plan sees it (this lane's row; lanes past the rows hold an empty one).
+struct PlanRow {
+  int q0, q_len, kv, tiles, shift;
+  bool bad;  // a length error the plan reports (kv_len below q_len or past the table, or more tokens
+             // than the grid's token tiles cover)
+};
+
+__device__ __forceinline__ PlanRow plan_row(const int32_t* cu_seqlens_q, const int32_t* seq_lens, int rows, int gy,
+                                            int lt, int64_t cap, int lane) {
+  PlanRow r{0, 0, 0, 0, 0, false};
+  if (lane < rows) {
+    const int q0 = cu_seqlens_q[lane];
+    const int64_t q_len = static_cast<int64_t>(cu_seqlens_q[lane + 1]) - q0;
+    const int64_t raw = seq_lens[lane];
+    const int64_t covered = static_cast<int64_t>(gy) << lt;
+    r.q0 = q0;
+    r.q_len = q_len > 0 ? static_cast<int>(q_len) : 0;
+    r.kv = static_cast<int>(raw < 0 ? 0 : (raw > cap ? cap : raw));
+    if (q_len > 0) {
+      r.tiles = static_cast<int>((min(q_len, covered) + (int64_t{1} << lt) - 1) >> lt);
+      r.bad = raw < q_len || raw > cap || q_len > covered;
+    }
+    r.shift = r.kv - r.q_len;
+  }
+  return r;
+}
+
+// Token tiles of a row reaching more than p key tiles: its last ones (a tile's reach grows with it).
+__device__ __forceinline__ int tiles_over(int shift, int q_len, int tiles, int lt, int p) {
+  if (tiles == 0 || tile_key_tiles(shift, q_len, lt, tiles - 1) <= p) return 0;
+  const int x = p * kTileP - shift;  // tile t < tiles - 1 qualifies when (t + 1) * 2^lt > x
+  const int t0 = x < 0 ? 0 : x >> lt;
+  return tiles - min(t0, tiles - 1);
+}
+
+// ceil(a / b) for 0 <= a < 2^24 and b >= 1, from rb = 1 / b: the fp32 quotient is within one of
+// the integer one, which one correction settles.
+__device__ __forceinline__ int ceil_div_small(int a, int b, float rb) {
+  const int n = a + b - 1;
+  int q = static_cast<int>(static_cast<float>(n) * rb);
+  q -= q * b > n ? 1 : 0;
+  q += (q + 1) * b <= n ? 1 : 0;
+  return q;
+}
+
+// Key ranges of a row's token tiles under a split of length per (rp = 1 / per): one per tile, and
+// ceil(key tiles / per) for each of its `split` last tiles.
+__device__ __forceinline__ int row_ranges(int shift, int q_len, int tiles, int lt, int per, float rp, int split) {
+  int ranges = tiles - split;
+  for (int t = tiles - split; t < tiles; ++t) ranges += ceil_div_small(tile_key_tiles(shift, q_len, lt, t), per, rp);
+  return ranges;
+}
+
+__device__ __forceinline__ int lane_i(int x, int l) { return __builtin_amdgcn_readlane(x, l); }
+
+// Minimum over the 64 lanes: DPP within rows of 16, then the four rows' minima.
+__device__ __forceinline__ float wave_min_f(float v) {
+  v = fminf(v, dpp_move<0xb1>(v));   // quad_perm [1,0,3,2]
+  v = fminf(v, dpp_move<0x4e>(v));   // quad_perm [2,3,0,1]
+  v = fminf(v, dpp_move<0x141>(v));  // row_half_mirror
+  v = fminf(v, dpp_move<0x140>(v));  // row_mirror
+  const auto rd = [&](int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l)); };
+  return fminf(fminf(rd(0), rd(16)), fminf(rd(32), rd(48)));
+}
+
+// What the plan's two kernels need besides ContextArgs' fields.
+struct PlanShape {
+  int rows, gy, lt, head_blocks, heads_per_wg, hq, head_dim;  // token tiles of 2^lt tokens
+};
+
+// The plan's split decision, as context_plan makes it: the split count (1: none) and length, the
+// rows with query tokens, and the unsplit plan's workgroups.
+struct SelfPlan {
+  int splits, per;
+  uint64_t live;
+  int grid_items;
+};
+
+// Every row-wise sum below is a scalar loop over the rows with query tokens (`live`, one to three in
+// the runner's graph steps), reading each row's fields from its lane. context_plan checks after the
+// split count that the plan's workgroups and partials fit; they always do: the estimate admits a
+// count only if its bounds on both fit (at most (units + split units x (count - 1)) x head blocks
+// workgroups, since no unit is cut into more ranges than the count, and exactly the partials).
+__device__ SelfPlan self_plan(const PlanRow& r, const PlanShape& s, int cus, int resident, int64_t item_cap,
+                              int64_t entry_cap, int lane) {
+  const uint64_t live = __ballot(r.tiles > 0);
+  SelfPlan pl{1, 0, live, s.rows * s.gy * s.head_blocks};
+  int units = 0, longest = 0;
+  for (uint64_t b = live; b != 0; b &= b - 1) {
+    const int q = __builtin_ctzll(b), tiles = lane_i(r.tiles, q);
+    units += tiles;
+    longest = max(longest, tile_key_tiles(lane_i(r.shift, q), lane_i(r.q_len, q), s.lt, tiles - 1));
+  }
+  if (plan_never_splits(longest) || units == 0 || units * s.head_blocks >= cus) return pl;
+  PlanModel m{};
+  m.units = units;
+  m.head_blocks = s.head_blocks;
+  m.longest = longest;
+  m.cus = cus;
+  m.resident = resident;
+  m.item_cap = static_cast<int>(item_cap);
+  m.entry_cap = entry_cap;
+  m.entries_per_unit = s.head_blocks * (s.heads_per_wg << s.lt);
+  m.pair_us = static_cast<float>(1 << s.lt) * s.hq * 9.0e-4f;
+  m.entry_us = (s.head_dim + 2) * 4.f / 5.0e6f;
+  // lane l weighs l + 2 splits (plan_best_splits), counting the units longer than its split length
+  const int k = lane + 2;
+  const int per_k = plan_per(m, k);
+  float c = __builtin_huge_valf();
+  if (per_k != 0 && per_k < longest) {
+    int split = 0;
+    for (uint64_t b = live; b != 0; b &= b - 1) {
+      const int q = __builtin_ctzll(b);
+      split += tiles_over(lane_i(r.shift, q), lane_i(r.q_len, q), lane_i(r.tiles, q), s.lt, per_k);
+    }
+    const int64_t wgs = static_cast<int64_t>(units + split * (k - 1)) * s.head_blocks;  // at most
+    const int64_t entries = static_cast<int64_t>(split) * m.entries_per_unit * k;
+    if (wgs <= m.item_cap && entries <= m.entry_cap)
+      c = plan_time(m, static_cast<int>(wgs), per_k) + 5.0f +
+          fmaxf(static_cast<float>(entries) * m.entry_us, static_cast<float>(split) * m.pair_us);
+  }
+  const float low = wave_min_f(c);
+  if (!(low < 0.8f * plan_time(m, units * s.head_blocks, longest))) return pl;
+  pl.splits = __builtin_ctzll(__ballot(c == low)) + 2;
+  pl.per = max(4, (longest + pl.splits - 1) / pl.splits);
+  return pl;
+}
+
+// A self-planned launch's workgroup: lays out the plan from the rows' lengths (every wavefront lays
+// out the same plan), then finds workgroup `i`'s item, as context_plan would have written it (the
+// layout of ContextArgs::plan_items). Returns false for a workgroup past the plan's items.
+template <int D, int kWaves>
+__device__ __forceinline__ bool self_plan_item(const ContextArgs& a, int hgroups, int lane, int i, i32x4& d0,
+                                               i32x4& d1) {
+  constexpr int kCtxWaves = kWaves;
+  // the plan from the rows' lengths (every wavefront lays out the same plan), then this
+  // workgroup's item, as context_plan would have written it
+  const int lt = 5 + __builtin_ctz(static_cast<unsigned>(kCtxWaves / a.heads_per_wg));  // log2 tokens per tile
+  const int hb = a.hk * hgroups;
+  const PlanShape shape{a.plan_rows, a.plan_gy, lt, hb, a.heads_per_wg, a.hq, D};
+  const PlanRow r = plan_row(a.cu_seqlens_q, a.seq_lens, a.plan_rows, a.plan_gy, lt, a.plan_cap, lane);
+  const SelfPlan pl = self_plan(r, shape, a.plan_cus, a.plan_resident, a.plan_item_cap, a.plan_entry_cap, lane);
+  if (pl.splits == 1) {
+    // the grid launch's workgroup i
+    if (i >= pl.grid_items) return false;
+    const int per_row = a.plan_gy * hb;
+    const int grid_row = i / per_row, rem = i - grid_row * per_row;
+    const int y = rem / hb, block = rem - y * hb;
+    d0 = i32x4{lane_i(r.q0, grid_row), lane_i(r.q_len, grid_row), lane_i(r.kv, grid_row), grid_row | (1 << 24)};
+    d1 = i32x4{(a.plan_gy - 1 - y) | (block << 16), 0, INT32_MAX, -1};
+  } else {
+    // the row holding item i (items in row order; a row's units in order of reach, longest first:
+    // its split units, each a key range per head block times its ranges, then the rest, one item
+    // per head block each), counting only the rows before it
+    const float rp = 1.0f / static_cast<float>(pl.per);
+    int rl = -1, off = i, su = 0, split_here = 0;
+    for (uint64_t b = pl.live; b != 0; b &= b - 1) {
+      const int q = __builtin_ctzll(b);
+      const int shift = lane_i(r.shift, q), q_len = lane_i(r.q_len, q), tiles = lane_i(r.tiles, q);
+      const int sp = tiles_over(shift, q_len, tiles, lt, pl.per);
+      const int ni = row_ranges(shift, q_len, tiles, lt, pl.per, rp, sp) * hb;
+      if (off < ni) {
+        rl = q;
+        split_here = sp;
+        break;
+      }
+      off -= ni;
+      su += sp;
+    }
+    if (rl < 0) return false;  // past the plan's items
+    const int shift = lane_i(r.shift, rl), q_len = lane_i(r.q_len, rl), tiles = lane_i(r.tiles, rl);
+    int tile = -1, used = 1, nt = 0;
+    for (int u = 0; u < split_here; ++u) {
+      const int t = tiles - 1 - u;
+      nt = tile_key_tiles(shift, q_len, lt, t);
+      used = ceil_div_small(nt, pl.per, rp);
+      if (off < used * hb) {
+        tile = t;
+        break;
+      }
+      off -= used * hb;
+      ++su;
+    }
+    if (tile < 0) {
+      const int u = off / hb;
+      tile = tiles - 1 - split_here - u;
+      off -= u * hb;
+      nt = tile_key_tiles(shift, q_len, lt, tile);
+      used = 1;
+    }
+    const int range = off / hb, block = off - range * hb;
+    const int len = used > 1 ? pl.per : nt, first = range * len;
+    d0 = i32x4{lane_i(r.q0, rl), q_len, lane_i(r.kv, rl), rl | (range << 16) | (pl.splits << 24)};
+    d1 = i32x4{tile | (block << 16), first, min(nt, first + len), used > 1 ? su * hb + block : -1};
+  }
+  return true;
+}
+
 // kWork: how workgroups map to work (each a separate instance, so that the one-kernel instances
 // keep their code).
 template <int D, int kPages, int kWaves, int kWork>
 __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextArgs a) {
   constexpr bool kSplit = kWork == kWorkSplit;
-  constexpr bool kPlan = kWork == kWorkPlan;
+  constexpr bool kPlan = kWork == kWorkPlan || kWork == kWorkSelfPlan;  // items from a plan
   constexpr int kCtxWaves = kWaves;
   constexpr int kCtxThreads = 64 * kWaves;
   constexpr int KS = D / 16;            // MFMA k-steps over the head dim (S^T)
@@ -215,7 +472,30 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   // are read from the plan; workgroups past the plan's count exit (the item array holds one slot
   // per workgroup of the grid, so the load stays inside it).
   i32x4 d0{}, d1{};
-  if constexpr (kPlan) {
+  if constexpr (kWork == kWorkSelfPlan) {
+    // wavefront 0 lays the plan out and hands the item to the others through LDS: the plan's uniform
+    // arithmetic runs on the CU's one scalar unit, which every wavefront on the CU shares
+    __shared__ i32x4 item_lds[2];
+    __shared__ int item_ok;
+    if (wave == 0) {
+      i32x4 e0{}, e1{};
+      const bool ok = self_plan_item<D, kWaves>(a, hgroups, lane, static_cast<int>(blockIdx.x), e0, e1);
+      if (lane == 0) {
+        item_ok = ok ? 1 : 0;
+        item_lds[0] = e0;
+        item_lds[1] = e1;
+      }
+    }
+    __syncthreads();
+    if (item_ok == 0) return;  // uniform over the workgroup
+    d0 = item_lds[0];
+    d1 = item_lds[1];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      d0[e] = __builtin_amdgcn_readfirstlane(d0[e]);
+      d1[e] = __builtin_amdgcn_readfirstlane(d1[e]);
+    }
+  } else if constexpr (kPlan) {
     const int n_items = a.plan_hdr[0], plan_splits = a.plan_hdr[2];
     const unsigned per_row = static_cast<unsigned>(a.plan_gy) * (a.hk * hgroups);
     const unsigned grid_row = blockIdx.x / per_row, rem = blockIdx.x - grid_row * per_row;
@@ -764,6 +1044,74 @@ __global__ __launch_bounds__(64 * kMergeWaves) void context_combine_plan(Context
   }
 }
 
+// The merge of a self-planned launch: lays out the same plan from the rows' lengths, then merges its
+// split units' (token, query head) pairs, one per wavefront in turn (the split units of a row are
+// its first units: the token tiles of longest reach). Also reports the rows' length errors, as
+// context_plan does for planned launches.
+template <int D>
+__global__ __launch_bounds__(64 * kMergeWaves) void context_combine_self_plan(ContextArgs a, int tokens_per_wg) {
+  const int lane = threadIdx.x & 63;
+  const int hgroups = (a.group + a.heads_per_wg - 1) / a.heads_per_wg;
+  const int hb = a.hk * hgroups;
+  const int lt = __builtin_ctz(static_cast<unsigned>(tokens_per_wg));
+  const PlanShape shape{a.plan_rows, a.plan_gy, lt, hb, a.heads_per_wg, a.hq, D};
+  const PlanRow r = plan_row(a.cu_seqlens_q, a.seq_lens, a.plan_rows, a.plan_gy, lt, a.plan_cap, lane);
+  // wavefront 0 makes the split decision and hands it to the others through LDS (its uniform
+  // arithmetic runs on the CU's one scalar unit, shared by every wavefront on the CU)
+  __shared__ int plan_lds[4];
+  if (wave_id_uniform() == 0) {
+    if (blockIdx.x == 0 && __ballot(r.bad) != 0 && lane == 0) report(a.err, MAS_ERRBIT_POSITION);
+    const SelfPlan own = self_plan(r, shape, a.plan_cus, a.plan_resident, a.plan_item_cap, a.plan_entry_cap, lane);
+    if (lane == 0) {
+      plan_lds[0] = own.splits;
+      plan_lds[1] = own.per;
+      plan_lds[2] = static_cast<int>(own.live);
+      plan_lds[3] = static_cast<int>(own.live >> 32);
+    }
+  }
+  __syncthreads();
+  SelfPlan pl{};
+  pl.splits = __builtin_amdgcn_readfirstlane(plan_lds[0]);
+  pl.per = __builtin_amdgcn_readfirstlane(plan_lds[1]);
+  pl.live = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(plan_lds[2])) |
+            (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(plan_lds[3]))) << 32);
+  if (pl.splits == 1) return;
+  // split units, per row and in all (a row's split units are its token tiles reaching more than per)
+  int split_units = 0, row_units = 0;
+  for (uint64_t b = pl.live; b != 0; b &= b - 1) {
+    const int q = __builtin_ctzll(b);
+    const int sp = tiles_over(lane_i(r.shift, q), lane_i(r.q_len, q), lane_i(r.tiles, q), lt, pl.per);
+    row_units = lane == q ? sp : row_units;
+    split_units += sp;
+  }
+  const int per_unit = tokens_per_wg * a.hq;  // pairs per split unit; split units * per_unit <= 2^31 - 1 (host-checked)
+  const int total = split_units * per_unit;
+  const float rp = 1.0f / static_cast<float>(pl.per);
+  const int waves = static_cast<int>(gridDim.x) * kMergeWaves;
+  for (int m = static_cast<int>(blockIdx.x) * kMergeWaves + wave_id_uniform(); m < total; m += waves) {
+    const int su = m / per_unit, rem = m - su * per_unit;
+    const int j = rem / a.hq, h = rem - j * a.hq;  // token of the unit's tile, query head
+    // the row holding split unit su (split units in row order; a row's are its last token tiles)
+    int rl = 0, k = su;
+    for (uint64_t b = pl.live; b != 0; b &= b - 1) {
+      rl = __builtin_ctzll(b);
+      const int nu = lane_i(row_units, rl);
+      if (k < nu) break;
+      k -= nu;
+    }
+    const int q_len = lane_i(r.q_len, rl);
+    const int tile = lane_i(r.tiles, rl) - 1 - k;
+    const int t = (tile << lt) + j;
+    if (t >= q_len) continue;
+    const int nt = tile_key_tiles(lane_i(r.shift, rl), q_len, lt, tile);
+    const int nsplit = ceil_div_small(nt, pl.per, rp);
+    const int kvh = h / a.group, g = h - kvh * a.group, hg = g / a.heads_per_wg, hs = g - hg * a.heads_per_wg;
+    const int slot = su * hb + kvh * hgroups + hg;
+    const int64_t base = ((static_cast<int64_t>(slot) * tokens_per_wg + j) * a.heads_per_wg + hs) * pl.splits;
+    merge_partials<D>(a, base, nsplit, lane_i(r.q0, rl) + t, h, lane);
+  }
+}
+
 // ---- the planner of planned launches ----------------------------------------------------------
 
 struct PlanArgs {
@@ -823,46 +1171,6 @@ __device__ int plan_max(int x, int* slots) {
 #pragma unroll
   for (int w = 1; w < kPlanThreads / 64; ++w) m = max(m, slots[w]);
   return m;
-}
-
-// The planner's estimate (SplitModel's terms, with the real lengths): split k ways, the longest
-// unit is cut into ranges of per = max(4, ceil(longest / k)) key tiles and so is every unit longer
-// than per; the rest stay whole. Its time is that of a workgroup of per tiles, (per + 4.8) x 1.8 us
-// with at most one workgroup per CU, else x 2.1 us per round of resident workgroups, plus, split,
-// 5 us (the merge's launch and the planner's item writes, 3 us more than an unsplit plan's on
-// MI355X) and the merge: the partials' bytes at 5 TB/s or 0.9 ns per (token, head) pair of the
-// split units, whichever is longer (the planned merge takes its pairs in turn on a fixed grid:
-// 12,288 pairs in 9.6-11 us, against 0.6 ns per pair for the grid launch's merge, which has a
-// wavefront per pair).
-struct PlanModel {
-  int units, head_blocks, longest;
-  int cus, resident;
-  int item_cap;           // workgroups of the main grid
-  int64_t entry_cap;      // partial entries the workspace holds
-  int entries_per_unit;   // partial entries of a split unit per split (head blocks x tokens x heads)
-  float pair_us;          // merge microseconds per split unit (its (token, head) pairs)
-  float entry_us;         // microseconds per partial entry moved at 5 TB/s
-};
-
-__device__ float plan_time(const PlanModel& m, int wgs, int per) {
-  const float per_wg = static_cast<float>(per) + 4.8f;
-  return wgs <= m.cus ? per_wg * 1.8f : static_cast<float>((wgs + m.resident - 1) / m.resident) * per_wg * 2.1f;
-}
-
-// Whether no split can pay for units reaching at most `longest` key tiles: the unsplit estimate,
-// at most one workgroup per CU (else no split is weighed), against the least any split costs (a
-// split length of 4 tiles in one round, plus the fixed 5 us).
-__device__ bool plan_never_splits(int longest) {
-  return 0.8f * ((static_cast<float>(longest) + 4.8f) * 1.8f) <= (4.f + 4.8f) * 1.8f + 5.0f;
-}
-
-// The split length for k splits, or 0 where k is not weighed (the same split as a smaller count,
-// or more splits than kMaxCtxSplits).
-__device__ int plan_per(const PlanModel& m, int k) {
-  if (k > kMaxCtxSplits) return 0;
-  const int tiles = (m.longest + k - 1) / k;
-  if ((m.longest + tiles - 1) / tiles != k) return 0;
-  return max(4, tiles);
 }
 
 // The estimate for k > 1 splits (infinite if the grid or the workspace would not hold them); the
@@ -1150,7 +1458,7 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   const int64_t base_wgs = gx * gy * num_rows;
   bool planned = false;
   PlanLayout plan{};
-  int64_t plan_entries = 0;
+  int64_t plan_entries = 0, self_entries = 0;
   int cus = 0;
   int64_t resident = 0;
   if (workspace != nullptr && workspace_bytes > 0 && (reinterpret_cast<uintptr_t>(workspace) & 15u) == 0) {
@@ -1172,8 +1480,11 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
     } else if (base_wgs >= cus && num_rows >= kPlanMinRows && num_rows <= kPlanMaxRows && units_bound <= kPlanMaxUnits &&
                row_tokens <= kPlanMaxTokens && gx <= 32767 && units_bound * tokens_per_wg * num_q_heads <= INT32_MAX) {
       plan = plan_layout(units_bound, gx, resident);
-      if (workspace_bytes > plan.partial_off) {
-        plan_entries = (workspace_bytes - plan.partial_off) / entry_bytes;
+      // a self-planned launch (up to kSelfPlanMaxRows rows) keeps no plan in the workspace: all of it
+      // holds partials
+      self_entries = workspace_bytes / entry_bytes;
+      if (num_rows <= kSelfPlanMaxRows || workspace_bytes > plan.partial_off) {
+        plan_entries = num_rows <= kSelfPlanMaxRows ? self_entries : (workspace_bytes - plan.partial_off) / entry_bytes;
         SplitModel m{};
         m.base = gx;
         m.cus = cus;
@@ -1229,6 +1540,31 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
                    : 2 * page_size >= pos_step ? kPagesStep
                                                : kPagesLane;
   const dim3 block(static_cast<uint32_t>(64 * waves));
+  if (planned && num_rows <= kSelfPlanMaxRows) {
+    // every workgroup lays the plan out itself: no planner launch, partials from the workspace's start
+    a.plan_rows = static_cast<int>(num_rows);
+    a.plan_gy = static_cast<int>(gy);
+    a.plan_cus = cus;
+    a.plan_resident = static_cast<int>(resident);
+    a.plan_item_cap = plan.item_cap;
+    a.plan_entry_cap = self_entries;
+    a.plan_cap = cap;
+    a.part_o = static_cast<float*>(workspace);
+    a.part_ml = a.part_o + self_entries * head_dim;
+    launch_context<kWorkSelfPlan>(head_dim, waves, mode, dim3(static_cast<uint32_t>(plan.item_cap)), block, stream, a);
+    if (const int st = launch_status(); st != MAS_OK) return st;
+    const int64_t pairs = units_bound * tokens_per_wg * num_q_heads;
+    const dim3 merge_grid(
+        static_cast<uint32_t>(std::min<int64_t>(cdiv(pairs, kMergeWaves), 24 * static_cast<int64_t>(cus) / kMergeWaves)));
+    const dim3 merge_block(64 * kMergeWaves);
+    if (head_dim == 64)
+      hipLaunchKernelGGL(context_combine_self_plan<64>, merge_grid, merge_block, 0, stream, a,
+                         static_cast<int>(tokens_per_wg));
+    else
+      hipLaunchKernelGGL(context_combine_self_plan<128>, merge_grid, merge_block, 0, stream, a,
+                         static_cast<int>(tokens_per_wg));
+    return launch_status();
+  }
   if (planned) {
     uint8_t* ws = static_cast<uint8_t*>(workspace);
     PlanArgs pa{};

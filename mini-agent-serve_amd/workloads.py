@@ -313,6 +313,8 @@ CONTEXT_SHAPES: dict[str, ContextShape] = {s.name: s for s in [
     ContextShape("context_attn_graph_1x100_after4000_123b", 1, 100, 4000, 96, 8, 128, 16, graph_rows=17,
                  reach=8192),
     ContextShape("context_attn_graph_3x100_after2000_24b", 3, 100, 2000, 32, 8, 128, 16, graph_rows=17, reach=8192),
+    # a graph step where no split pays (a fresh prompt): the planned launch against the one-kernel grid
+    ContextShape("context_attn_graph_1x120_after0_24b", 1, 120, 0, 32, 8, 128, 16, graph_rows=17, reach=8192),
 ]}
 
 

@@ -96,6 +96,28 @@ def test_planned_context_attention_matches_oracle(mas, dev, prompts, pad, hq, hk
     _check(bits(out), want, min_exact=0.0)
 
 
+@pytest.mark.parametrize("case", [0, 2, 3, 4, 6])
+def test_self_planned_launch_equals_the_planner_launch(mas, dev, case):
+    """A step of up to 64 rows lays its plan out in the kernels themselves (no planner launch); with
+    more rows the planner launch writes it. From the same real rows both lay out the same plan, so
+    the outputs match bit for bit: 17 rows against the same prompts padded to 70 rows (cases whose
+    split counts stay within both grids, so the grid size does not change the plan)."""
+    prompts, pad, hq, hk, dim, ps = PLANNED_CASES[case]
+    seed = sum(n for n, _ in prompts) + hq + ps
+    q, kc, vc, tables, seq, cu, max_q = _graph_case(seed, prompts, pad, hq, hk, dim, ps)
+    q70, kc70, vc70, tables70, seq70, cu70, max_q70 = _graph_case(seed, prompts, pad, hq, hk, dim, ps, rows=70)
+    assert torch.equal(q, q70) and torch.equal(kc, kc70) and max_q == max_q70
+    reach = tables.shape[1] * ps
+    scale = dim ** -0.5
+    flags, flags70 = (torch.zeros(1, dtype=torch.int32, device=dev) for _ in range(2))
+    out = _call(mas, dev, q, kc, vc, tables, seq, cu, max_q, reach, scale, flags=flags)
+    out70 = _call(mas, dev, q70, kc70, vc70, tables70, seq70, cu70, max_q70, reach, scale, flags=flags70)
+    assert int(flags.item()) == 0 and int(flags70.item()) == 0
+    assert torch.equal(out, out70)
+    one_kernel = _call(mas, dev, q, kc, vc, tables, seq, cu, max_q, reach, scale, ws_bytes=16)
+    assert not torch.equal(out, one_kernel)  # the plan split the long rows
+
+
 def test_planned_context_attention_short_rows_equal_one_kernel(mas, dev):
     """A step of short prompts: the plan splits nothing and its items are the one-kernel grid's
     workgroups, so the output is the one-kernel output bit for bit."""
