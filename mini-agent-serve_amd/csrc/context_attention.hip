@@ -45,7 +45,8 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 //                the device (a graph captured with padded rows and token counts: the host only knows
 //                bounds, so the split decision waits for the lengths);
 //   kWorkSelfPlan - the same plan, laid out by each workgroup itself from the rows' lengths (at most
-//                64 rows: one per lane), with no planner launch.
+//                64 rows: one per lane), with no planner launch; the workgroups write the split
+//                units the merge reads.
 constexpr int kWorkGrid = 0, kWorkSplit = 1, kWorkPlan = 2, kWorkSelfPlan = 3;
 constexpr int kSelfPlanMaxRows = 64;
 
@@ -84,9 +85,10 @@ struct ContextArgs {
   // first key tile, end key tile, partial slot or -1}) and its split units ({q0, q_len, kv_len, row},
   // {first token, splits used, splits, first partial slot}). Partials of slot s: (token of the
   // tile, head of the block, split) entries at ((s * tokens + token) * heads + head) * splits + split.
-  const int* plan_hdr;
+  // A self-planned launch (kWorkSelfPlan) writes plan_hdr[1] and the split units itself.
+  int* plan_hdr;
   const i32x4* plan_items;
-  const i32x4* plan_units;
+  i32x4* plan_units;
   int plan_rows, plan_gy;  // the rows and token tiles per row of the unsplit grid
   // kWorkSelfPlan: what the plan's estimate needs (CUs, resident workgroups, the grid's workgroups,
   // the partial entries the workspace holds) and the block table's reach
@@ -290,14 +292,6 @@ __device__ __forceinline__ int ceil_div_small(int a, int b, float rb) {
   return q;
 }
 
-// Key ranges of a row's token tiles under a split of length per (rp = 1 / per): one per tile, and
-// ceil(key tiles / per) for each of its `split` last tiles.
-__device__ __forceinline__ int row_ranges(int shift, int q_len, int tiles, int lt, int per, float rp, int split) {
-  int ranges = tiles - split;
-  for (int t = tiles - split; t < tiles; ++t) ranges += ceil_div_small(tile_key_tiles(shift, q_len, lt, t), per, rp);
-  return ranges;
-}
-
 __device__ __forceinline__ int lane_i(int x, int l) { return __builtin_amdgcn_readlane(x, l); }
 
 // Minimum over the 64 lanes: DPP within rows of 16, then the four rows' minima.
@@ -373,72 +367,95 @@ __device__ SelfPlan self_plan(const PlanRow& r, const PlanShape& s, int cus, int
   return pl;
 }
 
-// A self-planned launch's workgroup: lays out the plan from the rows' lengths (every wavefront lays
-// out the same plan), then finds workgroup `i`'s item, as context_plan would have written it (the
-// layout of ContextArgs::plan_items). Returns false for a workgroup past the plan's items.
+// Sum over the 64 lanes (|sum| < 2^31): DPP within rows of 16, then the four rows' sums.
+__device__ __forceinline__ int wave_sum_i(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xb1, 0xf, 0xf, false);   // quad_perm [1,0,3,2]
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4e, 0xf, 0xf, false);   // quad_perm [2,3,0,1]
+  v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false);  // row_half_mirror
+  v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xf, 0xf, false);  // row_mirror
+  return lane_i(v, 0) + lane_i(v, 16) + lane_i(v, 32) + lane_i(v, 48);
+}
+
+// A self-planned launch's workgroup (run by one wavefront): lays out the plan from the rows'
+// lengths and finds workgroup `i`'s item in the layout of ContextArgs::plan_items. Items are in row
+// order, a row's token tiles longest reach first, each tile's key ranges times the head blocks
+// (head block fastest); a split plan's split units are a row's first tiles. An unsplit plan is the
+// grid launch's work without its empty workgroups. Workgroup 0 also reports the rows' length errors
+// and writes the split-unit count to plan_hdr[1]; the workgroup of each split unit's first range and
+// head block writes the unit's plan_units entry: what context_plan writes for the merge. Returns
+// false for a workgroup past the plan's items.
 template <int D, int kWaves>
 __device__ __forceinline__ bool self_plan_item(const ContextArgs& a, int hgroups, int lane, int i, i32x4& d0,
                                                i32x4& d1) {
-  constexpr int kCtxWaves = kWaves;
-  // the plan from the rows' lengths (every wavefront lays out the same plan), then this
-  // workgroup's item, as context_plan would have written it
-  const int lt = 5 + __builtin_ctz(static_cast<unsigned>(kCtxWaves / a.heads_per_wg));  // log2 tokens per tile
+  const int lt = 5 + __builtin_ctz(static_cast<unsigned>(kWaves / a.heads_per_wg));  // log2 tokens per tile
   const int hb = a.hk * hgroups;
   const PlanShape shape{a.plan_rows, a.plan_gy, lt, hb, a.heads_per_wg, a.hq, D};
   const PlanRow r = plan_row(a.cu_seqlens_q, a.seq_lens, a.plan_rows, a.plan_gy, lt, a.plan_cap, lane);
+  if (i == 0 && __ballot(r.bad) != 0 && lane == 0) report(a.err, MAS_ERRBIT_POSITION);
+  // No plan has more items than every token tile cut into ranges of 4 key tiles (the shortest
+  // split) per head block: workgroups past that bound leave before the plan is laid out. A row's
+  // last tile reaches the most key tiles. Clamped to the grid (item_cap < 2^24, host-checked).
+  int64_t cut = 0;
+  if (r.tiles > 0)
+    cut = static_cast<int64_t>(r.tiles) * max(1, (tile_key_tiles(r.shift, r.q_len, lt, r.tiles - 1) + 3) >> 2) * hb;
+  const int bound = wave_sum_i(static_cast<int>(min(cut, a.plan_item_cap)));
+  if (i >= bound) {
+    if (i == 0 && lane == 0) a.plan_hdr[1] = 0;  // no query tokens
+    return false;
+  }
   const SelfPlan pl = self_plan(r, shape, a.plan_cus, a.plan_resident, a.plan_item_cap, a.plan_entry_cap, lane);
-  if (pl.splits == 1) {
-    // the grid launch's workgroup i
-    if (i >= pl.grid_items) return false;
-    const int per_row = a.plan_gy * hb;
-    const int grid_row = i / per_row, rem = i - grid_row * per_row;
-    const int y = rem / hb, block = rem - y * hb;
-    d0 = i32x4{lane_i(r.q0, grid_row), lane_i(r.q_len, grid_row), lane_i(r.kv, grid_row), grid_row | (1 << 24)};
-    d1 = i32x4{(a.plan_gy - 1 - y) | (block << 16), 0, INT32_MAX, -1};
+  const int per = pl.splits > 1 ? pl.per : (1 << 30);  // unsplit: no tile reaches past per
+  const float rp = 1.0f / static_cast<float>(per);
+  // each row's split tiles (its last ones) and key ranges, a row per lane
+  const int sp_l = tiles_over(r.shift, r.q_len, r.tiles, lt, per);
+  int rng_l = r.tiles - sp_l;
+  for (int t = r.tiles - sp_l; t < r.tiles; ++t) rng_l += ceil_div_small(tile_key_tiles(r.shift, r.q_len, lt, t), per, rp);
+  if (i == 0) {
+    const int split_units = wave_sum_i(sp_l);
+    if (lane == 0) a.plan_hdr[1] = split_units;
+  }
+  // the row holding item i and the split units of the rows before it
+  int rl = -1, off = i, su = 0;
+  for (uint64_t b = pl.live; b != 0; b &= b - 1) {
+    const int q = __builtin_ctzll(b);
+    const int ni = lane_i(rng_l, q) * hb;
+    if (off < ni) {
+      rl = q;
+      break;
+    }
+    off -= ni;
+    su += lane_i(sp_l, q);
+  }
+  if (rl < 0) return false;  // past the plan's items
+  const int shift = lane_i(r.shift, rl), q_len = lane_i(r.q_len, rl), tiles = lane_i(r.tiles, rl);
+  const int split_here = lane_i(sp_l, rl);
+  // the row's split units, one per lane (lane u: tile tiles - 1 - u): their key ranges
+  const int used_l = lane < split_here ? ceil_div_small(tile_key_tiles(shift, q_len, lt, tiles - 1 - lane), per, rp) : 1;
+  int k = 0;
+  for (; k < split_here; ++k) {
+    const int nk = lane_i(used_l, k) * hb;
+    if (off < nk) break;
+    off -= nk;
+  }
+  int tile, used = 1;
+  if (k < split_here) {
+    tile = tiles - 1 - k;
+    used = lane_i(used_l, k);
+    su += k;
   } else {
-    // the row holding item i (items in row order; a row's units in order of reach, longest first:
-    // its split units, each a key range per head block times its ranges, then the rest, one item
-    // per head block each), counting only the rows before it
-    const float rp = 1.0f / static_cast<float>(pl.per);
-    int rl = -1, off = i, su = 0, split_here = 0;
-    for (uint64_t b = pl.live; b != 0; b &= b - 1) {
-      const int q = __builtin_ctzll(b);
-      const int shift = lane_i(r.shift, q), q_len = lane_i(r.q_len, q), tiles = lane_i(r.tiles, q);
-      const int sp = tiles_over(shift, q_len, tiles, lt, pl.per);
-      const int ni = row_ranges(shift, q_len, tiles, lt, pl.per, rp, sp) * hb;
-      if (off < ni) {
-        rl = q;
-        split_here = sp;
-        break;
-      }
-      off -= ni;
-      su += sp;
-    }
-    if (rl < 0) return false;  // past the plan's items
-    const int shift = lane_i(r.shift, rl), q_len = lane_i(r.q_len, rl), tiles = lane_i(r.tiles, rl);
-    int tile = -1, used = 1, nt = 0;
-    for (int u = 0; u < split_here; ++u) {
-      const int t = tiles - 1 - u;
-      nt = tile_key_tiles(shift, q_len, lt, t);
-      used = ceil_div_small(nt, pl.per, rp);
-      if (off < used * hb) {
-        tile = t;
-        break;
-      }
-      off -= used * hb;
-      ++su;
-    }
-    if (tile < 0) {
-      const int u = off / hb;
-      tile = tiles - 1 - split_here - u;
-      off -= u * hb;
-      nt = tile_key_tiles(shift, q_len, lt, tile);
-      used = 1;
-    }
-    const int range = off / hb, block = off - range * hb;
-    const int len = used > 1 ? pl.per : nt, first = range * len;
-    d0 = i32x4{lane_i(r.q0, rl), q_len, lane_i(r.kv, rl), rl | (range << 16) | (pl.splits << 24)};
-    d1 = i32x4{tile | (block << 16), first, min(nt, first + len), used > 1 ? su * hb + block : -1};
+    const int u = off / hb;  // an unsplit tile: one item per head block
+    tile = tiles - 1 - split_here - u;
+    off -= u * hb;
+  }
+  const int nt = tile_key_tiles(shift, q_len, lt, tile);
+  const int range = off / hb, block = off - range * hb;
+  const int len = used > 1 ? per : nt, first = range * len;
+  const int q0 = lane_i(r.q0, rl), kv = lane_i(r.kv, rl);
+  d0 = i32x4{q0, q_len, kv, rl | (range << 16) | (pl.splits << 24)};
+  d1 = i32x4{tile | (block << 16), first, min(nt, first + len), used > 1 ? su * hb + block : -1};
+  if (used > 1 && range == 0 && block == 0 && lane == 0) {
+    a.plan_units[2 * su] = i32x4{q0, q_len, kv, rl};
+    a.plan_units[2 * su + 1] = i32x4{tile << lt, used, pl.splits, su * hb};
   }
   return true;
 }
@@ -1044,74 +1061,6 @@ __global__ __launch_bounds__(64 * kMergeWaves) void context_combine_plan(Context
   }
 }
 
-// The merge of a self-planned launch: lays out the same plan from the rows' lengths, then merges its
-// split units' (token, query head) pairs, one per wavefront in turn (the split units of a row are
-// its first units: the token tiles of longest reach). Also reports the rows' length errors, as
-// context_plan does for planned launches.
-template <int D>
-__global__ __launch_bounds__(64 * kMergeWaves) void context_combine_self_plan(ContextArgs a, int tokens_per_wg) {
-  const int lane = threadIdx.x & 63;
-  const int hgroups = (a.group + a.heads_per_wg - 1) / a.heads_per_wg;
-  const int hb = a.hk * hgroups;
-  const int lt = __builtin_ctz(static_cast<unsigned>(tokens_per_wg));
-  const PlanShape shape{a.plan_rows, a.plan_gy, lt, hb, a.heads_per_wg, a.hq, D};
-  const PlanRow r = plan_row(a.cu_seqlens_q, a.seq_lens, a.plan_rows, a.plan_gy, lt, a.plan_cap, lane);
-  // wavefront 0 makes the split decision and hands it to the others through LDS (its uniform
-  // arithmetic runs on the CU's one scalar unit, shared by every wavefront on the CU)
-  __shared__ int plan_lds[4];
-  if (wave_id_uniform() == 0) {
-    if (blockIdx.x == 0 && __ballot(r.bad) != 0 && lane == 0) report(a.err, MAS_ERRBIT_POSITION);
-    const SelfPlan own = self_plan(r, shape, a.plan_cus, a.plan_resident, a.plan_item_cap, a.plan_entry_cap, lane);
-    if (lane == 0) {
-      plan_lds[0] = own.splits;
-      plan_lds[1] = own.per;
-      plan_lds[2] = static_cast<int>(own.live);
-      plan_lds[3] = static_cast<int>(own.live >> 32);
-    }
-  }
-  __syncthreads();
-  SelfPlan pl{};
-  pl.splits = __builtin_amdgcn_readfirstlane(plan_lds[0]);
-  pl.per = __builtin_amdgcn_readfirstlane(plan_lds[1]);
-  pl.live = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(plan_lds[2])) |
-            (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(plan_lds[3]))) << 32);
-  if (pl.splits == 1) return;
-  // split units, per row and in all (a row's split units are its token tiles reaching more than per)
-  int split_units = 0, row_units = 0;
-  for (uint64_t b = pl.live; b != 0; b &= b - 1) {
-    const int q = __builtin_ctzll(b);
-    const int sp = tiles_over(lane_i(r.shift, q), lane_i(r.q_len, q), lane_i(r.tiles, q), lt, pl.per);
-    row_units = lane == q ? sp : row_units;
-    split_units += sp;
-  }
-  const int per_unit = tokens_per_wg * a.hq;  // pairs per split unit; split units * per_unit <= 2^31 - 1 (host-checked)
-  const int total = split_units * per_unit;
-  const float rp = 1.0f / static_cast<float>(pl.per);
-  const int waves = static_cast<int>(gridDim.x) * kMergeWaves;
-  for (int m = static_cast<int>(blockIdx.x) * kMergeWaves + wave_id_uniform(); m < total; m += waves) {
-    const int su = m / per_unit, rem = m - su * per_unit;
-    const int j = rem / a.hq, h = rem - j * a.hq;  // token of the unit's tile, query head
-    // the row holding split unit su (split units in row order; a row's are its last token tiles)
-    int rl = 0, k = su;
-    for (uint64_t b = pl.live; b != 0; b &= b - 1) {
-      rl = __builtin_ctzll(b);
-      const int nu = lane_i(row_units, rl);
-      if (k < nu) break;
-      k -= nu;
-    }
-    const int q_len = lane_i(r.q_len, rl);
-    const int tile = lane_i(r.tiles, rl) - 1 - k;
-    const int t = (tile << lt) + j;
-    if (t >= q_len) continue;
-    const int nt = tile_key_tiles(lane_i(r.shift, rl), q_len, lt, tile);
-    const int nsplit = ceil_div_small(nt, pl.per, rp);
-    const int kvh = h / a.group, g = h - kvh * a.group, hg = g / a.heads_per_wg, hs = g - hg * a.heads_per_wg;
-    const int slot = su * hb + kvh * hgroups + hg;
-    const int64_t base = ((static_cast<int64_t>(slot) * tokens_per_wg + j) * a.heads_per_wg + hs) * pl.splits;
-    merge_partials<D>(a, base, nsplit, lane_i(r.q0, rl) + t, h, lane);
-  }
-}
-
 // ---- the planner of planned launches ----------------------------------------------------------
 
 struct PlanArgs {
@@ -1386,6 +1335,10 @@ struct PlanLayout {
   int64_t item_cap, units_bound, partial_off;
 };
 
+// A self-planned launch's workspace: the plan's counts (256 bytes), its split units (32 bytes
+// each, at most one per (row, token tile)), then the partials.
+int64_t self_plan_partial_off(int64_t units_bound) { return 256 + 32 * units_bound; }
+
 PlanLayout plan_layout(int64_t units_bound, int64_t head_blocks, int64_t resident) {
   // items: at most one per (unit, head block) unsplit; split, the estimate keeps the grid within
   // two rounds of resident workgroups (best_splits)
@@ -1458,7 +1411,8 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   const int64_t base_wgs = gx * gy * num_rows;
   bool planned = false;
   PlanLayout plan{};
-  int64_t plan_entries = 0, self_entries = 0;
+  int64_t plan_entries = 0;
+  bool self_plan = false;
   int cus = 0;
   int64_t resident = 0;
   if (workspace != nullptr && workspace_bytes > 0 && (reinterpret_cast<uintptr_t>(workspace) & 15u) == 0) {
@@ -1480,11 +1434,12 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
     } else if (base_wgs >= cus && num_rows >= kPlanMinRows && num_rows <= kPlanMaxRows && units_bound <= kPlanMaxUnits &&
                row_tokens <= kPlanMaxTokens && gx <= 32767 && units_bound * tokens_per_wg * num_q_heads <= INT32_MAX) {
       plan = plan_layout(units_bound, gx, resident);
-      // a self-planned launch (up to kSelfPlanMaxRows rows) keeps no plan in the workspace: all of it
-      // holds partials
-      self_entries = workspace_bytes / entry_bytes;
-      if (num_rows <= kSelfPlanMaxRows || workspace_bytes > plan.partial_off) {
-        plan_entries = num_rows <= kSelfPlanMaxRows ? self_entries : (workspace_bytes - plan.partial_off) / entry_bytes;
+      // a self-planned launch (up to kSelfPlanMaxRows rows) keeps only the plan's counts and split
+      // units in the workspace, no items
+      self_plan = num_rows <= kSelfPlanMaxRows && plan.item_cap < (int64_t{1} << 24);
+      const int64_t plan_off = self_plan ? self_plan_partial_off(units_bound) : plan.partial_off;
+      if (workspace_bytes > plan_off) {
+        plan_entries = (workspace_bytes - plan_off) / entry_bytes;
         SplitModel m{};
         m.base = gx;
         m.cus = cus;
@@ -1540,32 +1495,24 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
                    : 2 * page_size >= pos_step ? kPagesStep
                                                : kPagesLane;
   const dim3 block(static_cast<uint32_t>(64 * waves));
-  if (planned && num_rows <= kSelfPlanMaxRows) {
-    // every workgroup lays the plan out itself: no planner launch, partials from the workspace's start
+  if (planned && self_plan) {
+    // every workgroup lays the plan out itself (no planner launch) and writes what the merge reads:
+    // the plan's counts, then its split units, then the partials
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    a.plan_hdr = reinterpret_cast<int*>(ws);
+    a.plan_units = reinterpret_cast<i32x4*>(ws + 256);
     a.plan_rows = static_cast<int>(num_rows);
     a.plan_gy = static_cast<int>(gy);
     a.plan_cus = cus;
     a.plan_resident = static_cast<int>(resident);
     a.plan_item_cap = plan.item_cap;
-    a.plan_entry_cap = self_entries;
+    a.plan_entry_cap = plan_entries;
     a.plan_cap = cap;
-    a.part_o = static_cast<float*>(workspace);
-    a.part_ml = a.part_o + self_entries * head_dim;
+    a.part_o = reinterpret_cast<float*>(ws + self_plan_partial_off(units_bound));
+    a.part_ml = a.part_o + plan_entries * head_dim;
     launch_context<kWorkSelfPlan>(head_dim, waves, mode, dim3(static_cast<uint32_t>(plan.item_cap)), block, stream, a);
     if (const int st = launch_status(); st != MAS_OK) return st;
-    const int64_t pairs = units_bound * tokens_per_wg * num_q_heads;
-    const dim3 merge_grid(
-        static_cast<uint32_t>(std::min<int64_t>(cdiv(pairs, kMergeWaves), 24 * static_cast<int64_t>(cus) / kMergeWaves)));
-    const dim3 merge_block(64 * kMergeWaves);
-    if (head_dim == 64)
-      hipLaunchKernelGGL(context_combine_self_plan<64>, merge_grid, merge_block, 0, stream, a,
-                         static_cast<int>(tokens_per_wg));
-    else
-      hipLaunchKernelGGL(context_combine_self_plan<128>, merge_grid, merge_block, 0, stream, a,
-                         static_cast<int>(tokens_per_wg));
-    return launch_status();
-  }
-  if (planned) {
+  } else if (planned) {
     uint8_t* ws = static_cast<uint8_t*>(workspace);
     PlanArgs pa{};
     pa.cu_seqlens_q = cu_seqlens_q;
@@ -1597,6 +1544,8 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
     if (const int st = launch_status(); st != MAS_OK) return st;
     launch_context<kWorkPlan>(head_dim, waves, mode, dim3(static_cast<uint32_t>(plan.item_cap)), block, stream, a);
     if (const int st = launch_status(); st != MAS_OK) return st;
+  }
+  if (planned) {
     // each wavefront takes (token, head) pairs of the split units in turn; 24 per CU (6 per SIMD,
     // as many as the merge's registers allow: 12,288 pairs merged in 9.6 us against 11.1 with 16)
     const int64_t pairs = units_bound * tokens_per_wg * num_q_heads;
