@@ -1154,6 +1154,105 @@ def trace_probe(mas, args, shape, dev) -> None:
     print(json.dumps(out), flush=True)
 
 
+def step_credited_bytes(fs) -> dict[str, int]:
+    """Credited bytes of each kernel of a whole forward step (one launch; per layer for the layer
+    ops): every mandatory input element read once and every output written once, index arrays and
+    norm weights included, the cos/sin table and attention partials not."""
+    ls, lay = fs.shape.layer, fs.layout
+    n, d, h, i = fs.num_tokens, fs.num_decodes, ls.hidden, ls.inter
+    hq, hk, dim, ps = ls.q_heads, ls.kv_heads, ls.head_dim, fs.shape.page_size
+    lens = lay.seq_lens.long()
+    dec_pages = int(((lens[:d] + ps - 1) // ps).sum())
+    prompt_positions = sum(q + c for q, c in fs.shape.prompts)
+    prompt_tokens = sum(q for q, _ in fs.shape.prompts)
+    return {
+        "embedding": n * (4 * h + 8),
+        "norm_in": 7 * n * h + 2 * h,
+        "rope_append": n * (4 * (hq + hk) * dim + 6 * hk * dim + 8),
+        "decode_attention": (lay.decode_positions * hk * dim * 4 + d * hq * dim * 3 + dec_pages * 4 + d * 4
+                             if d else 0),
+        "context_attention": (prompt_positions * hk * dim * 4 + prompt_tokens * hq * dim * 3 + 8 * len(fs.shape.prompts)
+                              if fs.shape.prompts else 0),
+        "norm_post": 7 * n * h + 2 * h,
+        "silu": 5 * n * i,
+        "final_norm": 8 * n * h + 2 * h,
+    }
+
+
+def step_main(mas, args, shape, dev) -> int:
+    """A whole forward step (embedding, every layer's kernels with its attention, final norm) in the
+    reference's fp8 dataflow, graph-replayed; the value is credited bytes per second. Beside it, each
+    kernel's µs per launch over the step's layers (a graph of back-to-back launches, one per layer)
+    and its share of the step."""
+    fs = mas.layer_pass.ForwardStep(shape, dev, seed=0)
+    cb = step_credited_bytes(fs)
+    layer_ops = [op for op in fs.LAYER_OPS if cb[op] > 0]
+    per_step = cb["embedding"] + cb["final_norm"] + shape.layers * sum(cb[op] for op in layer_ops)
+    steps = args.steps if args.steps is not None else 10
+    warmup = args.warmup if args.warmup is not None else 2
+    fs.run()
+    torch.cuda.synchronize()
+
+    def run_range(lo, hi):
+        for _ in range(lo, hi):
+            fs.run()
+
+    if args.trace_probe == "steps":
+        timing = time_steps(run_range, steps, warmup, lead=1, per_graph=2)
+        print(json.dumps({"trace_probe": "steps", "workload": shape.name, "steps": steps,
+                          "us_per_step": round(timing["device_s"] / steps * 1e6, 3)}), flush=True)
+        return 0
+
+    def per_launch_us(fn, launches) -> float:
+        g = capture(lambda: [fn(x) for x in launches])
+        g.replay()
+        events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(5)]
+        for start, stop in events:
+            start.record()
+            g.replay()
+            stop.record()
+        torch.cuda.synchronize()
+        return 1000.0 * sorted(a.elapsed_time(b) for a, b in events)[2] / len(launches)
+
+    op_us = {op: per_launch_us(getattr(fs, "run_" + op), fs.layers) for op in layer_ops}
+    op_us["embedding"] = per_launch_us(lambda _: fs.run_embedding(), range(shape.layers))
+    op_us["final_norm"] = per_launch_us(lambda _: fs.run_final_norm(), range(shape.layers))
+    if args.trace_probe == "ops":
+        print(json.dumps({"trace_probe": "ops", "workload": shape.name, "launches_per_graph": shape.layers,
+                          "event_us": {k: round(v, 3) for k, v in op_us.items()}}), flush=True)
+        return 0
+    timing = time_steps(run_range, steps, warmup, lead=1, per_graph=2)
+    ms_per_step = timing["device_s"] / steps * 1e3
+    step_us = ms_per_step * 1e3
+    ops = {}
+    for op, us in op_us.items():
+        count = shape.layers if op in layer_ops else 1
+        ops[op] = {"us": round(us, 3), "launches": count, "us_per_step": round(us * count, 1),
+                   "share": round(us * count / step_us, 4), "GB/s": round(cb[op] / us / 1e3, 1),
+                   "frac": round(cb[op] / us / 1e3 / PEAK_HBM_GBS, 4)}
+    value = per_step / (ms_per_step * 1e-3) / 1e9
+    ls = shape.layer
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(ms_per_step, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": shape.name, "tokens": fs.num_tokens, "decode_rows": fs.num_decodes,
+                   "decode_positions": fs.layout.decode_positions, "prompts": [list(p) for p in shape.prompts],
+                   "prefill_rows": fs.num_prefills, "layers": shape.layers, "hidden": ls.hidden,
+                   "intermediate": ls.inter, "q_heads": ls.q_heads, "kv_heads": ls.kv_heads, "head_dim": ls.head_dim,
+                   "page_size": shape.page_size, "block_table_width": shape.reach // shape.page_size,
+                   "kv_pages_per_layer": fs.layout.pages, "launch": "hip-graph", "dataflow": "fp8",
+                   "gemms": "N(0,1) stand-in outputs"},
+        "us_per_layer": round(step_us / shape.layers, 3), "frac_of_peak": round(value / PEAK_HBM_GBS, 4),
+        "credited_bytes_per_step": per_step, "ops": ops,
+        "ops_sum_us": round(sum(o["us_per_step"] for o in ops.values()), 1),
+        "graph_us_per_step": round(timing["graph_s"] / steps * 1e6, 3),
+        "host_us_per_step": round(timing["host_s"] / steps * 1e6, 3),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -1174,6 +1273,8 @@ def main() -> int:
         return context_main(mas, args, mas.workloads.CONTEXT_SHAPES[args.workload], dev)
     if args.workload in mas.workloads.ATTENTION_SHAPES:
         return attention_main(mas, args, mas.workloads.ATTENTION_SHAPES[args.workload], dev)
+    if args.workload in mas.workloads.STEP_SHAPES:
+        return step_main(mas, args, mas.workloads.STEP_SHAPES[args.workload], dev)
     shape = mas.workloads.SHAPES[args.workload]
     if args.pmc_probe:
         pmc_probe(mas, args, shape, dev)

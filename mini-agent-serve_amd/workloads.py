@@ -19,7 +19,7 @@ from .rope import cos_sin_cache
 __all__ = ["Shape", "SHAPES", "LayerInputs", "make_layer_inputs", "credited_bytes", "layer_credited_bytes",
            "AttentionShape", "ATTENTION_SHAPES", "AttentionInputs", "make_attention_inputs",
            "attention_credited_bytes", "ContextShape", "CONTEXT_SHAPES", "ContextInputs", "make_context_inputs",
-           "context_flops"]
+           "context_flops", "StepShape", "STEP_SHAPES", "StepLayout", "make_step_layout"]
 
 
 @dataclass(frozen=True)
@@ -374,3 +374,102 @@ def context_flops(shape: ContextShape) -> int:
     padding)."""
     positions = sum(shape.cached + i + 1 for i in range(shape.q_len))
     return shape.rows * positions * shape.q_heads * shape.head_dim * 4
+
+
+# ---- whole forward steps (decode rows and prompt rows, as the runner lays a graph step out) -----------
+
+@dataclass(frozen=True)
+class StepShape:
+    """One step of the reference's captured forward (Devstral2Model.forward, devstral2.py:265-307)
+    at Devstral-Small-2's sizes: ``decode_rows`` decode sequences with lengths drawn from U[1,
+    max_len] (each appends its one new token at position len - 1) and, when ``prompts`` is not
+    empty, the runner's 17 prompt rows: the prompts ((new tokens, cached positions) each), one
+    padding row and empty rows (model_runner.py:179-221). Pages of ``page_size`` slots and block
+    tables ``reach / page_size`` columns wide: the reference engine's defaults (serving_engine.py:23-27,
+    model_runner.py:79)."""
+    name: str
+    decode_rows: int
+    max_len: int
+    prompts: tuple = ()
+    layers: int = 40
+    page_size: int = 16
+    reach: int = 8192
+    layer: Shape = SHAPES["decode64_24b"]     # hidden / intermediate / head sizes
+    prefill_rows: int = 17                    # model_runner.py:21
+    token_step: int = 64                      # model_runner.py:19: graph token counts are multiples of it
+
+
+STEP_SHAPES: dict[str, StepShape] = {s.name: s for s in [
+    # a decode step of 64 sequences up to 8192 positions through all 40 layers
+    StepShape("decode_step_64x8192_40", 64, 8192),
+    # the same decode rows with an agent turn's prompt chunk in the same step: 100 new tokens after
+    # 4000 cached (a 192-token graph step: 64 decode tokens, 100 prompt tokens, 28 padding tokens)
+    StepShape("mixed_step_64x8192_1x100_40", 64, 8192, prompts=((100, 4000),)),
+]}
+
+
+@dataclass
+class StepLayout:
+    """A step's index tensors on the CPU, as the runner's prepare() fills them for a graph step:
+    decode rows first (decode row i owns token i), then the prompt rows; tokens of the padding row at
+    positions 0.. of the sink page (the pool's last page)."""
+    num_tokens: int
+    num_decodes: int
+    positions: torch.Tensor     # [num_tokens] int32
+    batch_indices: torch.Tensor  # [num_tokens] int32
+    seq_lens: torch.Tensor      # [rows] int32
+    cu_seqlens_q: torch.Tensor  # [prefill rows + 1] int32 (prompt tokens, counted after the decode tokens)
+    block_tables: torch.Tensor  # [rows, reach / page_size] int32
+    pages: int                  # pages in the pool, the sink page last
+    decode_positions: int       # positions the decode rows attend (their seq_lens summed)
+
+
+def make_step_layout(shape: StepShape, seed: int = 0) -> StepLayout:
+    g = torch.Generator().manual_seed(seed)
+    ps, width = shape.page_size, shape.reach // shape.page_size
+    d = shape.decode_rows
+    dec_lens = torch.randint(1, shape.max_len + 1, (d,), generator=g)
+    npf = len(shape.prompts)
+    tokens = d + sum(q for q, _ in shape.prompts)
+    if npf:
+        tokens = -(-tokens // shape.token_step) * shape.token_step
+    prefill_rows = shape.prefill_rows if npf else 0
+    rows = d + prefill_rows
+    row_lens = [int(n) for n in dec_lens] + [q + c for q, c in shape.prompts]
+    need = [-(-n // ps) for n in row_lens]
+    if max(need) > width:
+        raise ValueError("a row reaches past the block table")
+    pages = sum(need) + 1
+    sink = pages - 1
+    perm = torch.randperm(pages - 1, generator=g).to(torch.int32)
+    tables = torch.full((rows, width), sink, dtype=torch.int32)   # past seq_lens: never read
+    at = 0
+    for r, k in enumerate(need):
+        tables[r, :k] = perm[at:at + k]
+        at += k
+    positions = torch.zeros(tokens, dtype=torch.int32)
+    batch = torch.zeros(tokens, dtype=torch.int32)
+    lens = torch.ones(rows, dtype=torch.int32)
+    cu = torch.zeros(prefill_rows + 1, dtype=torch.int32)
+    positions[:d] = (dec_lens - 1).to(torch.int32)
+    batch[:d] = torch.arange(d, dtype=torch.int32)
+    lens[:d] = dec_lens.to(torch.int32)
+    t = 0
+    for j, (q, c) in enumerate(shape.prompts):
+        cu[j] = t
+        positions[d + t:d + t + q] = torch.arange(c, c + q, dtype=torch.int32)
+        batch[d + t:d + t + q] = d + j
+        lens[d + j] = c + q
+        t += q
+    if prefill_rows > npf:
+        first, start = d + npf, d + t
+        positions[start:] = torch.arange(tokens - start, dtype=torch.int32)
+        batch[start:] = first
+        lens[first:] = 1
+        lens[first] = max(tokens - start, 1)
+        cu[npf] = t
+        cu[npf + 1:] = tokens - d
+        tables[first:, :] = sink
+    if prefill_rows:
+        cu[prefill_rows] = tokens - d
+    return StepLayout(tokens, d, positions, batch, lens, cu, tables, pages, int(dec_lens.sum()))
