@@ -93,6 +93,7 @@ struct ContextArgs {
   // kWorkSelfPlan: what the plan's estimate needs (CUs, resident workgroups, the grid's workgroups,
   // the partial entries the workspace holds) and the block table's reach
   int plan_cus, plan_resident;
+  int plan_lt, plan_hb;  // log2 of the tokens per token tile, head blocks per (row, token tile)
   int64_t plan_item_cap, plan_entry_cap, plan_cap;
   float scale_log2;
   float out_scale;
@@ -282,15 +283,21 @@ __device__ __forceinline__ int tiles_over(int shift, int q_len, int tiles, int l
   return tiles - min(t0, tiles - 1);
 }
 
-// ceil(a / b) for 0 <= a < 2^24 and b >= 1, from rb = 1 / b: the fp32 quotient is within one of
-// the integer one, which one correction settles.
-__device__ __forceinline__ int ceil_div_small(int a, int b, float rb) {
-  const int n = a + b - 1;
-  int q = static_cast<int>(static_cast<float>(n) * rb);
-  q -= q * b > n ? 1 : 0;
-  q += (q + 1) * b <= n ? 1 : 0;
+// Integer quotients of small operands without the integer-division sequence: rb = rcp_small(b)
+// (v_rcp_f32, within 1 ulp of 1 / b). For a numerator below 2^22 the fp32 quotient is within 3/4 of
+// the real one, so one correction each way gives the exact integer result.
+__device__ __forceinline__ float rcp_small(int b) { return __builtin_amdgcn_rcpf(static_cast<float>(b)); }
+
+// floor(a / b) for 0 <= a < 2^22 and b >= 1.
+__device__ __forceinline__ int floor_div_small(int a, int b, float rb) {
+  int q = static_cast<int>(static_cast<float>(a) * rb);
+  q -= q * b > a ? 1 : 0;
+  q += (q + 1) * b <= a ? 1 : 0;
   return q;
 }
+
+// ceil(a / b) for 0 <= a, a + b <= 2^22 and b >= 1.
+__device__ __forceinline__ int ceil_div_small(int a, int b, float rb) { return floor_div_small(a + b - 1, b, rb); }
 
 __device__ __forceinline__ int lane_i(int x, int l) { return __builtin_amdgcn_readlane(x, l); }
 
@@ -344,9 +351,19 @@ __device__ SelfPlan self_plan(const PlanRow& r, const PlanShape& s, int cus, int
   m.entries_per_unit = s.head_blocks * (s.heads_per_wg << s.lt);
   m.pair_us = static_cast<float>(1 << s.lt) * s.hq * 9.0e-4f;
   m.entry_us = (s.head_dim + 2) * 4.f / 5.0e6f;
-  // lane l weighs l + 2 splits (plan_best_splits), counting the units longer than its split length
+  // the workgroup rounds of plan_time from a reciprocal of the resident count (every operand here
+  // is below 2^22, host-checked)
+  const float rres = rcp_small(resident);
+  const auto time_of = [&](int wgs, int per) {
+    const float per_wg = static_cast<float>(per) + 4.8f;
+    return wgs <= cus ? per_wg * 1.8f : static_cast<float>(ceil_div_small(wgs, resident, rres)) * per_wg * 2.1f;
+  };
+  // lane l weighs l + 2 splits (plan_best_splits), counting the units longer than its split length;
+  // its split length as plan_per gives it
   const int k = lane + 2;
-  const int per_k = plan_per(m, k);
+  const int tiles_k = ceil_div_small(longest, k, rcp_small(k));
+  const int per_k =
+      k <= kMaxCtxSplits && ceil_div_small(longest, tiles_k, rcp_small(tiles_k)) == k ? max(4, tiles_k) : 0;
   float c = __builtin_huge_valf();
   if (per_k != 0 && per_k < longest) {
     int split = 0;
@@ -357,13 +374,13 @@ __device__ SelfPlan self_plan(const PlanRow& r, const PlanShape& s, int cus, int
     const int64_t wgs = static_cast<int64_t>(units + split * (k - 1)) * s.head_blocks;  // at most
     const int64_t entries = static_cast<int64_t>(split) * m.entries_per_unit * k;
     if (wgs <= m.item_cap && entries <= m.entry_cap)
-      c = plan_time(m, static_cast<int>(wgs), per_k) + 5.0f +
+      c = time_of(static_cast<int>(wgs), per_k) + 5.0f +
           fmaxf(static_cast<float>(entries) * m.entry_us, static_cast<float>(split) * m.pair_us);
   }
   const float low = wave_min_f(c);
-  if (!(low < 0.8f * plan_time(m, units * s.head_blocks, longest))) return pl;
+  if (!(low < 0.8f * time_of(units * s.head_blocks, longest))) return pl;
   pl.splits = __builtin_ctzll(__ballot(c == low)) + 2;
-  pl.per = max(4, (longest + pl.splits - 1) / pl.splits);
+  pl.per = max(4, ceil_div_small(longest, pl.splits, rcp_small(pl.splits)));
   return pl;
 }
 
@@ -384,11 +401,10 @@ __device__ __forceinline__ int wave_sum_i(int v) {
 // and writes the split-unit count to plan_hdr[1]; the workgroup of each split unit's first range and
 // head block writes the unit's plan_units entry: what context_plan writes for the merge. Returns
 // false for a workgroup past the plan's items.
-template <int D, int kWaves>
-__device__ __forceinline__ bool self_plan_item(const ContextArgs& a, int hgroups, int lane, int i, i32x4& d0,
-                                               i32x4& d1) {
-  const int lt = 5 + __builtin_ctz(static_cast<unsigned>(kWaves / a.heads_per_wg));  // log2 tokens per tile
-  const int hb = a.hk * hgroups;
+template <int D>
+__device__ __forceinline__ bool self_plan_item(const ContextArgs& a, int lane, int i, i32x4& d0, i32x4& d1) {
+  const int lt = a.plan_lt, hb = a.plan_hb;  // log2 tokens per tile, head blocks
+  const float rhb = rcp_small(hb);
   const PlanShape shape{a.plan_rows, a.plan_gy, lt, hb, a.heads_per_wg, a.hq, D};
   const PlanRow r = plan_row(a.cu_seqlens_q, a.seq_lens, a.plan_rows, a.plan_gy, lt, a.plan_cap, lane);
   if (i == 0 && __ballot(r.bad) != 0 && lane == 0) report(a.err, MAS_ERRBIT_POSITION);
@@ -405,7 +421,7 @@ __device__ __forceinline__ bool self_plan_item(const ContextArgs& a, int hgroups
   }
   const SelfPlan pl = self_plan(r, shape, a.plan_cus, a.plan_resident, a.plan_item_cap, a.plan_entry_cap, lane);
   const int per = pl.splits > 1 ? pl.per : (1 << 30);  // unsplit: no tile reaches past per
-  const float rp = 1.0f / static_cast<float>(per);
+  const float rp = rcp_small(per);
   // each row's split tiles (its last ones) and key ranges, a row per lane
   const int sp_l = tiles_over(r.shift, r.q_len, r.tiles, lt, per);
   int rng_l = r.tiles - sp_l;
@@ -443,12 +459,12 @@ __device__ __forceinline__ bool self_plan_item(const ContextArgs& a, int hgroups
     used = lane_i(used_l, k);
     su += k;
   } else {
-    const int u = off / hb;  // an unsplit tile: one item per head block
+    const int u = floor_div_small(off, hb, rhb);  // an unsplit tile: one item per head block
     tile = tiles - 1 - split_here - u;
     off -= u * hb;
   }
   const int nt = tile_key_tiles(shift, q_len, lt, tile);
-  const int range = off / hb, block = off - range * hb;
+  const int range = floor_div_small(off, hb, rhb), block = off - range * hb;
   const int len = used > 1 ? per : nt, first = range * len;
   const int q0 = lane_i(r.q0, rl), kv = lane_i(r.kv, rl);
   d0 = i32x4{q0, q_len, kv, rl | (range << 16) | (pl.splits << 24)};
@@ -496,7 +512,7 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
     __shared__ int item_ok;
     if (wave == 0) {
       i32x4 e0{}, e1{};
-      const bool ok = self_plan_item<D, kWaves>(a, hgroups, lane, static_cast<int>(blockIdx.x), e0, e1);
+      const bool ok = self_plan_item<D>(a, lane, static_cast<int>(blockIdx.x), e0, e1);
       if (lane == 0) {
         item_ok = ok ? 1 : 0;
         item_lds[0] = e0;
@@ -1436,7 +1452,8 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
       plan = plan_layout(units_bound, gx, resident);
       // a self-planned launch (up to kSelfPlanMaxRows rows) keeps only the plan's counts and split
       // units in the workspace, no items
-      self_plan = num_rows <= kSelfPlanMaxRows && plan.item_cap < (int64_t{1} << 24);
+      // (the kernels' small-operand quotients need the grid and the reach in key tiles below 2^22)
+      self_plan = num_rows <= kSelfPlanMaxRows && plan.item_cap < (int64_t{1} << 22) && cap <= (int64_t{1} << 27);
       const int64_t plan_off = self_plan ? self_plan_partial_off(units_bound) : plan.partial_off;
       if (workspace_bytes > plan_off) {
         plan_entries = (workspace_bytes - plan_off) / entry_bytes;
@@ -1505,6 +1522,8 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
     a.plan_gy = static_cast<int>(gy);
     a.plan_cus = cus;
     a.plan_resident = static_cast<int>(resident);
+    a.plan_lt = __builtin_ctzll(static_cast<uint64_t>(tokens_per_wg));
+    a.plan_hb = static_cast<int>(gx);
     a.plan_item_cap = plan.item_cap;
     a.plan_entry_cap = plan_entries;
     a.plan_cap = cap;
