@@ -118,6 +118,40 @@ def test_self_planned_launch_equals_the_planner_launch(mas, dev, case):
     assert not torch.equal(out, one_kernel)  # the plan split the long rows
 
 
+@pytest.mark.parametrize("n_prompts,cached", [(40, 3000), (24, 6000)], ids=["40_unsplit", "24_split"])
+def test_self_planned_64_rows_equal_the_planner_on_65(mas, dev, n_prompts, cached):
+    """The largest self-planned step (64 rows, a row per lane) against the same prompts on 65 rows,
+    which the planner launch lays out, bit for bit: 40 one-tile prompts (320 workgroups, unsplit)
+    and 24 after longer prefixes (split), so the per-row counts fill lanes across the wavefront's
+    four 16-lane rows. The first three prompts also against the oracle."""
+    g = torch.Generator().manual_seed(640 + n_prompts)
+    prompts = [(int(torch.randint(1, 25, (1,), generator=g)), int(torch.randint(0, cached, (1,), generator=g)))
+               for _ in range(n_prompts)]
+    tokens = sum(n for n, _ in prompts)
+    pad = -(-tokens // 64) * 64 - tokens
+    q, kc, vc, tables, seq, cu, max_q = _graph_case(640, prompts, pad, 32, 8, 128, 16, rows=64)
+    q65, kc65, vc65, tables65, seq65, cu65, max_q65 = _graph_case(640, prompts, pad, 32, 8, 128, 16, rows=65)
+    assert torch.equal(q, q65) and torch.equal(kc, kc65) and max_q == max_q65
+    reach = tables.shape[1] * 16
+    flags, flags65 = (torch.zeros(1, dtype=torch.int32, device=dev) for _ in range(2))
+    out = _call(mas, dev, q, kc, vc, tables, seq, cu, max_q, reach, 0.088, flags=flags)
+    out65 = _call(mas, dev, q65, kc65, vc65, tables65, seq65, cu65, max_q65, reach, 0.088, flags=flags65)
+    assert int(flags.item()) == 0 and int(flags65.item()) == 0
+    assert torch.equal(out, out65)
+    one_kernel = _call(mas, dev, q, kc, vc, tables, seq, cu, max_q, reach, 0.088, ws_bytes=16)
+    if n_prompts == 40:
+        assert torch.equal(out, one_kernel)      # unsplit: the grid launch's work
+    else:
+        assert not torch.equal(out, one_kernel)  # the plan split the long rows
+    t3 = int(cu[3])
+    want = ops.paged_context_attention(bits(q[:t3]), bits(kc), bits(vc), tables[:3].numpy(), seq[:3].numpy(),
+                                       cu[:4].numpy(), 0.088)
+    exact = np.mean(bits(out[:t3]) == want)
+    exact_one = np.mean(bits(one_kernel[:t3]) == want)
+    assert exact >= min(0.6, exact_one - 0.02), (exact, exact_one)
+    _check(bits(out[:t3]), want, min_exact=0.0)
+
+
 def test_planned_context_attention_short_rows_equal_one_kernel(mas, dev):
     """A step of short prompts: the plan splits nothing and its items are the one-kernel grid's
     workgroups, so the output is the one-kernel output bit for bit."""
