@@ -453,3 +453,52 @@ def test_planned_context_attention_random_steps(mas, dev, seed):
     assert int(flags.item()) == 0
     want = ops.paged_context_attention(bits(q), bits(kc), bits(vc), tables.numpy(), seq.numpy(), cu.numpy(), scale)
     _check(bits(out), want, min_exact=0.5)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_self_planned_random_steps_equal_the_planner(mas, dev, seed):
+    """Seeded graph steps of 18-64 rows (self-planned) with 1-40 prompts of 1-60 new tokens after
+    0-9000 cached positions (8 kv heads, group sizes 1-12, head_dim 64 / 128, pages of 8-256 slots),
+    against the same prompts on 65 rows (the planner launch): the same output and error bits, bit for
+    bit; and the first prompt against the oracle. Both launches are planned only when the grid holds
+    a workgroup per CU or more (smaller grids take the host's split-KV), so the row count is raised
+    to make the self-planned grid that large."""
+    rng = np.random.default_rng(5000 + seed)
+    rows = int(rng.integers(18, 65))
+    n = int(rng.integers(1, min(rows - 1, 40) + 1))
+    prompts = []
+    for _ in range(n):
+        new = int(rng.integers(1, 61))
+        if sum(p for p, _ in prompts) + new > 900:   # planned steps cover at most 1024 tokens
+            break
+        prompts.append((new, int(rng.choice([0, rng.integers(1, 9001)]))))
+    hk = 8
+    group = int(rng.choice([1, 2, 3, 4, 6, 8, 12]))
+    dim = int(rng.choice([64, 128]))
+    ps = int(rng.choice([8, 16, 64, 256]))
+    hq = hk * group
+    used = sum(p for p, _ in prompts)
+    pad = -(-used // 64) * 64 - used
+    # the grid of the host's launch rules: 4 heads per workgroup from groups of 4 (2 for 2, else 1),
+    # 8 wavefronts from groups of 8, 32 tokens per wavefront row
+    per_wg = 4 if group >= 4 else (2 if group == 2 else 1)
+    tokens_per_wg = 32 * ((8 if group >= 8 else 4) // per_wg)
+    blocks = hk * -(-group // per_wg) * -(-(used + pad) // tokens_per_wg)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    rows = max(rows, -(-cus // blocks), len(prompts) + 1)
+    assert rows <= 64
+    q, kc, vc, tables, seq, cu, max_q = _graph_case(6000 + seed, prompts, pad, hq, hk, dim, ps, reach=16384,
+                                                    rows=rows)
+    q65, kc65, vc65, tables65, seq65, cu65, max_q65 = _graph_case(6000 + seed, prompts, pad, hq, hk, dim, ps,
+                                                                  reach=16384, rows=65)
+    assert torch.equal(q, q65) and torch.equal(kc, kc65) and max_q == max_q65
+    scale = dim ** -0.5
+    flags, flags65 = (torch.zeros(1, dtype=torch.int32, device=dev) for _ in range(2))
+    out = _call(mas, dev, q, kc, vc, tables, seq, cu, max_q, 16384, scale, flags=flags)
+    out65 = _call(mas, dev, q65, kc65, vc65, tables65, seq65, cu65, max_q65, 16384, scale, flags=flags65)
+    assert int(flags.item()) == int(flags65.item()) == 0
+    assert torch.equal(out, out65), (rows, prompts, hq, hk, dim, ps)
+    t1 = int(cu[1])
+    want = ops.paged_context_attention(bits(q[:t1]), bits(kc), bits(vc), tables[:1].numpy(), seq[:1].numpy(),
+                                       cu[:2].numpy(), scale)
+    _check(bits(out[:t1]), want, min_exact=0.5)
