@@ -5,7 +5,9 @@ token's rotated key and its value at the slot its row's block table gives; the a
 (the o_proj input quantize) of the decode rows and of the prompt rows is the oracle's attention of
 the rotated queries over that cache, quantized, within one e4m3 step plus the bf16 tolerance
 (rtol 1.6e-2, atol 1e-2) divided by the scale; and so is the last SiluAndMul + quantize output.
-The residual chain, the cache rows and the layout are the bit-exact checks."""
+The residual chain, the cache rows and the layout are the bit-exact checks. Two fixed steps (5
+decode rows, with and without a prompt) and six seeded ones (1-12 decode rows, 0-3 prompts, pages
+of 16-256 slots)."""
 from __future__ import annotations
 
 import dataclasses
@@ -21,12 +23,12 @@ from oracle import ops
 pytestmark = pytest.mark.gpu
 
 
-def _step(mas, dev, prompts):
+def _step(mas, dev, prompts, decode_rows=5, max_len=300, page_size=16, reach=512, seed=3):
     wl = mas.workloads
     layer = dataclasses.replace(wl.SHAPES["decode64_24b"], vocab=4096)
-    shape = wl.StepShape("test_step", decode_rows=5, max_len=300, prompts=prompts, layers=2, reach=512,
-                         layer=layer)
-    fs = mas.layer_pass.ForwardStep(shape, dev, seed=3)
+    shape = wl.StepShape("test_step", decode_rows=decode_rows, max_len=max_len, prompts=prompts, layers=2,
+                         page_size=page_size, reach=reach, layer=layer)
+    fs = mas.layer_pass.ForwardStep(shape, dev, seed=seed)
     final_in = bits(fs.final_in)   # the final norm writes its output over its input
     fs.run()
     torch.cuda.synchronize()
@@ -41,9 +43,22 @@ def _fp8_close(got_codes, want_codes, scale):
     assert np.all(np.abs(got - want) <= step)
 
 
-@pytest.mark.parametrize("prompts", [(), ((20, 50),)], ids=["decode", "mixed"])
-def test_forward_step_against_the_oracle(mas, dev, prompts):
-    fs, final_in = _step(mas, dev, prompts)
+def _random_step(seed):
+    """1-12 decode rows up to 40-600 positions, 0-3 prompts of 1-60 new tokens after 0-400 cached,
+    pages of 16, 64 or 256 slots, a 1024-position table."""
+    rng = np.random.default_rng(seed)
+    n = int(rng.integers(1, 4)) if rng.random() < 0.75 else 0
+    prompts = tuple((int(rng.integers(1, 61)), int(rng.integers(0, 401))) for _ in range(n))
+    return dict(prompts=prompts, decode_rows=int(rng.integers(1, 13)), max_len=int(rng.integers(40, 601)),
+                page_size=int(rng.choice([16, 64, 256])), reach=1024, seed=seed)
+
+
+CASES = [dict(prompts=()), dict(prompts=((20, 50),))] + [_random_step(700 + k) for k in range(6)]
+
+
+@pytest.mark.parametrize("case", CASES, ids=["decode", "mixed"] + [f"seed{700 + k}" for k in range(6)])
+def test_forward_step_against_the_oracle(mas, dev, case):
+    fs, final_in = _step(mas, dev, **case)
     ls, lay = fs.shape.layer, fs.layout
     n, d = fs.num_tokens, fs.num_decodes
     scale = float(fs.act_scale)
@@ -75,8 +90,9 @@ def test_forward_step_against_the_oracle(mas, dev, prompts):
         assert np.array_equal(kc[page, e], kb[t]) and np.array_equal(vc[page, e], vb[t])
     qb = bits(q).reshape(n, ls.q_heads, ls.head_dim)
     got = fp8_codes(fs.attn_out)
-    att = ops.paged_decode_attention(qb[:d], kc, vc, tables[:d], lens[:d], fs.scale)
-    _fp8_close(got[:d], ops.quantize_activation(att, scale), scale)
+    if d:
+        att = ops.paged_decode_attention(qb[:d], kc, vc, tables[:d], lens[:d], fs.scale)
+        _fp8_close(got[:d], ops.quantize_activation(att, scale), scale)
     if fs.shape.prompts:
         att = ops.paged_context_attention(qb[d:], kc, vc, tables[d:], lens[d:], lay.cu_seqlens_q.numpy(), fs.scale)
         _fp8_close(got[d:real], ops.quantize_activation(att, scale)[:real - d], scale)
