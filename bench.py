@@ -63,7 +63,7 @@ KERNEL_SOURCES = {
     "paged_context_attention": ("csrc/context_attention.hip", "csrc/device.h"),
 }
 # Git blob hashes of the kernel sources the profiled figures below were measured on.
-_SILU_SOURCES = {"csrc/silu_and_mul.hip": "bad18b16d062f19d55aead1bf7b7d74e2f49874a",
+_SILU_SOURCES = {"csrc/silu_and_mul.hip": "23b0260df03f552c5aeb3be5992d159ad4873f02",
                  "csrc/device.h": "4a649fbd27cb9b4a8503ee1b497b4df962d5650e"}
 _NORM_SOURCES = {"csrc/rmsnorm.hip": "089cb088624451ba8a83f3bc292864153fe93b0d",
                  "csrc/device.h": "4a649fbd27cb9b4a8503ee1b497b4df962d5650e"}
@@ -74,13 +74,13 @@ _DECODE_ATTN_SOURCES = {"csrc/attention.hip": "fedddcdb2d8be7c237ff8a5857fcbfc36
 # device copy.
 MEASURED_TRAFFIC = {
     ("decode64_24b", "silu_and_mul"): {
-        "bytes": 12_610_966, "profile": "profiles/silu_and_mul_decode64_hbm_traffic.md", "sources": _SILU_SOURCES},
+        "bytes": 12_612_732, "profile": "profiles/silu_and_mul_decode64_hbm_traffic.md", "sources": _SILU_SOURCES},
     ("rmsnorm_256x5120", "fused_add_rmsnorm"): {
         "bytes": 10_607_023, "profile": "profiles/rmsnorm_256x5120_kernel_trace.md", "sources": _NORM_SOURCES},
     ("decode_pass_256x40", "silu_and_mul"): {
-        "bytes": 50_359_743, "profile": "profiles/decode_pass_256x40_kernel_trace.md", "sources": _SILU_SOURCES},
+        "bytes": 50_357_113, "profile": "profiles/decode_pass_256x40_kernel_trace.md", "sources": _SILU_SOURCES},
     ("prefill8192_24b", "silu_and_mul"): {
-        "bytes": 1_610_476_668, "profile": "profiles/silu_and_mul_prefill_hbm_traffic.md", "sources": _SILU_SOURCES},
+        "bytes": 1_610_475_810, "profile": "profiles/silu_and_mul_prefill_hbm_traffic.md", "sources": _SILU_SOURCES},
     ("decode_attn_64x8192_24b", "paged_decode_attention"): {
         "bytes": 1_115_053_768, "profile": "profiles/decode_attention_64x8192_kernel_trace.md",
         "sources": _DECODE_ATTN_SOURCES},
@@ -93,13 +93,13 @@ MEASURED_TRAFFIC = {
 # events, and nothing else). The roofline's `achieved` and `frac` use this duration.
 TRACED_LAUNCH_US = {
     ("decode64_24b", "silu_and_mul"): {
-        "us": 4.565, "profile": "profiles/layer_decode64_kernel_trace.md", "sources": _SILU_SOURCES},
+        "us": 3.919, "profile": "profiles/layer_decode64_kernel_trace.md", "sources": _SILU_SOURCES},
     ("rmsnorm_256x5120", "fused_add_rmsnorm"): {
-        "us": 4.751, "profile": "profiles/rmsnorm_256x5120_kernel_trace.md", "sources": _NORM_SOURCES},
+        "us": 3.899, "profile": "profiles/rmsnorm_256x5120_kernel_trace.md", "sources": _NORM_SOURCES},
     ("decode_pass_256x40", "silu_and_mul"): {
-        "us": 9.680, "profile": "profiles/decode_pass_256x40_kernel_trace.md", "sources": _SILU_SOURCES},
+        "us": 9.562, "profile": "profiles/decode_pass_256x40_kernel_trace.md", "sources": _SILU_SOURCES},
     ("prefill8192_24b", "silu_and_mul"): {
-        "us": 245.177, "profile": "profiles/layer_prefill8192_kernel_trace.md", "sources": _SILU_SOURCES},
+        "us": 234.195, "profile": "profiles/layer_prefill8192_kernel_trace.md", "sources": _SILU_SOURCES},
     ("decode_attn_64x8192_24b", "paged_decode_attention"): {     # split + combine
         "us": 206.838 + 7.119, "profile": "profiles/decode_attention_64x8192_kernel_trace.md",
         "sources": _DECODE_ATTN_SOURCES},
@@ -225,11 +225,11 @@ def load_skeletons(mas) -> None:
     lib = ctypes.CDLL(str(path))
     fn = lib.mas_bench_stream_skeleton
     fn.restype = ctypes.c_int
-    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64] * 4 + [ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p]
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64] * 4 + [ctypes.c_int64] * 3 + [ctypes.c_void_p]
     _skeleton_fn = fn
     fn = lib.mas_bench_rope_append_skeleton
     fn.restype = ctypes.c_int
-    fn.argtypes = [ctypes.c_void_p] + [ctypes.c_int64] * 3 + [ctypes.c_void_p] * 2 + [ctypes.c_int64] * 2 + \
+    fn.argtypes = [ctypes.c_void_p] + [ctypes.c_int64] * 3 + [ctypes.c_void_p] * 2 + [ctypes.c_int64] * 3 + \
         [ctypes.c_void_p]
     _rope_append_skeleton_fn = fn
     _stamp_fn = lib.mas_bench_timestamp
@@ -293,11 +293,11 @@ def time_steps(run_steps, k: int, w: int, lead: int, per_graph: int) -> dict:
     return {"device_s": ticks / (_clock_khz * 1e3), "graph_s": graph_s, "host_s": host_s, "chunks": len(sizes)}
 
 
-def skeleton_launcher(b, op):
+def skeleton_launcher(b, op, block: int = 256):
     """A closure launching the memory skeleton of ``op`` on the buffers of ``b``: the kernel's
-    streams (same rows, row strides and read / write mix) moved with no arithmetic. The KV store's
-    skeleton writes the cache's first rows instead of the mapped slots; index arrays and the norm
-    weight are not moved."""
+    streams (same rows, row strides and read / write mix) moved with no arithmetic, in workgroups of
+    ``block`` threads. The KV store's skeleton writes the cache's first rows instead of the mapped
+    slots; index arrays and the norm weight are not moved."""
     li, s = b.inputs, b.inputs.shape
     n = s.tokens
     if op == "fused_add_rmsnorm":
@@ -316,7 +316,7 @@ def skeleton_launcher(b, op):
     elif op == "rope_append":
         qkv, row = li.qkv, s.kv_heads * s.head_dim
         ptrs = (qkv.data_ptr(), qkv.stride(0), (s.q_heads + s.kv_heads) * s.head_dim, row, li.k_cache.data_ptr(),
-                li.v_cache.data_ptr(), row, n)
+                li.v_cache.data_ptr(), row, n, block)
 
         def launch_fused():
             st = _rope_append_skeleton_fn(*ptrs, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
@@ -325,7 +325,7 @@ def skeleton_launcher(b, op):
         return launch_fused
     else:
         raise ValueError(op)
-    ptrs = [a.data_ptr() if isinstance(a, torch.Tensor) else a for a in args]
+    ptrs = [a.data_ptr() if isinstance(a, torch.Tensor) else a for a in args] + [block]
 
     def launch():
         st = _skeleton_fn(*ptrs, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
@@ -339,6 +339,8 @@ def op_launcher(mas, b, op):
     memory skeleton)."""
     if op.startswith("skeleton:"):
         return skeleton_launcher(b, op.split(":", 1)[1])
+    if op.startswith("skeleton64:"):
+        return skeleton_launcher(b, op.split(":", 1)[1], block=64)
     li, s = b.inputs, b.inputs.shape
     if op == "fused_add_rmsnorm":
         return lambda: mas.norm.fused_add_rmsnorm(li.hidden, li.residual, li.norm_weight, s.eps)
@@ -663,11 +665,14 @@ class EmbeddingBench:
         ids, step_ids, last, ph = self.ids[i], self.step_ids[i], self.last[i], self.placeholders
         if op == "embedding":
             return lambda: mas.embedding.embedding(ids, self.table, out=out)
-        if op == "skeleton:embedding":
-            # the same bytes and launch shape with no id lookup: rows i, i + stride, ... of the table
+        if op in ("skeleton:embedding", "skeleton64:embedding"):
+            # the same bytes with no id lookup: rows i, i + stride, ... of the table, in workgroups of
+            # 256 or 64 threads
             stride = (self.vocab // self.tokens) * self.table.stride(0)
             src = self.table[i % (self.vocab // self.tokens)]
-            ptrs = (src.data_ptr(), stride, None, 0, out.data_ptr(), out.stride(0), None, 0, self.tokens, self.hidden)
+            block = 64 if op.startswith("skeleton64:") else 256
+            ptrs = (src.data_ptr(), stride, None, 0, out.data_ptr(), out.stride(0), None, 0, self.tokens, self.hidden,
+                    block)
 
             def launch():
                 st = _skeleton_fn(*ptrs, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
@@ -721,14 +726,16 @@ class EmbeddingBench:
         """(the embedding's ``ops`` entry, the step-input comparison)."""
         ops = ("embedding", "step_input_reset", "step_input_reference", "step_input_fused")
         if _skeleton_fn is not None:
-            ops = ops + ("skeleton:embedding",)
+            ops = ops + ("skeleton:embedding", "skeleton64:embedding")
         t = self.time(ops)
         cb = self.credited()
         entry = {"us": round(t["embedding"], 3), "GB/s": round(cb / t["embedding"] / 1e3, 1),
                  "frac": round(cb / t["embedding"] / 1e3 / PEAK_HBM_GBS, 4), "launches_per_replay": self.launches}
         if "skeleton:embedding" in t:
-            entry["skeleton_us"] = round(t["skeleton:embedding"], 3)
-            entry["of_skeleton"] = round(t["skeleton:embedding"] / t["embedding"], 3)
+            sk, block = skeleton_best(t, "embedding")
+            entry["skeleton_us"] = round(sk, 3)
+            entry["skeleton_block"] = block
+            entry["of_skeleton"] = round(sk / t["embedding"], 3)
         steps = {"ids_refresh_us": round(t["step_input_reset"], 3),
                  "reference_us": round(t["step_input_reference"], 3),
                  "fused_us": round(t["step_input_fused"], 3),
@@ -761,8 +768,8 @@ def op_launches(shape, n_sets: int) -> int:
 def timed_kernels(shape, fp8: bool) -> tuple[str, ...]:
     """The step's kernels followed by the memory skeletons of those that have one."""
     kernels = step_ops(shape, fp8)
-    skeletons = tuple(f"skeleton:{op}" for op in kernels if op in SKELETON_OPS and shape.tokens <= 65535) \
-        if _skeleton_fn is not None else ()
+    skeletons = tuple(f"{kind}:{op}" for op in kernels if op in SKELETON_OPS and shape.tokens <= 65535
+                      for kind in ("skeleton", "skeleton64")) if _skeleton_fn is not None else ()
     return kernels + skeletons
 
 
@@ -774,10 +781,20 @@ def op_table(mas, shape, kernels: tuple[str, ...], op_us: dict) -> dict:
                 "frac": round(cb[op] / op_us[op] / 1e3 / PEAK_HBM_GBS, 4)} for op in kernels}
     for op in kernels:
         if f"skeleton:{op}" in op_us:
-            sk = op_us[f"skeleton:{op}"]
+            sk, block = skeleton_best(op_us, op)
             ops[op]["skeleton_us"] = round(sk, 3)
+            ops[op]["skeleton_block"] = block
             ops[op]["of_skeleton"] = round(sk / op_us[op], 3)
     return ops
+
+
+def skeleton_best(op_us: dict, op: str) -> tuple[float, int]:
+    """The faster of an op's two skeleton shapes (workgroups of 256 or 64 threads; neither is the
+    faster one at every size) and its block size."""
+    sk, block = op_us[f"skeleton:{op}"], 256
+    if op_us.get(f"skeleton64:{op}", float("inf")) < sk:
+        sk, block = op_us[f"skeleton64:{op}"], 64
+    return sk, block
 
 
 def run_layer_workload(mas, args, shape, dev) -> dict:

@@ -62,12 +62,15 @@ __global__ __launch_bounds__(256) void rope_append_skeleton(const uint16_t* qkv,
 
 // rows x row_elems bf16 elements per stream; src1 / dst1 null for one stream. Supported mixes:
 // 1 -> 1, 2 -> 2 (pairwise copies) and 2 -> 1. Rows up to 65535 (one grid row each); row_elems a
-// multiple of 8 and every pointer and stride 16-byte aligned.
+// multiple of 8 and every pointer and stride 16-byte aligned. `block_threads`: threads per
+// workgroup, 64 or 256 (neither shape is the faster one at every size, so the benchmark times both).
 extern "C" int mas_bench_stream_skeleton(const void* src0, int64_t src0_stride, const void* src1,
                                          int64_t src1_stride, void* dst0, int64_t dst0_stride, void* dst1,
-                                         int64_t dst1_stride, int64_t rows, int64_t row_elems, hipStream_t stream) {
+                                         int64_t dst1_stride, int64_t rows, int64_t row_elems, int64_t block_threads,
+                                         hipStream_t stream) {
   using namespace mas;
-  if (rows < 0 || row_elems < 0 || rows > 65535) return MAS_ERR_INVALID_VALUE;
+  if (rows < 0 || row_elems < 0 || rows > 65535 || (block_threads != 64 && block_threads != 256))
+    return MAS_ERR_INVALID_VALUE;
   if (rows == 0 || row_elems == 0) return MAS_OK;
   if (src0 == nullptr || dst0 == nullptr || (dst1 != nullptr && src1 == nullptr)) return MAS_ERR_INVALID_VALUE;
   if (row_elems % 8 != 0 || !aligned16(src0) || !aligned16(dst0) || src0_stride % 8 != 0 || dst0_stride % 8 != 0)
@@ -80,7 +83,8 @@ extern "C" int mas_bench_stream_skeleton(const void* src0, int64_t src0_stride, 
                     {static_cast<uint16_t*>(dst0), static_cast<uint16_t*>(dst1)},
                     {dst0_stride, dst1_stride}};
   const int64_t row_vecs = row_elems / 8;
-  const int block = row_vecs >= 256 ? 256 : static_cast<int>(cdiv(row_vecs, kWave) * kWave);
+  const int block = row_vecs >= block_threads ? static_cast<int>(block_threads)
+                                              : static_cast<int>(cdiv(row_vecs, kWave) * kWave);
   const dim3 grid(static_cast<uint32_t>(cdiv(row_vecs, block)), static_cast<uint32_t>(rows));
   if (src1 == nullptr)
     hipLaunchKernelGGL((stream_skeleton<1, 1>), grid, dim3(block), 0, stream, s, row_vecs);
@@ -94,12 +98,14 @@ extern "C" int mas_bench_stream_skeleton(const void* src0, int64_t src0_stride, 
 // The fused RoPE + KV append's memory skeleton: rows of [q | k | v] (qk_elems + kv_elems elements
 // each, the last kv_elems of the q|k part being k) read once; q|k written back in place, k to
 // k_cache and v to v_cache rows of cache_stride elements. Rows up to 65535; every size a multiple
-// of 8 and every pointer and stride 16-byte aligned.
+// of 8 and every pointer and stride 16-byte aligned. `block_threads`: 64 or 256.
 extern "C" int mas_bench_rope_append_skeleton(void* qkv, int64_t qkv_stride, int64_t qk_elems, int64_t kv_elems,
                                               void* k_cache, void* v_cache, int64_t cache_stride, int64_t rows,
-                                              hipStream_t stream) {
+                                              int64_t block_threads, hipStream_t stream) {
   using namespace mas;
-  if (rows < 0 || rows > 65535 || qk_elems < kv_elems || kv_elems < 0) return MAS_ERR_INVALID_VALUE;
+  if (rows < 0 || rows > 65535 || qk_elems < kv_elems || kv_elems < 0 ||
+      (block_threads != 64 && block_threads != 256))
+    return MAS_ERR_INVALID_VALUE;
   if (rows == 0 || qk_elems == 0) return MAS_OK;
   if (qkv == nullptr || k_cache == nullptr || v_cache == nullptr) return MAS_ERR_INVALID_VALUE;
   if (qk_elems % 8 != 0 || kv_elems % 8 != 0 || qkv_stride % 8 != 0 || cache_stride % 8 != 0 ||
@@ -107,9 +113,10 @@ extern "C" int mas_bench_rope_append_skeleton(void* qkv, int64_t qkv_stride, int
       !aligned16(v_cache))
     return MAS_ERR_INVALID_VALUE;
   const int64_t vecs = (qk_elems + kv_elems) / 8;
-  const dim3 grid(static_cast<uint32_t>(cdiv(vecs, 256)), static_cast<uint32_t>(rows));
-  hipLaunchKernelGGL(rope_append_skeleton, grid, dim3(256), 0, stream, static_cast<const uint16_t*>(qkv),
-                     static_cast<uint16_t*>(qkv), qkv_stride, qk_elems / 8, kv_elems / 8,
+  const dim3 grid(static_cast<uint32_t>(cdiv(vecs, block_threads)), static_cast<uint32_t>(rows));
+  hipLaunchKernelGGL(rope_append_skeleton, grid, dim3(static_cast<uint32_t>(block_threads)), 0, stream,
+                     static_cast<const uint16_t*>(qkv), static_cast<uint16_t*>(qkv), qkv_stride, qk_elems / 8,
+                     kv_elems / 8,
                      static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), cache_stride);
   return launch_status();
 }

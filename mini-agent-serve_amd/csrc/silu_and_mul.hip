@@ -14,6 +14,7 @@ namespace mas {
 namespace {
 
 constexpr int kBlock = 256;
+constexpr int kVecBlock = 64;
 
 // silu(g) * u with the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32): a few fp32 ulps from
 // the correctly rounded g / (1 + e^-g), far below the bf16 rounding of the result, at a quarter
@@ -26,11 +27,11 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 }
 
 template <int UNROLL>
-__global__ __launch_bounds__(kBlock) void silu_and_mul_vec(void* __restrict__ out, int64_t out_stride,
+__global__ __launch_bounds__(kVecBlock) void silu_and_mul_vec(void* __restrict__ out, int64_t out_stride,
                                                            const void* __restrict__ in, int64_t in_stride,
                                                            int64_t rows, int64_t inter) {
   const int64_t nvec = inter >> 3;
-  const int64_t v0 = static_cast<int64_t>(blockIdx.x) * (kBlock * UNROLL) + threadIdx.x;
+  const int64_t v0 = static_cast<int64_t>(blockIdx.x) * (kVecBlock * UNROLL) + threadIdx.x;
   for (int64_t row = blockIdx.y; row < rows; row += gridDim.y) {
     const uint16_t* g = static_cast<const uint16_t*>(in) + row * in_stride;
     const uint16_t* u = g + inter;
@@ -41,7 +42,7 @@ __global__ __launch_bounds__(kBlock) void silu_and_mul_vec(void* __restrict__ ou
     u32x4 gv[UNROLL], uv[UNROLL];
 #pragma unroll
     for (int j = 0; j < UNROLL; ++j) {
-      const int64_t v = v0 + j * kBlock;
+      const int64_t v = v0 + j * kVecBlock;
       const int64_t vl = v < nvec ? v : nvec - 1;
       gv[j] = load_stream(g + 8 * vl);
       uv[j] = load_stream(u + 8 * vl);
@@ -49,7 +50,7 @@ __global__ __launch_bounds__(kBlock) void silu_and_mul_vec(void* __restrict__ ou
     load_fence();
 #pragma unroll
     for (int j = 0; j < UNROLL; ++j) {
-      const int64_t v = v0 + j * kBlock;
+      const int64_t v = v0 + j * kVecBlock;
       if (v < nvec) {
         float gf[8], uf[8], y[8];
         unpack8(gv[j], gf);
@@ -66,12 +67,12 @@ __global__ __launch_bounds__(kBlock) void silu_and_mul_vec(void* __restrict__ ou
 // devstral2/devstral2.py:93-95,110-111,224): y = bf16(silu(g) * u) as the unfused op writes it, then
 // out = e4m3fn(clamp(f32(y) / scale, -448, 448)). Reads 4 bytes and writes 1 per element instead of
 // the unfused 6 + 3.
-__global__ __launch_bounds__(kBlock) void silu_and_mul_quant_vec(void* __restrict__ out, int64_t out_stride,
+__global__ __launch_bounds__(kVecBlock) void silu_and_mul_quant_vec(void* __restrict__ out, int64_t out_stride,
                                                                  const void* __restrict__ in, int64_t in_stride,
                                                                  int64_t rows, int64_t inter,
                                                                  const float* __restrict__ scale_dev, float scale_host) {
   const int64_t nvec = inter >> 3;
-  const int64_t v = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  const int64_t v = static_cast<int64_t>(blockIdx.x) * kVecBlock + threadIdx.x;
   for (int64_t row = blockIdx.y; row < rows; row += gridDim.y) {
     const uint16_t* g = static_cast<const uint16_t*>(in) + row * in_stride;
     const int64_t vl = v < nvec ? v : nvec - 1;
@@ -138,7 +139,7 @@ dim3 row_tile_grid(int64_t tiles_per_row, int64_t rows) {
 // from the 64-token decode to 16384 x 28672 (more waves in flight beat 2 and 4 vectors per lane).
 int launch_vec(void* out, int64_t out_stride, const void* in, int64_t in_stride, int64_t rows, int64_t inter,
                hipStream_t s) {
-  hipLaunchKernelGGL((silu_and_mul_vec<1>), row_tile_grid(cdiv(inter / 8, kBlock), rows), dim3(kBlock), 0, s, out,
+  hipLaunchKernelGGL((silu_and_mul_vec<1>), row_tile_grid(cdiv(inter / 8, kVecBlock), rows), dim3(kVecBlock), 0, s, out,
                      out_stride, in, in_stride, rows, inter);
   return launch_status();
 }
@@ -188,7 +189,7 @@ extern "C" int mas_silu_and_mul_quant_fp8(void* out, int64_t out_stride, const v
                        out_stride, input, input_stride, rows, inter, scale_dev, scale_host);
     return launch_status();
   }
-  hipLaunchKernelGGL(silu_and_mul_quant_vec, row_tile_grid(cdiv(inter / 8, kBlock), rows), dim3(kBlock), 0, stream,
+  hipLaunchKernelGGL(silu_and_mul_quant_vec, row_tile_grid(cdiv(inter / 8, kVecBlock), rows), dim3(kVecBlock), 0, stream,
                      out, out_stride, input, input_stride, rows, inter, scale_dev, scale_host);
   return launch_status();
 }

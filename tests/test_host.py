@@ -42,11 +42,13 @@ def test_benchmark_skeletons_live_in_their_own_library(mas):
         pytest.skip("libmas_bench.so not built")
     fn = ctypes.CDLL(str(mas._build.BENCH_LIBRARY_PATH)).mas_bench_stream_skeleton
     fn.restype = ctypes.c_int
-    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64] * 4 + [ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p]
-    assert fn(None, 0, None, 0, None, 0, None, 0, 0, 8, None) == 0          # empty: nothing launched
-    assert fn(16, 8, None, 0, 32, 8, None, 0, 70000, 8, None) == -1        # rows past one grid row each
-    assert fn(16, 8, None, 0, 32, 8, 48, 8, 4, 8, None) == -1              # two destinations, one source
-    assert fn(16, 8, None, 0, 40, 8, None, 0, 4, 8, None) == -1            # misaligned destination
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64] * 4 + [ctypes.c_int64] * 3 + [ctypes.c_void_p]
+    assert fn(None, 0, None, 0, None, 0, None, 0, 0, 8, 256, None) == 0          # empty: nothing launched
+    assert fn(None, 0, None, 0, None, 0, None, 0, 0, 8, 64, None) == 0
+    assert fn(16, 8, None, 0, 32, 8, None, 0, 70000, 8, 256, None) == -1        # rows past one grid row each
+    assert fn(16, 8, None, 0, 32, 8, 48, 8, 4, 8, 256, None) == -1              # two destinations, one source
+    assert fn(16, 8, None, 0, 40, 8, None, 0, 4, 8, 256, None) == -1            # misaligned destination
+    assert fn(16, 8, None, 0, 32, 8, None, 0, 4, 8, 128, None) == -1            # neither 64 nor 256 threads
 
 
 def test_context_workspace_bytes(mas):
