@@ -127,3 +127,48 @@ def test_context_attention_full_size(mas, dev, name):
                                  inp.cu_seqlens_q.cpu(), scale)
     _assert_close(out, want)
     assert int(flags.item()) == 0
+
+
+def _grid_order_tile_major(cus: int, rows: int, q_len: int, kv_hint: int, hq: int, hk: int) -> bool:
+    """The launch's choice between rows in turn and tile-major order for a grid launch (24B-style
+    heads, four wavefronts of 32 tokens per workgroup): the longest tile's time against the
+    launch's time per resident workgroup."""
+    group = hq // hk
+    waves, tokens = (8, 64) if group >= 8 else (4, 32)
+    gx, gy = hk * -(-group // 4), -(-q_len // tokens)
+    mean = max(kv_hint - q_len // 2 + tokens // 2, tokens)
+    return 10 * kv_hint * cus * (8 // waves) >= 3 * rows * gx * gy * mean
+
+
+@pytest.mark.gpu
+def test_context_attention_grid_orders_agree(mas, dev):
+    """16 prompts of 512 tokens: the max_kv_len hint moves the launch between its two grid orders
+    (rows in turn, or every row's longest tiles first). Workgroups compute the same tiles either
+    way, so the outputs are bit-identical, and both match the float32 restatement."""
+    rows, q_len, hq, hk, dim, ps, width = 16, 512, 32, 8, 128, 256, 32
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    if _grid_order_tile_major(cus, rows, q_len, q_len, hq, hk) == _grid_order_tile_major(cus, rows, q_len,
+                                                                                          width * ps, hq, hk):
+        pytest.skip(f"on {cus} CUs both hints pick the same order")
+    g = torch.Generator().manual_seed(11)
+    pages = rows * 2 + 1
+    q = torch.randn(rows * q_len, hq, dim, generator=g).bfloat16().to(dev)
+    kc = torch.randn(pages, ps, hk, dim, generator=g).bfloat16().to(dev)
+    vc = torch.randn(pages, ps, hk, dim, generator=g).bfloat16().to(dev)
+    tables = torch.zeros(rows, width, dtype=torch.int32)
+    tables[:, :2] = torch.randperm(pages - 1, generator=g)[: rows * 2].reshape(rows, 2).to(torch.int32) + 1
+    tables = tables.to(dev)
+    seq = torch.full((rows,), q_len, dtype=torch.int32, device=dev)
+    cu = torch.arange(0, rows * q_len + 1, q_len, dtype=torch.int32, device=dev)
+    scale = dim ** -0.5
+    ws = torch.zeros(16, dtype=torch.uint8, device=dev)
+    outs = []
+    for hint in (q_len, width * ps):
+        flags = torch.zeros(1, dtype=torch.int32, device=dev)
+        outs.append(mas.attention.trtllm_batch_context_with_kv_cache(
+            q, (kc, vc), ws, tables, seq, q_len, hint, scale, 1.0, rows, cu, None, kv_layout="NHD",
+            error_flags=flags))
+        assert int(flags.item()) == 0
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    want = context_reference_f32(q, kc, vc, tables.cpu(), seq.cpu(), cu.cpu(), scale)
+    _assert_close(outs[0], want)
