@@ -1600,7 +1600,10 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
     // the launch's time per resident workgroup, the rows taken as long as the longest (max_q_len
     // new tokens, kv_max positions): measured on MI355X, 24B heads 4 x 2048 tokens (48%) -4%,
     // 4 x 512 after 2048 cached (110%) -5%, 16 x 1024 (24%) -2%, 8 x 2048 (24%) even; 32 x 512
-    // (22%) +3%; 123B heads 16 x 512 (15%) +4%, 4 x 4096 (8%) +0.7%.
+    // (22%) +3%; 123B heads 16 x 512 (15%) +4%, 4 x 4096 (8%) +0.7%. Only for fewer than
+    // kPlanMinRows rows: a grid of more may be a captured graph's padded layout (17 rows, 1-3 real
+    // ones far shorter than max_q_len), where tile-major order dispatches every row's empty last
+    // tiles before any real work (3 x 100 tokens after 2000 in the 17-row layout: 62 -> 85 us).
     if (cus == 0) {
       if (const int st = device_cu_count(&cus); st != MAS_OK) return st;
     }
@@ -1608,8 +1611,9 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
     const int64_t kv_max = max_kv_len > 0 ? std::min(cap, max_kv_len) : cap;
     // a workgroup's mean reach in positions: the cached ones plus half the new tokens
     const int64_t mean_reach = std::max(kv_max - max_q_len / 2 + tokens_per_wg / 2, tokens_per_wg);
-    a.tile_major = 10.0 * static_cast<double>(kv_max) * static_cast<double>(resident_wgs) >=
-                   3.0 * static_cast<double>(num_rows * gx * gy) * static_cast<double>(mean_reach);
+    a.tile_major = num_rows < kPlanMinRows &&
+                   10.0 * static_cast<double>(kv_max) * static_cast<double>(resident_wgs) >=
+                       3.0 * static_cast<double>(num_rows * gx * gy) * static_cast<double>(mean_reach);
     const dim3 grid = a.tile_major
                           ? dim3(static_cast<uint32_t>(gx), static_cast<uint32_t>(num_rows), static_cast<uint32_t>(gy))
                           : dim3(static_cast<uint32_t>(gx), static_cast<uint32_t>(gy), static_cast<uint32_t>(num_rows));

@@ -130,33 +130,35 @@ def test_context_attention_full_size(mas, dev, name):
 
 
 def _grid_order_tile_major(cus: int, rows: int, q_len: int, kv_hint: int, hq: int, hk: int) -> bool:
-    """The launch's choice between rows in turn and tile-major order for a grid launch (24B-style
-    heads, four wavefronts of 32 tokens per workgroup): the longest tile's time against the
-    launch's time per resident workgroup."""
+    """The launch's choice between rows in turn and tile-major order for a grid launch: fewer than 8
+    rows, and the longest tile's time against the launch's time per resident workgroup."""
     group = hq // hk
     waves, tokens = (8, 64) if group >= 8 else (4, 32)
     gx, gy = hk * -(-group // 4), -(-q_len // tokens)
     mean = max(kv_hint - q_len // 2 + tokens // 2, tokens)
-    return 10 * kv_hint * cus * (8 // waves) >= 3 * rows * gx * gy * mean
+    return rows < 8 and 10 * kv_hint * cus * (8 // waves) >= 3 * rows * gx * gy * mean
 
 
 @pytest.mark.gpu
 def test_context_attention_grid_orders_agree(mas, dev):
-    """16 prompts of 512 tokens: the max_kv_len hint moves the launch between its two grid orders
-    (rows in turn, or every row's longest tiles first). Workgroups compute the same tiles either
-    way, so the outputs are bit-identical, and both match the float32 restatement."""
-    rows, q_len, hq, hk, dim, ps, width = 16, 512, 32, 8, 128, 256, 32
+    """4 prompts of 2048 tokens under a block table 32768 positions wide: the max_kv_len hint moves
+    the launch between its two grid orders (rows in turn, or every row's longest tiles first).
+    Workgroups compute the same tiles either way, so the outputs are bit-identical, and both match
+    the float32 restatement."""
+    rows, q_len, hq, hk, dim, ps, width = 4, 2048, 32, 8, 128, 256, 128
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     if _grid_order_tile_major(cus, rows, q_len, q_len, hq, hk) == _grid_order_tile_major(cus, rows, q_len,
                                                                                           width * ps, hq, hk):
         pytest.skip(f"on {cus} CUs both hints pick the same order")
     g = torch.Generator().manual_seed(11)
-    pages = rows * 2 + 1
+    pages = rows * (q_len // ps) + 1
     q = torch.randn(rows * q_len, hq, dim, generator=g).bfloat16().to(dev)
     kc = torch.randn(pages, ps, hk, dim, generator=g).bfloat16().to(dev)
     vc = torch.randn(pages, ps, hk, dim, generator=g).bfloat16().to(dev)
     tables = torch.zeros(rows, width, dtype=torch.int32)
-    tables[:, :2] = torch.randperm(pages - 1, generator=g)[: rows * 2].reshape(rows, 2).to(torch.int32) + 1
+    per_row = q_len // ps
+    tables[:, :per_row] = (torch.randperm(pages - 1, generator=g)[: rows * per_row].reshape(rows, per_row)
+                           .to(torch.int32) + 1)
     tables = tables.to(dev)
     seq = torch.full((rows,), q_len, dtype=torch.int32, device=dev)
     cu = torch.arange(0, rows * q_len + 1, q_len, dtype=torch.int32, device=dev)
