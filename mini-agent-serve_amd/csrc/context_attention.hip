@@ -16,7 +16,8 @@
 // 32-token tiles of them (more tokens of fewer heads for groups of 1 or 2), so every 64-position
 // key / value tile they stage in LDS serves 128 (256) query rows. Per tile:
 //   S^T = K Q^T on MFMA (v_mfma_f32_32x32x16_bf16; A = 32 key rows read from LDS, B = the
-//   wavefront's 32 query rows, held in registers), causal mask, online softmax per query row, then
+//   wavefront's 32 query rows, held in registers), causal mask, online softmax per query row (its
+//   running max moved only by rises of more than 2^8 in p, so O is seldom rescaled), then
 //   O^T += V^T P^T on MFMA, where P^T is packed to bf16 straight from the S^T accumulators and V^T
 //   is read from the row-major value tile with gfx950's transposing LDS read (ds_read_b64_tr_b16:
 //   in each group of 16 lanes, lane 4a + b receives element b of the 4-element rows that lanes
@@ -34,6 +35,8 @@ constexpr int kTileP = 64;        // key positions per tile
 constexpr int kRowsPerWave = 32;  // query rows (tokens of one head) per wavefront
 constexpr int kMaxCtxSplits = 32;  // split-KV: key-range splits per token tile, at most
 constexpr float kNegInf = -__builtin_huge_valf();
+// The online softmax's lazy reference point: p = 2^(s c - m c) stays below 2^kLazyLog2.
+constexpr float kLazyLog2 = 8.f;
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
@@ -625,7 +628,7 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
     return;
   }
 
-  float m_run = kNegInf, l_run = 0.f;  // token n's running max (raw score units) and sum
+  float m_run = kNegInf, l_run = 0.f;  // token n's running max (raw score units) and this half's sum
   f32x16 acc[DB];                      // O^T: element j of block db holds O[token n][32 db + 8 (j/4) + 4 hf + j%4]
 #pragma unroll
   for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
@@ -798,21 +801,39 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
     }
   };
   // ---- online softmax per query row; scores stay in raw units, the scale enters the exponent
-  // through one fma: p = 2^(s c - m c). P^T is packed to bf16 as the B operands of O^T += V^T P^T:
-  // k-step kk = positions 16 kk .. 16 kk + 15, lane half hf holding 16 kk + 4 hf + e (e < 4) and
-  // 16 kk + 8 + 4 hf + e - 4 (e >= 4), i.e. elements 8 (kk % 2) .. + 7 of s[kk / 2]. Returns the
-  // factor O must be rescaled by.
+  // through one fma: p = 2^(s c - m c). The reference point m is lazy: a row moves it only to a max
+  // more than kLazyLog2 above it (in exponent units), so p stays below 2^kLazyLog2 and O and l are
+  // rescaled (64 multiplies per lane) only when some row of the wavefront moved from a finite m;
+  // otherwise the stale m holds. bf16 P and the fp32 sums carry the same relative precision at any
+  // such magnitude, and O / l does not depend on m. The split partials carry this m with their sums.
+  // A row's 64 scores of a tile sit in lanes n and n + 32 (32 each). Whether any row must move its m
+  // is decided from each lane's own half (max(a, b) c exceeds a bound iff a c or b c does, c > 0), so
+  // the two halves exchange their maxima only on the seldom path that moves some m; each lane keeps
+  // its half's sum in l_run, and the halves are added once, after the last tile.
+  // P^T is packed to bf16 as the B operands of O^T += V^T P^T: k-step kk = positions 16 kk ..
+  // 16 kk + 15, lane half hf holding 16 kk + 4 hf + e (e < 4) and 16 kk + 8 + 4 hf + e - 4 (e >= 4),
+  // i.e. elements 8 (kk % 2) .. + 7 of s[kk / 2].
   auto softmax = [&](f32x16 (&s)[2], bf16x8 (&pbo)[4]) {
-    float mx = kNegInf;
+    float mh = kNegInf;  // this lane's half of the row
 #pragma unroll
     for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[pb][j]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = m_new == kNegInf ? 0.f : m_new;
-    const float mc = m_use * c;
-    const float alpha = __builtin_amdgcn_exp2f(__builtin_fmaf(m_run, c, -mc));
+      for (int j = 0; j < 16; ++j) mh = fmaxf(mh, s[pb][j]);
+    // a row's first finite score (m = -inf) always moves it; -inf against -inf does not
+    const float bound = m_run * c + kLazyLog2;
+    if (__builtin_amdgcn_ballot_w64(mh * c > bound) != 0) {  // wavefront-uniform
+      const float mx = fmaxf(mh, __shfl_xor(mh, 32));        // the row's max, the same in both halves
+      const bool grow = mx * c > bound;
+      // rows that had no finite score have O = 0 and l = 0: their factor is 1
+      const float alpha = grow && m_run != kNegInf ? __builtin_amdgcn_exp2f(__builtin_fmaf(m_run, c, -(mx * c))) : 1.f;
+      if (grow) m_run = mx;
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) acc[db] *= alpha;
+      }
+    }
+    const float mc = (m_run == kNegInf ? 0.f : m_run) * c;
     float sum = 0.f;
 #pragma unroll
     for (int pb = 0; pb < 2; ++pb)
@@ -821,9 +842,7 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
         s[pb][j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[pb][j], c, -mc));
         sum += s[pb][j];
       }
-    sum += __shfl_xor(sum, 32);
-    l_run = l_run * alpha + sum;
-    m_run = m_new;
+    l_run += sum;  // this half's share
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const int o = 8 * (kk & 1);
@@ -831,14 +850,6 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
       const u32x4 packed = {pack_bf16x2(sv[o], sv[o + 1]), pack_bf16x2(sv[o + 2], sv[o + 3]),
                             pack_bf16x2(sv[o + 4], sv[o + 5]), pack_bf16x2(sv[o + 6], sv[o + 7])};
       pbo[kk] = __builtin_bit_cast(bf16x8, packed);
-    }
-    return alpha;
-  };
-  // O rescale, skipped when no row's max moved
-  auto rescale = [&](float alpha) {
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
-#pragma unroll
-      for (int db = 0; db < DB; ++db) acc[db] *= alpha;
     }
   };
   // ---- O^T += V^T P^T: A = V^T[32 dims][16 positions], read transposed from the row-major value
@@ -883,8 +894,7 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
       mask(cur, it * kTileP);
       bf16x8 pbo[4];
       scores(buf ^ 1, nxt);  // the next tile's (stale buffer contents after the last tile: unused)
-      const float alpha = softmax(cur, pbo);
-      rescale(alpha);
+      softmax(cur, pbo);
       pv(buf, pbo);
     }
   };
@@ -899,6 +909,7 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   if (len_bad && tid == 0 && blockIdx.x == 0 && tile_idx == 0) report(a.err, MAS_ERRBIT_POSITION);
 
   if (!wave_live) return;
+  l_run += __shfl_xor(l_run, 32);  // the row's sum: both halves' shares
   const int t = tok + n;
   if (t >= q_len) return;
   if (split_tile) {

@@ -46,7 +46,12 @@ def _run(mas, dev, q, kc, vc, tables, seq, cu, scale, out=None, flags=None, scal
         out_quant_scale=quant)
 
 
-def _check(got, want, min_exact=0.6):
+def _check(got, want, min_exact=0.55):
+    """Within tolerance of the oracle, and at least `min_exact` of the outputs bit-identical. The
+    kernel rounds P to bf16 against a lazy running max (moved only when a row's max rises by more
+    than 2^8 in p), so the largest p of a row is rounded too: 58-73% of the outputs of the cases
+    checked at the default share match the exact-max oracle bit for bit (60-73% with the max moved
+    on every rise)."""
     np.testing.assert_allclose(on.bf16_to_f32(got), on.bf16_to_f32(want), rtol=RTOL, atol=ATOL)
     assert np.mean(got == want) >= min_exact
 
