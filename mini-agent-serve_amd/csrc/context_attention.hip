@@ -126,6 +126,16 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// Raw buffer loads: a resource with no stride and no record limit (num_records 0xffffffff; dword
+// 3 = 0x00020000, the 32-bit data format that untyped buffer loads take on gfx9), and 16 bytes at
+// byte offset voffset (per lane) + soffset (uniform) from its base.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const uint16_t* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, -1, 0x00020000);
+}
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int voffset, int soffset) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, soffset, 0));
+}
+
 // How a tile's key / value rows find their pages (the block-table reads of a tile):
 //   kPagesTile  - pages of at least a tile: the tile lies in one page, one scalar read per tile;
 //   kPagesStep1 - pages of at least a thread-row step (kPosStep positions): each step of a tile lies
@@ -645,11 +655,18 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   const int64_t lane_off = static_cast<int64_t>(prow) * a.entry_stride + kvh * a.head_stride + 8 * dcol;
   struct TileRegs {
     u32x4 k[LOADS], v[LOADS];
-    bool lok[LOADS];
-    bool full;  // every chunk of the tile valid: stores need no zeroing
+    bool lok[LOADS];  // one-page tiles: derived when staged, from the two below
+    bool full;        // every chunk of the tile valid: stores need no zeroing
+    bool page_ok;     // one-page tiles: the page id is inside the cache
+    int base;         // one-page tiles: the first position
   };
   bool page_bad = false;  // a real position's page id outside the cache (reported once, at the end)
   const int last_page = kv_len > 0 ? (kv_len - 1) >> a.log2_page : 0;  // the sequence's last block-table entry
+  // Pages of at least a tile: the tile's first row in its page is the base of a buffer resource
+  // (scalar arithmetic), each lane's row and head-dim chunk a fixed 32-bit byte offset from it (the
+  // host keeps this mode to pages whose in-page offsets fit 31 bits), and step u a scalar offset.
+  const int lane_off_bytes = static_cast<int>(lane_off) * 2;
+  const int step_bytes = static_cast<int>(kPosStep * a.entry_stride) * 2;
   auto issue_tile = [&](TileRegs& tr, int base) {
     if constexpr (kPages == kPagesTile) {
       const int32_t page = bt[base >> a.log2_page];
@@ -658,12 +675,14 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
       const int64_t tile_off = (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
                                static_cast<int64_t>(base & pmask) * a.entry_stride;
       tr.full = ok && base + kTileP <= kv_len;
+      tr.page_ok = ok;
+      tr.base = base;
+      const __amdgpu_buffer_rsrc_t kr = make_rsrc(a.k_cache + tile_off);
+      const __amdgpu_buffer_rsrc_t vr = make_rsrc(a.v_cache + tile_off);
 #pragma unroll
       for (int u = 0; u < LOADS; ++u) {
-        const int64_t off = tile_off + lane_off + static_cast<int64_t>(kPosStep * u) * a.entry_stride;
-        tr.k[u] = load_cached(a.k_cache + off);
-        tr.v[u] = load_cached(a.v_cache + off);
-        tr.lok[u] = ok && base + prow + kPosStep * u < kv_len;
+        tr.k[u] = buffer_load16(kr, lane_off_bytes, step_bytes * u);
+        tr.v[u] = buffer_load16(vr, lane_off_bytes, step_bytes * u);
       }
     } else if constexpr (kPages == kPagesStep1) {
       // Step u starts at a multiple of kPosStep <= page size, so its rows lie in one page at entries
@@ -762,8 +781,9 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
 #pragma unroll
       for (int u = 0; u < LOADS; ++u) {
         const int p = prow + kPosStep * u;
-        const u32x4 kv = tr.lok[u] ? tr.k[u] : u32x4{0u, 0u, 0u, 0u};
-        const u32x4 vv = tr.lok[u] ? tr.v[u] : u32x4{0u, 0u, 0u, 0u};
+        const bool lok = kPages == kPagesTile ? tr.page_ok && tr.base + p < kv_len : tr.lok[u];
+        const u32x4 kv = lok ? tr.k[u] : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 vv = lok ? tr.v[u] : u32x4{0u, 0u, 0u, 0u};
         *reinterpret_cast<u32x4*>(k_lds + p * KROW + 8 * dcol) = kv;
         *reinterpret_cast<u32x4*>(v_lds + p * VROW + 8 * dcol) = vv;
       }
@@ -790,14 +810,14 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   // of the sequence (a wavefront-uniform branch)
   auto mask = [&](f32x16 (&s)[2], int base) {
     if (base + kTileP - 1 > shift + tok || base + kTileP > kv_len) {
-      const int qpos = shift + tok + n;  // this lane's query row position
+      // position kp is masked past min(this lane's query position, kv_len - 1); element j of s[pb]
+      // sits at kp = base + 4 hf + (32 pb + 8 (j / 4) + j % 4), the bracket a constant
+      const int lim = min(shift + tok + n, kv_len - 1) - base - 4 * hf;
 #pragma unroll
       for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int kp = base + 32 * pb + 8 * (j >> 2) + 4 * hf + (j & 3);
-          if (kp > qpos || kp >= kv_len) s[pb][j] = kNegInf;
-        }
+        for (int j = 0; j < 16; ++j)
+          if (32 * pb + 8 * (j >> 2) + (j & 3) > lim) s[pb][j] = kNegInf;
     }
   };
   // ---- online softmax per query row; scores stay in raw units, the scale enters the exponent
@@ -1530,7 +1550,11 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   a.part_ml = kv_splits > 1 ? a.part_o + num_rows * row_tokens * num_q_heads * kv_splits * head_dim : nullptr;
   // Page mode: a tile within one page, a thread-row step within one or two pages, or per lane.
   const int64_t pos_step = 64 * waves / (head_dim / 8);
-  const int mode = page_size >= kTileP     ? kPagesTile
+  // One-page tiles load through buffer resources, with 31-bit byte offsets from the tile's first row.
+  const bool tile_offsets_fit =
+      entry_stride >= 0 && head_stride >= 0 &&
+      ((kTileP - 1) * entry_stride + (num_kv_heads - 1) * head_stride + head_dim) * 2 < (int64_t{1} << 31);
+  const int mode = page_size >= kTileP && tile_offsets_fit ? kPagesTile
                    : page_size >= pos_step ? kPagesStep1
                    : 2 * page_size >= pos_step ? kPagesStep
                                                : kPagesLane;
