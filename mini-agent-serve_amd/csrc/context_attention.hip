@@ -126,15 +126,18 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// Raw buffer loads: a resource with no stride and no record limit (num_records 0xffffffff; dword
-// 3 = 0x00020000, the 32-bit data format that untyped buffer loads take on gfx9), and 16 bytes at
-// byte offset voffset (per lane) + soffset (uniform) from its base.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const uint16_t* base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, -1, 0x00020000);
+// A raw buffer resource: no stride, `bytes` records (a load at a byte offset past them returns
+// zeros), dword 3 = 0x00020000 (the 32-bit data format that untyped buffer loads take on gfx9).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const uint16_t* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, bytes, 0x00020000);
 }
-__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int voffset, int soffset) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, soffset, 0));
+// LDS DMA: lane i of the wavefront writes the 16 bytes at byte offset voffset of resource r to LDS
+// address dst + 16 i (dst wavefront-uniform); zeros for an offset past the resource's records.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint16_t* dst, int voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(dst), 16, voffset, 0, 0, 0);
 }
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt fields at their maxima: not waited on)
+constexpr int kWaitVmcnt0 = 0x0f70;
 
 // How a tile's key / value rows find their pages (the block-table reads of a tile):
 //   kPagesTile  - pages of at least a tile: the tile lies in one page, one scalar read per tile;
@@ -506,11 +509,15 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   constexpr int VROW = D + 16;          // bf16 per LDS value row (+32 B: conflict-free column reads)
   constexpr int CPR = D / 8;            // 16-byte chunks per key / value row
   constexpr int LOADS = kTileP * CPR / kCtxThreads;  // 16-byte chunks per thread per tile, each of K and V
-  // Two tile buffers: with the software pipeline, the next tile's keys are read while this tile's
-  // values are.
-  constexpr int kBufs = 2;
-  __shared__ __align__(16) uint16_t k_lds_all[kBufs][kTileP * KROW];
-  __shared__ __align__(16) uint16_t v_lds_all[kBufs][kTileP * VROW];
+  // Two tile buffers each of keys and values: with the software pipeline, the next tile's keys are
+  // read while this tile's values are. Four separate arrays, so that the compiler's wait insertion
+  // tells a buffer that an LDS DMA load is filling from the ones being read.
+  __shared__ __align__(16) uint16_t k_lds0[kTileP * KROW];
+  __shared__ __align__(16) uint16_t k_lds1[kTileP * KROW];
+  __shared__ __align__(16) uint16_t v_lds0[kTileP * VROW];
+  __shared__ __align__(16) uint16_t v_lds1[kTileP * VROW];
+  const auto klds = [&](int b) { return b ? k_lds1 : k_lds0; };
+  const auto vlds = [&](int b) { return b ? v_lds1 : v_lds0; };
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id_uniform();
   const int n = lane & 31, hf = lane >> 5;  // this lane's query row (token) and lane half
@@ -655,36 +662,72 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   const int64_t lane_off = static_cast<int64_t>(prow) * a.entry_stride + kvh * a.head_stride + 8 * dcol;
   struct TileRegs {
     u32x4 k[LOADS], v[LOADS];
-    bool lok[LOADS];  // one-page tiles: derived when staged, from the two below
-    bool full;        // every chunk of the tile valid: stores need no zeroing
-    bool page_ok;     // one-page tiles: the page id is inside the cache
-    int base;         // one-page tiles: the first position
+    bool lok[LOADS];
+    bool full;  // every chunk of the tile valid: stores need no zeroing
   };
   bool page_bad = false;  // a real position's page id outside the cache (reported once, at the end)
   const int last_page = kv_len > 0 ? (kv_len - 1) >> a.log2_page : 0;  // the sequence's last block-table entry
-  // Pages of at least a tile: the tile's first row in its page is the base of a buffer resource
-  // (scalar arithmetic), each lane's row and head-dim chunk a fixed 32-bit byte offset from it (the
-  // host keeps this mode to pages whose in-page offsets fit 31 bits), and step u a scalar offset.
-  const int lane_off_bytes = static_cast<int>(lane_off) * 2;
-  const int step_bytes = static_cast<int>(kPosStep * a.entry_stride) * 2;
-  auto issue_tile = [&](TileRegs& tr, int base) {
-    if constexpr (kPages == kPagesTile) {
-      const int32_t page = bt[base >> a.log2_page];
-      const bool ok = page >= 0 && page < a.num_pages;
-      page_bad |= !ok;
-      const int64_t tile_off = (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
-                               static_cast<int64_t>(base & pmask) * a.entry_stride;
-      tr.full = ok && base + kTileP <= kv_len;
-      tr.page_ok = ok;
-      tr.base = base;
-      const __amdgpu_buffer_rsrc_t kr = make_rsrc(a.k_cache + tile_off);
-      const __amdgpu_buffer_rsrc_t vr = make_rsrc(a.v_cache + tile_off);
+
+  // ---- Pages of at least a tile (kDirect): the tiles go to LDS by DMA (buffer_load ... lds), with
+  // no registers or stores in between. A wavefront's load instruction fills 64 consecutive 16-byte
+  // slots of an LDS tile buffer, lane i slot i. The buffers keep their row padding (SK / SV slots per
+  // key / value row, the last one or two of them padding), so lane i of instruction ii loads row
+  // (64 ii + i) / S, head-dim chunk (64 ii + i) % S (a padding slot loads the row's last chunk once
+  // more); a tile's instructions are dealt out to the wavefronts in turn. The rows are read through a
+  // buffer resource based at the tile's first row of this kv head, its records ending after the
+  // tile's last position below kv_len (none for a page id outside the cache): the rows past them
+  // arrive as zeros. The host keeps this mode to layouts whose in-page byte offsets fit 31 bits.
+  constexpr bool kDirect = kPages == kPagesTile;
+  constexpr int SK = KROW / 8, SV = VROW / 8;  // 16-byte slots per LDS key / value row
+  constexpr int NK = (SK + kCtxWaves - 1) / kCtxWaves, NV = (SV + kCtxWaves - 1) / kCtxWaves;
+  int koff[NK], voff[NV];  // this wavefront's instructions' byte offsets (per lane)
+  if constexpr (kDirect) {
 #pragma unroll
-      for (int u = 0; u < LOADS; ++u) {
-        tr.k[u] = buffer_load16(kr, lane_off_bytes, step_bytes * u);
-        tr.v[u] = buffer_load16(vr, lane_off_bytes, step_bytes * u);
-      }
-    } else if constexpr (kPages == kPagesStep1) {
+    for (int j = 0; j < NK; ++j) {
+      const int slot = 64 * (wave + kCtxWaves * j) + lane;
+      koff[j] = static_cast<int>((slot / SK) * a.entry_stride) * 2 + 16 * min(slot % SK, CPR - 1);
+    }
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int slot = 64 * (wave + kCtxWaves * j) + lane;
+      voff[j] = static_cast<int>((slot / SV) * a.entry_stride) * 2 + 16 * min(slot % SV, CPR - 1);
+    }
+  }
+  struct TileRsrc {
+    __amdgpu_buffer_rsrc_t k, v;
+  };
+  // The block table through the constant address space: a scalar load (the DMA instructions would
+  // otherwise keep the compiler from proving the table unwritten, and it would load the page id
+  // with a vector load and wait on every load in flight).
+  const auto bt_const = (const __attribute__((address_space(4))) int32_t*)(bt);
+  auto tile_rsrc = [&](int base) {
+    const int32_t page = bt_const[base >> a.log2_page];
+    const bool ok = page >= 0 && page < a.num_pages;
+    page_bad |= !ok;
+    const int64_t off = (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
+                        static_cast<int64_t>(base & pmask) * a.entry_stride + kvh * a.head_stride;
+    const int bytes = ok ? static_cast<int>(min(kTileP, kv_len - base) * a.entry_stride) * 2 : 0;
+    return TileRsrc{make_rsrc(a.k_cache + off, bytes), make_rsrc(a.v_cache + off, bytes)};
+  };
+  // The LDS addresses are formed where the loads issue (the opaque copy of the wavefront's offset
+  // keeps the compiler from hoisting twenty of them out of the tile loop into spilled registers).
+  auto dma_keys = [&](const TileRsrc& t, uint16_t* dst) {
+    int wofs = 512 * wave;
+    asm volatile("" : "+s"(wofs));
+#pragma unroll
+    for (int j = 0; j < NK; ++j)
+      if (wave + kCtxWaves * j < SK) dma16(t.k, dst + wofs + 512 * kCtxWaves * j, koff[j]);
+  };
+  auto dma_values = [&](const TileRsrc& t, uint16_t* dst) {
+    int wofs = 512 * wave;
+    asm volatile("" : "+s"(wofs));
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+      if (wave + kCtxWaves * j < SV) dma16(t.v, dst + wofs + 512 * kCtxWaves * j, voff[j]);
+  };
+
+  auto issue_tile = [&](TileRegs& tr, int base) {
+    if constexpr (kPages == kPagesStep1) {
       // Step u starts at a multiple of kPosStep <= page size, so its rows lie in one page at entries
       // (gp & pmask) + prow: a wave-uniform base per step plus the lane's fixed offset. Rows past
       // kv_len are read from inside that page (the sequence's last page for steps past its end) and
@@ -768,8 +811,8 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   };
   // The tile in `tr` into LDS buffer `buf` (rows past kv_len or on a bad page zeroed).
   auto stage = [&](const TileRegs& tr, int buf) {
-    uint16_t* k_lds = k_lds_all[buf];
-    uint16_t* v_lds = v_lds_all[buf];
+    uint16_t* k_lds = klds(buf);
+    uint16_t* v_lds = vlds(buf);
     if (tr.full) {
 #pragma unroll
       for (int u = 0; u < LOADS; ++u) {
@@ -781,9 +824,8 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
 #pragma unroll
       for (int u = 0; u < LOADS; ++u) {
         const int p = prow + kPosStep * u;
-        const bool lok = kPages == kPagesTile ? tr.page_ok && tr.base + p < kv_len : tr.lok[u];
-        const u32x4 kv = lok ? tr.k[u] : u32x4{0u, 0u, 0u, 0u};
-        const u32x4 vv = lok ? tr.v[u] : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 kv = tr.lok[u] ? tr.k[u] : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 vv = tr.lok[u] ? tr.v[u] : u32x4{0u, 0u, 0u, 0u};
         *reinterpret_cast<u32x4*>(k_lds + p * KROW + 8 * dcol) = kv;
         *reinterpret_cast<u32x4*>(v_lds + p * VROW + 8 * dcol) = vv;
       }
@@ -795,7 +837,7 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   const float c = a.scale_log2;
   // ---- S^T = K Q^T: element j of s[pb] holds S[token n][position base + 32 pb + 8 (j/4) + 4 hf + j%4]
   auto scores = [&](int buf, f32x16 (&s)[2]) {
-    const uint16_t* k_lds = k_lds_all[buf];
+    const uint16_t* k_lds = klds(buf);
 #pragma unroll
     for (int pb = 0; pb < 2; ++pb) {
       s[pb] = f32x16{};
@@ -875,7 +917,7 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   // ---- O^T += V^T P^T: A = V^T[32 dims][16 positions], read transposed from the row-major value
   // tile in the position order of pbo
   auto pv = [&](int buf, const bf16x8 (&pbo)[4]) {
-    const uint16_t* v_lds = v_lds_all[buf];
+    const uint16_t* v_lds = vlds(buf);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
 #pragma unroll
@@ -895,21 +937,42 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   // that ends every read of tile it - 1, which used that buffer). The parity is counted from the
   // workgroup's first tile, so that it is a constant at each call of step even where the first tile
   // is not known at compile time (split ranges): LDS addresses then fold into the instructions.
+  // With LDS DMA (kDirect) the keys run a tile ahead of the values: in step it, key buffer buf ^ 1
+  // holds tile it + 1 and the DMA fills key buffer buf (tile it's keys, read in step it - 1) with
+  // tile it + 2 and value buffer buf ^ 1 (tile it - 1's values) with tile it + 1. One barrier per
+  // step, after this wavefront's DMA of the previous step has landed, covers both: every wavefront's
+  // loads are in LDS, and every read of the buffers refilled next is done.
   f32x16 s_a[2], s_b[2];
   if (it_begin < it_end) {
-    issue_tile(tr, it_begin * kTileP);
-    stage(tr, 0);
-    __syncthreads();
-    if (it_begin + 1 < it_end) issue_tile(tr, (it_begin + 1) * kTileP);
+    if constexpr (kDirect) {
+      const TileRsrc r0 = tile_rsrc(it_begin * kTileP);
+      dma_keys(r0, klds(0));
+      dma_values(r0, vlds(0));
+      if (it_begin + 1 < it_end) dma_keys(tile_rsrc((it_begin + 1) * kTileP), klds(1));
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+      __syncthreads();
+    } else {
+      issue_tile(tr, it_begin * kTileP);
+      stage(tr, 0);
+      __syncthreads();
+      if (it_begin + 1 < it_end) issue_tile(tr, (it_begin + 1) * kTileP);
+    }
     if (wave_live) scores(0, s_a);
   }
   // One tile in buffer `buf`; `cur` holds its scores, `nxt` receives the next tile's. Called with
   // the two score arrays in turn (no copy between them).
   auto step = [&](int it, int buf, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
-    __syncthreads();  // tile it - 1's reads (of buffer buf ^ 1) are done
-    if (it + 1 < it_end) stage(tr, buf ^ 1);
-    __syncthreads();
-    if (it + 2 < it_end) issue_tile(tr, (it + 2) * kTileP);
+    if constexpr (kDirect) {
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+      __syncthreads();
+      if (it + 1 < it_end) dma_values(tile_rsrc((it + 1) * kTileP), vlds(buf ^ 1));
+      if (it + 2 < it_end) dma_keys(tile_rsrc((it + 2) * kTileP), klds(buf));
+    } else {
+      __syncthreads();  // tile it - 1's reads (of buffer buf ^ 1) are done
+      if (it + 1 < it_end) stage(tr, buf ^ 1);
+      __syncthreads();
+      if (it + 2 < it_end) issue_tile(tr, (it + 2) * kTileP);
+    }
     if (wave_live) {
       mask(cur, it * kTileP);
       bf16x8 pbo[4];
@@ -1550,10 +1613,12 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   a.part_ml = kv_splits > 1 ? a.part_o + num_rows * row_tokens * num_q_heads * kv_splits * head_dim : nullptr;
   // Page mode: a tile within one page, a thread-row step within one or two pages, or per lane.
   const int64_t pos_step = 64 * waves / (head_dim / 8);
-  // One-page tiles load through buffer resources, with 31-bit byte offsets from the tile's first row.
+  // One-page tiles load by LDS DMA through buffer resources: 31-bit byte offsets and record counts
+  // from the tile's first row, and rows whose validity a record count can express (a position's
+  // row of one kv head inside its entry).
   const bool tile_offsets_fit =
-      entry_stride >= 0 && head_stride >= 0 &&
-      ((kTileP - 1) * entry_stride + (num_kv_heads - 1) * head_stride + head_dim) * 2 < (int64_t{1} << 31);
+      entry_stride >= head_dim && head_stride >= 0 &&
+      (kTileP * entry_stride + (num_kv_heads - 1) * head_stride + head_dim) * 2 < (int64_t{1} << 31);
   const int mode = page_size >= kTileP && tile_offsets_fit ? kPagesTile
                    : page_size >= pos_step ? kPagesStep1
                    : 2 * page_size >= pos_step ? kPagesStep
