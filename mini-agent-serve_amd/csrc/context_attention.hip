@@ -838,15 +838,28 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   // ---- S^T = K Q^T: element j of s[pb] holds S[token n][position base + 32 pb + 8 (j/4) + 4 hf + j%4]
   auto scores = [&](int buf, f32x16 (&s)[2]) {
     const uint16_t* k_lds = klds(buf);
+    bf16x8 ka[KS][2];
 #pragma unroll
-    for (int pb = 0; pb < 2; ++pb) {
-      s[pb] = f32x16{};
+    for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 ka = *reinterpret_cast<const bf16x8*>(k_lds + (32 * pb + n) * KROW + 16 * ks + 8 * hf);
-        s[pb] = mfma32(ka, qb[ks], s[pb]);
-      }
+      for (int pb = 0; pb < 2; ++pb)
+        ka[ks][pb] = *reinterpret_cast<const bf16x8*>(k_lds + (32 * pb + n) * KROW + 16 * ks + 8 * hf);
+    s[0] = f32x16{};
+    s[1] = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int pb = 0; pb < 2; ++pb) s[pb] = mfma32(ka[ks][pb], qb[ks], s[pb]);
+    // the key reads run four ahead of the MFMAs that take them (the compiler's own order kept two in
+    // flight; eight ahead spills): 4 reads, then (MFMA, read) pairs, then the last 4 MFMAs
+    constexpr int kAhead = 4;
+    __builtin_amdgcn_sched_group_barrier(0x100, kAhead, 0);  // DS reads
+#pragma unroll
+    for (int i = 0; i < 2 * KS - kAhead; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // an MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // a DS read
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, kAhead, 0);
   };
   // ---- causal mask, only on tiles that cross the diagonal of the wavefront's first row or the end
   // of the sequence (a wavefront-uniform branch)
