@@ -520,6 +520,7 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   const auto vlds = [&](int b) { return b ? v_lds1 : v_lds0; };
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id_uniform();
+  __builtin_assume(wave >= 0 && wave < kCtxWaves);  // lets the LDS DMA dealing fold its bounds
   const int n = lane & 31, hf = lane >> 5;  // this lane's query row (token) and lane half
   const int hgroups = (a.group + a.heads_per_wg - 1) / a.heads_per_wg;
   // A planned launch's item. Unsplit plans are the grid launch's workgroups in row order (each row's
