@@ -22,8 +22,10 @@
 //   is read from the row-major value tile with gfx950's transposing LDS read (ds_read_b64_tr_b16:
 //   in each group of 16 lanes, lane 4a + b receives element b of the 4-element rows that lanes
 //   a, a + 4, a + 8, a + 12 point at), two per operand, in the position order the packing implies.
-// Tiles are software-pipelined over two LDS buffers: while tile i is in the softmax, tile i + 1's
-// score MFMAs run and tile i + 2's key and value loads are in flight.
+// Tiles are software-pipelined over two LDS buffers each of keys and values: while tile i is in the
+// softmax, tile i + 1's score MFMAs run. With pages of at least a tile, the tiles go to LDS by DMA,
+// keys a tile ahead of values (tile i + 2's keys and tile i + 1's values in flight), one barrier
+// per tile; smaller pages stage tile i + 2 through registers, two barriers per tile.
 #include <algorithm>
 
 #include "device.h"
