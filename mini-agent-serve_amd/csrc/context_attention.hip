@@ -143,6 +143,8 @@ constexpr int kWaitVmcnt0 = 0x0f70;
 
 // How a tile's key / value rows find their pages (the block-table reads of a tile):
 //   kPagesTile  - pages of at least a tile: the tile lies in one page, one scalar read per tile;
+//   kPagesMulti8 / 16 / 32 - pages of 8, 16 or 32 slots (LDS DMA, as kPagesTile): the tile's pages
+//                 are dealt out to the wavefronts, each page loaded under a buffer resource of its own;
 //   kPagesStep1 - pages of at least a thread-row step (kPosStep positions): each step of a tile lies
 //                 in one page, one scalar read per step, each lane adding its fixed row offset;
 //   kPagesStep  - pages of at least half of a thread-row step: the rows of step u lie in one or two
@@ -152,6 +154,8 @@ constexpr int kWaitVmcnt0 = 0x0f70;
 // vector load issued before them, the next tiles' key / value loads included: they stall the
 // software pipeline, which the scalar reads do not.
 constexpr int kPagesLane = 0, kPagesStep = 1, kPagesTile = 2, kPagesStep1 = 3;
+// kPagesMulti8 + i: pages of 8 << i slots (i < 3)
+constexpr int kPagesMulti8 = 4, kPagesMulti16 = 5, kPagesMulti32 = 6;
 
 // Key tiles per split of a token tile that reaches `ntiles` key tiles: its kv_splits splits share
 // them evenly, at least 4 each (fewer splits then hold them all). From the tile's own reach, not
@@ -680,21 +684,30 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   // buffer resource based at the tile's first row of this kv head, its records ending after the
   // tile's last position below kv_len (none for a page id outside the cache): the rows past them
   // arrive as zeros. The host keeps this mode to layouts whose in-page byte offsets fit 31 bits.
-  constexpr bool kDirect = kPages == kPagesTile;
+  constexpr bool kMulti = kPages >= kPagesMulti8;
+  constexpr bool kDirect = kPages == kPagesTile || kMulti;
   constexpr int SK = KROW / 8, SV = VROW / 8;  // 16-byte slots per LDS key / value row
   constexpr int NK = (SK + kCtxWaves - 1) / kCtxWaves, NV = (SV + kCtxWaves - 1) / kCtxWaves;
-  int koff[NK], voff[NV];  // this wavefront's instructions' byte offsets (per lane)
+  // One-page tiles: instruction ii fills slots 64 ii .. 64 ii + 63 of the buffer, ii = wave + W j for
+  // this wavefront's j, and each lane keeps the byte offset of its row and chunk from the tile's
+  // first row.
+  // kMulti: page q of the tile (PS rows) fills the buffer's slots from q PS S on, in MQ = ceil(PS S /
+  // 64) instructions 64 slots apart (the last one with only the lanes inside the page's region).
+  // Page q is wavefront q % W's, and each lane keeps the byte offset of its row and chunk from the
+  // start of the page for each k < MQ (the same for every page).
+  constexpr int PS = kMulti ? (8 << (kPages - kPagesMulti8)) : kTileP;  // rows per page (kMulti)
+  constexpr int PT = kTileP / PS;                                         // pages per tile
+  constexpr int PPW = (PT + kCtxWaves - 1) / kCtxWaves;                   // pages per wavefront, at most
+  constexpr int MQK = kMulti ? (PS * SK + 63) / 64 : NK, MQV = kMulti ? (PS * SV + 63) / 64 : NV;
+  int koff[MQK], voff[MQV];
   if constexpr (kDirect) {
+    auto place = [&](int s, int S) {
+      return static_cast<int>((s / S) * a.entry_stride) * 2 + 16 * min(s % S, CPR - 1);
+    };
 #pragma unroll
-    for (int j = 0; j < NK; ++j) {
-      const int slot = 64 * (wave + kCtxWaves * j) + lane;
-      koff[j] = static_cast<int>((slot / SK) * a.entry_stride) * 2 + 16 * min(slot % SK, CPR - 1);
-    }
+    for (int j = 0; j < MQK; ++j) koff[j] = place(64 * (kMulti ? j : wave + kCtxWaves * j) + lane, SK);
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      const int slot = 64 * (wave + kCtxWaves * j) + lane;
-      voff[j] = static_cast<int>((slot / SV) * a.entry_stride) * 2 + 16 * min(slot % SV, CPR - 1);
-    }
+    for (int j = 0; j < MQV; ++j) voff[j] = place(64 * (kMulti ? j : wave + kCtxWaves * j) + lane, SV);
   }
   struct TileRsrc {
     __amdgpu_buffer_rsrc_t k, v;
@@ -712,22 +725,59 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
     const int bytes = ok ? static_cast<int>(min(kTileP, kv_len - base) * a.entry_stride) * 2 : 0;
     return TileRsrc{make_rsrc(a.k_cache + off, bytes), make_rsrc(a.v_cache + off, bytes)};
   };
-  // The LDS addresses are formed where the loads issue (the opaque copy of the wavefront's offset
-  // keeps the compiler from hoisting twenty of them out of the tile loop into spilled registers).
-  auto dma_keys = [&](const TileRsrc& t, uint16_t* dst) {
-    int wofs = 512 * wave;
-    asm volatile("" : "+s"(wofs));
-#pragma unroll
-    for (int j = 0; j < NK; ++j)
-      if (wave + kCtxWaves * j < SK) dma16(t.k, dst + wofs + 512 * kCtxWaves * j, koff[j]);
+  // kMulti: the resource of page q of the tile at `base` (pages start at multiples of their size,
+  // and tiles at multiples of 64): based at the page's first row of this kv head, its records ending
+  // after the page's last position below kv_len. A page wholly past kv_len has no records (its
+  // block-table entry, read clamped to the sequence's last one, is not used).
+  auto page_rsrc = [&](const uint16_t* cache, int base, int q) {
+    const int pos = base + q * PS;
+    // (readfirstlane: the clamp is selected as a vector med3, and a resource dword in a vector
+    // register would make the compiler loop over its distinct values)
+    const int rows = __builtin_amdgcn_readfirstlane(max(0, min(kv_len - pos, PS)));
+    const int32_t page = bt_const[min(pos >> a.log2_page, last_page)];
+    const bool ok = page >= 0 && page < a.num_pages;
+    page_bad |= rows > 0 && !ok;
+    const int64_t off = (ok ? static_cast<int64_t>(page) : 0) * a.page_stride + kvh * a.head_stride;
+    return make_rsrc(cache + off, ok ? static_cast<int>(rows * a.entry_stride) * 2 : 0);
   };
-  auto dma_values = [&](const TileRsrc& t, uint16_t* dst) {
-    int wofs = 512 * wave;
-    asm volatile("" : "+s"(wofs));
+  // One tile's keys or values into `dst`, this wavefront's instructions. The LDS addresses are
+  // formed where the loads issue (the opaque copy of the buffer's address keeps the compiler from
+  // hoisting twenty of them out of the tile loop into spilled registers).
+  auto dma_part = [&](bool keys, int base, uint16_t* dst) {
+    const uint16_t* cache = keys ? a.k_cache : a.v_cache;
+    uint16_t* d = dst;
+    asm volatile("" : "+s"(d));
+    if constexpr (kMulti) {
 #pragma unroll
-    for (int j = 0; j < NV; ++j)
-      if (wave + kCtxWaves * j < SV) dma16(t.v, dst + wofs + 512 * kCtxWaves * j, voff[j]);
+      for (int pj = 0; pj < PPW; ++pj) {
+        const int q = wave + kCtxWaves * pj;
+        if (q >= PT) continue;  // wavefront-uniform
+        const __amdgpu_buffer_rsrc_t r = page_rsrc(cache, base, q);
+        const int S = keys ? SK : SV;
+        uint16_t* dq = d + 8 * q * PS * S;
+        constexpr int MQ = MQK > MQV ? MQK : MQV;
+#pragma unroll
+        for (int k = 0; k < MQ; ++k) {
+          if (k >= (keys ? MQK : MQV)) continue;
+          const int nact = min(64, PS * S - 64 * k);  // a constant
+          const int off = keys ? koff[k] : voff[k];
+          if (nact == 64 || lane < nact) dma16(r, dq + 512 * k, off);
+        }
+      }
+    } else {
+      const TileRsrc t = tile_rsrc(base);
+      constexpr int N = NK > NV ? NK : NV;
+#pragma unroll
+      for (int j = 0; j < N; ++j) {
+        if (keys ? j >= NK : j >= NV) continue;
+        const int m = wave + kCtxWaves * j;
+        if (m >= (keys ? SK : SV)) continue;
+        dma16(keys ? t.k : t.v, d + 512 * m, keys ? koff[j] : voff[j]);
+      }
+    }
   };
+  auto dma_keys = [&](int base, uint16_t* dst) { dma_part(true, base, dst); };
+  auto dma_values = [&](int base, uint16_t* dst) { dma_part(false, base, dst); };
 
   auto issue_tile = [&](TileRegs& tr, int base) {
     if constexpr (kPages == kPagesStep1) {
@@ -961,10 +1011,9 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   f32x16 s_a[2], s_b[2];
   if (it_begin < it_end) {
     if constexpr (kDirect) {
-      const TileRsrc r0 = tile_rsrc(it_begin * kTileP);
-      dma_keys(r0, klds(0));
-      dma_values(r0, vlds(0));
-      if (it_begin + 1 < it_end) dma_keys(tile_rsrc((it_begin + 1) * kTileP), klds(1));
+      dma_keys(it_begin * kTileP, klds(0));
+      dma_values(it_begin * kTileP, vlds(0));
+      if (it_begin + 1 < it_end) dma_keys((it_begin + 1) * kTileP, klds(1));
       __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
       __syncthreads();
     } else {
@@ -981,8 +1030,8 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
     if constexpr (kDirect) {
       __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
       __syncthreads();
-      if (it + 1 < it_end) dma_values(tile_rsrc((it + 1) * kTileP), vlds(buf ^ 1));
-      if (it + 2 < it_end) dma_keys(tile_rsrc((it + 2) * kTileP), klds(buf));
+      if (it + 1 < it_end) dma_values((it + 1) * kTileP, vlds(buf ^ 1));
+      if (it + 2 < it_end) dma_keys((it + 2) * kTileP, klds(buf));
     } else {
       __syncthreads();  // tile it - 1's reads (of buffer buf ^ 1) are done
       if (it + 1 < it_end) stage(tr, buf ^ 1);
@@ -1428,6 +1477,12 @@ __global__ __launch_bounds__(kPlanThreads) void context_plan(PlanArgs p) {
 template <int D, int kWaves, int kWork>
 void launch_context_mode(int mode, dim3 grid, dim3 block, hipStream_t stream, const ContextArgs& a) {
   if (mode == kPagesTile) hipLaunchKernelGGL((context_attn<D, kPagesTile, kWaves, kWork>), grid, block, 0, stream, a);
+  else if (mode == kPagesMulti8)
+    hipLaunchKernelGGL((context_attn<D, kPagesMulti8, kWaves, kWork>), grid, block, 0, stream, a);
+  else if (mode == kPagesMulti16)
+    hipLaunchKernelGGL((context_attn<D, kPagesMulti16, kWaves, kWork>), grid, block, 0, stream, a);
+  else if (mode == kPagesMulti32)
+    hipLaunchKernelGGL((context_attn<D, kPagesMulti32, kWaves, kWork>), grid, block, 0, stream, a);
   else if (mode == kPagesStep1)
     hipLaunchKernelGGL((context_attn<D, kPagesStep1, kWaves, kWork>), grid, block, 0, stream, a);
   else if (mode == kPagesStep)
@@ -1635,7 +1690,12 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   const bool tile_offsets_fit =
       entry_stride >= head_dim && head_stride >= 0 &&
       (kTileP * entry_stride + (num_kv_heads - 1) * head_stride + head_dim) * 2 < (int64_t{1} << 31);
-  const int mode = page_size >= kTileP && tile_offsets_fit ? kPagesTile
+  // Pages of 8-32 slots: the same by page (offsets and records from a page's first row).
+  const bool page_offsets_fit = entry_stride >= head_dim && head_stride >= 0 &&
+                                page_size * entry_stride * 2 < (int64_t{1} << 31);
+  const int mode = page_size >= kTileP && tile_offsets_fit                     ? kPagesTile
+                   : page_size >= 8 && page_size < kTileP && page_offsets_fit
+                       ? (page_size == 8 ? kPagesMulti8 : page_size == 16 ? kPagesMulti16 : kPagesMulti32)
                    : page_size >= pos_step ? kPagesStep1
                    : 2 * page_size >= pos_step ? kPagesStep
                                                : kPagesLane;
