@@ -675,15 +675,15 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   bool page_bad = false;  // a real position's page id outside the cache (reported once, at the end)
   const int last_page = kv_len > 0 ? (kv_len - 1) >> a.log2_page : 0;  // the sequence's last block-table entry
 
-  // ---- Pages of at least a tile (kDirect): the tiles go to LDS by DMA (buffer_load ... lds), with
+  // ---- Pages of at least 8 slots (kDirect): the tiles go to LDS by DMA (buffer_load ... lds), with
   // no registers or stores in between. A wavefront's load instruction fills 64 consecutive 16-byte
   // slots of an LDS tile buffer, lane i slot i. The buffers keep their row padding (SK / SV slots per
-  // key / value row, the last one or two of them padding), so lane i of instruction ii loads row
-  // (64 ii + i) / S, head-dim chunk (64 ii + i) % S (a padding slot loads the row's last chunk once
-  // more); a tile's instructions are dealt out to the wavefronts in turn. The rows are read through a
-  // buffer resource based at the tile's first row of this kv head, its records ending after the
-  // tile's last position below kv_len (none for a page id outside the cache): the rows past them
-  // arrive as zeros. The host keeps this mode to layouts whose in-page byte offsets fit 31 bits.
+  // key / value row, the last one or two of them padding), so lane i of an instruction that starts
+  // at a row's first slot loads row i / S, head-dim chunk i % S of the rows from there (a padding
+  // slot loads the row's last chunk once more). The rows are read through a buffer resource based at
+  // the first row of the tile (one-page tiles) or of the page (kMulti) of this kv head, its records
+  // ending after the last position below kv_len (none for a page id outside the cache): the rows past
+  // them arrive as zeros. The host keeps this mode to layouts whose in-page byte offsets fit 31 bits.
   constexpr bool kMulti = kPages >= kPagesMulti8;
   constexpr bool kDirect = kPages == kPagesTile || kMulti;
   constexpr int SK = KROW / 8, SV = VROW / 8;  // 16-byte slots per LDS key / value row
