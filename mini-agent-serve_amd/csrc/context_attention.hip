@@ -145,15 +145,14 @@ constexpr int kWaitVmcnt0 = 0x0f70;
 //   kPagesTile  - pages of at least a tile: the tile lies in one page, one scalar read per tile;
 //   kPagesMulti8 / 16 / 32 - pages of 8, 16 or 32 slots (LDS DMA, as kPagesTile): the tile's pages
 //                 are dealt out to the wavefronts, each page loaded under a buffer resource of its own;
-//   kPagesStep1 - pages of at least a thread-row step (kPosStep positions): each step of a tile lies
-//                 in one page, one scalar read per step, each lane adding its fixed row offset;
-//   kPagesStep  - pages of at least half of a thread-row step: the rows of step u lie in one or two
-//                 pages, read with scalar loads, each lane picking its own;
-//   kPagesLane  - smaller pages: each lane reads the page of each of its rows (vector loads).
+//   kPagesLane  - pages of 1-4 slots, and layouts whose in-page byte offsets do not fit the DMA
+//                 modes' 31 bits: each lane reads the page of each of its rows (vector loads) into
+//                 registers, staged into LDS a tile ahead (two barriers per tile).
 // Vector loads of block-table entries make the compiler wait for them, and such waits cover every
-// vector load issued before them, the next tiles' key / value loads included: they stall the
-// software pipeline, which the scalar reads do not.
-constexpr int kPagesLane = 0, kPagesStep = 1, kPagesTile = 2, kPagesStep1 = 3;
+// vector load issued before them, the next tiles' key / value loads included: the DMA modes read
+// them as scalars. (Modes for pages of at least a thread-row step, staged through registers with
+// scalar page reads, served pages of 8-32 slots before the DMA modes.)
+constexpr int kPagesLane = 0, kPagesTile = 2;
 // kPagesMulti8 + i: pages of 8 << i slots (i < 3)
 constexpr int kPagesMulti8 = 4, kPagesMulti16 = 5, kPagesMulti32 = 6;
 
@@ -659,14 +658,11 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
 
   const int32_t* bt = a.block_tables + row * a.bt_stride;
   const int pmask = (1 << a.log2_page) - 1;
-  // Thread's chunks of a tile: chunk c = tid + T u (T threads) -> position tid / CPR + (T / CPR) u, head-dim
-  // chunk tid % CPR (the same for every u). Rows past kv_len or on a page id outside the cache load
-  // row 0 of page 0 and are zeroed when stored; the flags are kept so that the loads themselves are
-  // not waited on here. With pages of at least a tile, a tile lies in one page: one (wave-uniform)
-  // block-table read per tile and precomputed per-thread offsets.
+  // kPagesLane, a thread's chunks of a tile: chunk c = tid + T u (T threads) -> position tid / CPR +
+  // (T / CPR) u, head-dim chunk tid % CPR (the same for every u). The rows' validity flags are kept
+  // so that the loads themselves are not waited on before the stores.
   constexpr int kPosStep = kCtxThreads / CPR;
   const int dcol = tid % CPR, prow = tid / CPR;
-  const int64_t lane_off = static_cast<int64_t>(prow) * a.entry_stride + kvh * a.head_stride + 8 * dcol;
   struct TileRegs {
     u32x4 k[LOADS], v[LOADS];
     bool lok[LOADS];
@@ -779,87 +775,22 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void context_attn(ContextA
   auto dma_keys = [&](int base, uint16_t* dst) { dma_part(true, base, dst); };
   auto dma_values = [&](int base, uint16_t* dst) { dma_part(false, base, dst); };
 
+  // kPagesLane: each lane reads the page of each of its rows; rows past kv_len load the sequence's
+  // last row and are zeroed when staged, as are rows on a page id outside the cache (page 0 read).
   auto issue_tile = [&](TileRegs& tr, int base) {
-    if constexpr (kPages == kPagesStep1) {
-      // Step u starts at a multiple of kPosStep <= page size, so its rows lie in one page at entries
-      // (gp & pmask) + prow: a wave-uniform base per step plus the lane's fixed offset. Rows past
-      // kv_len are read from inside that page (the sequence's last page for steps past its end) and
-      // zeroed when staged.
-      bool all_ok = true;
+    tr.full = false;
 #pragma unroll
-      for (int u = 0; u < LOADS; ++u) {
-        const int gp = base + kPosStep * u;  // the step's first position (wave-uniform)
-        const int32_t page = bt[min(gp >> a.log2_page, last_page)];
-        const bool ok = page >= 0 && page < a.num_pages;
-        page_bad |= !ok && gp < kv_len;
-        all_ok = all_ok && ok;
-        const int64_t off = (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
-                            static_cast<int64_t>(gp & pmask) * a.entry_stride + lane_off;
-        tr.k[u] = load_cached(a.k_cache + off);
-        tr.v[u] = load_cached(a.v_cache + off);
-        tr.lok[u] = ok && gp + prow < kv_len;
-      }
-      tr.full = all_ok && base + kTileP <= kv_len;
-    } else if constexpr (kPages == kPagesStep) {
-      const int sub = prow >> a.log2_page;  // 0 or 1: which of the step's pages holds this lane's row
-      if (base + kTileP <= kv_len) {
-        // A full tile: every row is real, so the lane's row offset in its page is fixed (the step
-        // starts a page when it spans two) and only the page bases change.
-        bool all_ok = true;
-#pragma unroll
-        for (int u = 0; u < LOADS; ++u) {
-          const int gp = base + kPosStep * u;  // the step's first position (wave-uniform)
-          const int i0 = gp >> a.log2_page;
-          const int32_t page0 = bt[i0];
-          const int32_t page1 = bt[min(i0 + 1, last_page)];
-          const bool ok0 = page0 >= 0 && page0 < a.num_pages, ok1 = page1 >= 0 && page1 < a.num_pages;
-          const int32_t page = sub ? page1 : page0;
-          const bool ok = sub ? ok1 : ok0;
-          all_ok = all_ok && ok0 && (kPosStep <= (1 << a.log2_page) || ok1);
-          page_bad |= !ok;
-          const int64_t off = (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
-                              static_cast<int64_t>((gp + prow) & pmask) * a.entry_stride + kvh * a.head_stride +
-                              8 * dcol;
-          tr.k[u] = load_cached(a.k_cache + off);
-          tr.v[u] = load_cached(a.v_cache + off);
-          tr.lok[u] = ok;
-        }
-        tr.full = all_ok;
-      } else {
-        tr.full = false;
-#pragma unroll
-        for (int u = 0; u < LOADS; ++u) {
-          const int gp = base + kPosStep * u;
-          const int i0 = min(gp >> a.log2_page, last_page);
-          const int32_t page0 = bt[i0];
-          const int32_t page1 = bt[min(i0 + 1, last_page)];
-          const int32_t page = sub ? page1 : page0;
-          const int p = gp + prow;
-          const int pc = p < kv_len ? p : kv_len - 1;
-          const bool ok = page >= 0 && page < a.num_pages;
-          page_bad |= !ok && p < kv_len;
-          const int64_t off = (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
-                              static_cast<int64_t>(pc & pmask) * a.entry_stride + kvh * a.head_stride + 8 * dcol;
-          tr.k[u] = load_cached(a.k_cache + off);
-          tr.v[u] = load_cached(a.v_cache + off);
-          tr.lok[u] = ok && p < kv_len;
-        }
-      }
-    } else {
-      tr.full = false;
-#pragma unroll
-      for (int u = 0; u < LOADS; ++u) {
-        const int p = base + prow + kPosStep * u;
-        const int pc = p < kv_len ? p : kv_len - 1;
-        const int32_t page = bt[pc >> a.log2_page];
-        const bool ok = page >= 0 && page < a.num_pages;
-        page_bad |= !ok && p < kv_len;
-        const int64_t off = (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
-                            static_cast<int64_t>(pc & pmask) * a.entry_stride + kvh * a.head_stride + 8 * dcol;
-        tr.k[u] = load_cached(a.k_cache + off);
-        tr.v[u] = load_cached(a.v_cache + off);
-        tr.lok[u] = ok && p < kv_len;
-      }
+    for (int u = 0; u < LOADS; ++u) {
+      const int p = base + prow + kPosStep * u;
+      const int pc = p < kv_len ? p : kv_len - 1;
+      const int32_t page = bt[pc >> a.log2_page];
+      const bool ok = page >= 0 && page < a.num_pages;
+      page_bad |= !ok && p < kv_len;
+      const int64_t off = (ok ? static_cast<int64_t>(page) : 0) * a.page_stride +
+                          static_cast<int64_t>(pc & pmask) * a.entry_stride + kvh * a.head_stride + 8 * dcol;
+      tr.k[u] = load_cached(a.k_cache + off);
+      tr.v[u] = load_cached(a.v_cache + off);
+      tr.lok[u] = ok && p < kv_len;
     }
   };
   // The tile in `tr` into LDS buffer `buf` (rows past kv_len or on a bad page zeroed).
@@ -1483,10 +1414,6 @@ void launch_context_mode(int mode, dim3 grid, dim3 block, hipStream_t stream, co
     hipLaunchKernelGGL((context_attn<D, kPagesMulti16, kWaves, kWork>), grid, block, 0, stream, a);
   else if (mode == kPagesMulti32)
     hipLaunchKernelGGL((context_attn<D, kPagesMulti32, kWaves, kWork>), grid, block, 0, stream, a);
-  else if (mode == kPagesStep1)
-    hipLaunchKernelGGL((context_attn<D, kPagesStep1, kWaves, kWork>), grid, block, 0, stream, a);
-  else if (mode == kPagesStep)
-    hipLaunchKernelGGL((context_attn<D, kPagesStep, kWaves, kWork>), grid, block, 0, stream, a);
   else hipLaunchKernelGGL((context_attn<D, kPagesLane, kWaves, kWork>), grid, block, 0, stream, a);
 }
 
@@ -1682,8 +1609,7 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   a.split_from = static_cast<int>(split_from);
   a.part_o = static_cast<float*>(workspace);
   a.part_ml = kv_splits > 1 ? a.part_o + num_rows * row_tokens * num_q_heads * kv_splits * head_dim : nullptr;
-  // Page mode: a tile within one page, a thread-row step within one or two pages, or per lane.
-  const int64_t pos_step = 64 * waves / (head_dim / 8);
+  // Page mode: LDS DMA by tile or by page, or per-lane reads staged through registers.
   // One-page tiles load by LDS DMA through buffer resources: 31-bit byte offsets and record counts
   // from the tile's first row, and rows whose validity a record count can express (a position's
   // row of one kv head inside its entry).
@@ -1696,9 +1622,7 @@ extern "C" int mas_paged_context_attention_bf16(void* out, int64_t out_stride, i
   const int mode = page_size >= kTileP && tile_offsets_fit                     ? kPagesTile
                    : page_size >= 8 && page_size < kTileP && page_offsets_fit
                        ? (page_size == 8 ? kPagesMulti8 : page_size == 16 ? kPagesMulti16 : kPagesMulti32)
-                   : page_size >= pos_step ? kPagesStep1
-                   : 2 * page_size >= pos_step ? kPagesStep
-                                               : kPagesLane;
+                                                                                 : kPagesLane;
   const dim3 block(static_cast<uint32_t>(64 * waves));
   if (planned && self_plan) {
     // every workgroup lays the plan out itself (no planner launch) and writes what the merge reads:

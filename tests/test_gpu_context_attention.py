@@ -68,9 +68,9 @@ CASES = [
     ([20, 0, 7], [30, 10, 7], 8, 2, 128, 64),      # a row with no new tokens between two others
     ([45, 19], [80, 19], 16, 2, 64, 16),           # 8 per kv head (eight-wavefront groups), head_dim 64, small pages
     ([70, 33], [90, 33], 24, 2, 128, 32),          # 12 per kv head, pages smaller than a tile
-    ([50, 23], [75, 23], 32, 8, 128, 8),           # a thread-row step over two pages (four wavefronts)
-    ([60, 31], [99, 40], 96, 8, 128, 16),          # two pages per step, eight wavefronts (123B group)
-    ([41], [77], 8, 4, 64, 16),                    # two pages per step, head_dim 64
+    ([50, 23], [75, 23], 32, 8, 128, 8),           # pages of 8 slots: eight pages per tile by LDS DMA
+    ([60, 31], [99, 40], 96, 8, 128, 16),          # 16-slot pages, eight wavefronts (123B group)
+    ([41], [77], 8, 4, 64, 16),                    # 16-slot pages, head_dim 64
     ([90, 17], [150, 17], 16, 8, 64, 64),          # head_dim 64 on pages of one tile
     ([70], [200], 32, 8, 64, 128),                 # head_dim 64 on pages of two tiles
 ]
@@ -117,7 +117,7 @@ def test_context_attention_strided_views_and_bmm2_scale(mas, dev):
     assert torch.all(out_base[:, 0] == 5.0) and torch.all(out_base[:, hq + 1] == 5.0)
 
 
-@pytest.mark.parametrize("ps", [8, 16, 32])   # head_dim 64, four wavefronts (32-row steps): per-lane, two-page and one-page steps
+@pytest.mark.parametrize("ps", [8, 16, 32])   # head_dim 64, four wavefronts: each page by LDS DMA, 8, 4 or 2 per tile
 def test_context_attention_error_paths(mas, dev, ps):
     q_lens, kv_lens, hq, hk, dim = [20, 10], [40, 10], 8, 2, 64
     q, kc, vc, tables, _, cu = _case(8, q_lens, kv_lens, hq, hk, dim, ps)
@@ -347,7 +347,8 @@ def test_context_attention_split_kv_fp8_output(mas, dev, dim, hq, hk):
 
 def _random_config(seed):
     """A seeded mix: 1-3 rows of 1-96 new tokens after 0-2900 cached positions (some rows without
-    new tokens), group sizes 1-12, head_dim 64 / 128, pages of 8-256 slots, with and without a
+    new tokens), group sizes 1-12, head_dim 64 / 128, pages of 4-256 slots (every block-table read
+    mode: per lane, LDS DMA by page at 8 / 16 / 32 slots, and by tile), with and without a
     split-KV workspace and max_kv_len, block tables as wide as the rows or 4-32 times wider."""
     rng = np.random.default_rng(seed)
     rows = int(rng.integers(1, 4))
@@ -356,14 +357,14 @@ def _random_config(seed):
     hk = int(rng.choice([1, 2, 8]))
     group = int(rng.choice([1, 2, 3, 4, 8, 12]))
     dim = int(rng.choice([64, 128]))
-    ps = int(rng.choice([8, 16, 64, 256]))
+    ps = int(rng.choice([4, 8, 16, 32, 64, 256]))
     ws = int(rng.choice([16, SPLIT_WS]))
     max_kv = int(rng.choice([0, max(kv_lens)]))
     widen = int(rng.choice([1, 1, 4, 32]))  # a block table 4 or 32 times wider than the rows need
     return q_lens, kv_lens, hk * group, hk, dim, ps, ws, max_kv, widen
 
 
-@pytest.mark.parametrize("seed", range(40))
+@pytest.mark.parametrize("seed", range(64))
 def test_context_attention_random_configs(mas, dev, seed):
     q_lens, kv_lens, hq, hk, dim, ps, ws, max_kv, widen = _random_config(seed)
     q, kc, vc, tables, seq, cu = _case(100 + seed, q_lens, kv_lens, hq, hk, dim, ps)
