@@ -67,7 +67,7 @@ _SILU_SOURCES = {"csrc/silu_and_mul.hip": "23b0260df03f552c5aeb3be5992d159ad4873
                  "csrc/device.h": "4a649fbd27cb9b4a8503ee1b497b4df962d5650e"}
 _NORM_SOURCES = {"csrc/rmsnorm.hip": "089cb088624451ba8a83f3bc292864153fe93b0d",
                  "csrc/device.h": "4a649fbd27cb9b4a8503ee1b497b4df962d5650e"}
-_DECODE_ATTN_SOURCES = {"csrc/attention.hip": "fedddcdb2d8be7c237ff8a5857fcbfc369dc1031",
+_DECODE_ATTN_SOURCES = {"csrc/attention.hip": "dc9407d13c4dacbefa466e7aeb4a548403f5d5f6",
                         "csrc/device.h": "4a649fbd27cb9b4a8503ee1b497b4df962d5650e"}
 # HBM bytes per launch of a workload's dominant kernel: two rocprofv3 counter passes (FETCH_SIZE,
 # then WRITE_SIZE) over `bench.py --pmc-probe`, each calibrated by the same counter on a 256 MiB
@@ -82,10 +82,10 @@ MEASURED_TRAFFIC = {
     ("prefill8192_24b", "silu_and_mul"): {
         "bytes": 1_610_475_810, "profile": "profiles/silu_and_mul_prefill_hbm_traffic.md", "sources": _SILU_SOURCES},
     ("decode_attn_64x8192_24b", "paged_decode_attention"): {
-        "bytes": 1_115_053_768, "profile": "profiles/decode_attention_64x8192_kernel_trace.md",
+        "bytes": 1_115_079_915, "profile": "profiles/decode_attention_64x8192_kernel_trace.md",
         "sources": _DECODE_ATTN_SOURCES},
     ("decode_attn_64x8192_123b", "paged_decode_attention"): {
-        "bytes": 1_188_519_530, "profile": "profiles/decode_attention_64x8192_kernel_trace.md",
+        "bytes": 1_188_499_821, "profile": "profiles/decode_attention_64x8192_kernel_trace.md",
         "sources": _DECODE_ATTN_SOURCES},
 }
 # Average per-dispatch duration (µs) of a workload's dominant kernel in a committed kernel trace of
@@ -101,10 +101,10 @@ TRACED_LAUNCH_US = {
     ("prefill8192_24b", "silu_and_mul"): {
         "us": 234.195, "profile": "profiles/layer_prefill8192_kernel_trace.md", "sources": _SILU_SOURCES},
     ("decode_attn_64x8192_24b", "paged_decode_attention"): {     # split + combine
-        "us": 206.838 + 7.119, "profile": "profiles/decode_attention_64x8192_kernel_trace.md",
+        "us": 203.167 + 7.818, "profile": "profiles/decode_attention_64x8192_kernel_trace.md",
         "sources": _DECODE_ATTN_SOURCES},
     ("decode_attn_64x8192_123b", "paged_decode_attention"): {
-        "us": 226.885 + 13.941, "profile": "profiles/decode_attention_64x8192_kernel_trace.md",
+        "us": 222.873 + 15.600, "profile": "profiles/decode_attention_64x8192_kernel_trace.md",
         "sources": _DECODE_ATTN_SOURCES},
 }
 
